@@ -1,0 +1,218 @@
+"""Benchmark of the streaming semi-CRF scan on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg3] [--cpu-sample T] [--no-cpu]
+
+A step is one forward + backward (log semiring) over the whole synthetic
+workload of BASELINE.json config 3 by default: B=1, T=1,000,000, C=24, K=300,
+emissions N(0,1) cumsum'd along T, transition N(0,0.1), duration_bias[k,c] =
+-0.01k + N(0,0.05) for k >= 1 (row 0 = 0), seed 20261203, generated on the host
+and resident in HBM before timing.  Prints one JSON line; see DESIGN.md for the
+roofline model.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "torch-semimarkov_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import torch  # noqa: E402
+
+# FP32 VALU lane-op and transcendental peaks of one MI355X
+V_PEAK = 78.6e12
+T_PEAK = 9.83e12
+# algorithmic ops per cell (b, t, k, c_dst, c_src) of the direct recursion
+OPS = {"fwd_log": (5, 1), "bwd_log": (14, 3), "fwdbwd_log": (19, 4), "max": (3, 0)}
+
+
+def roofline_cells_per_s(kind):
+    nv, nt = OPS[kind]
+    return 1.0 / (nv / V_PEAK + nt / T_PEAK)
+
+
+def valu_equiv_ops_per_cell(kind):
+    nv, nt = OPS[kind]
+    return nv + nt * (V_PEAK / T_PEAK)
+
+
+CONFIGS = {
+    "cfg2": dict(B=32, T=10_000, C=8, K=1, seed=20261202),
+    "cfg3": dict(B=1, T=1_000_000, C=24, K=300, seed=20261203),
+    "cfg5": dict(B=8, T=50_000, C=128, K=500, seed=20261205),
+}
+
+
+def make_inputs(name):
+    cfg = CONFIGS[name]
+    B, T, C, K = cfg["B"], cfg["T"], cfg["C"], cfg["K"]
+    g = torch.Generator().manual_seed(cfg["seed"])
+    em = torch.randn(B, T, C, generator=g)
+    if name == "cfg5":
+        tr = 0.05 * torch.randn(C, C, generator=g)
+        k = torch.arange(1, K, dtype=torch.float64)
+        sigma, mu = 0.5, math.log(150.0) + 0.25
+        shape = -torch.log(k * sigma * math.sqrt(2 * math.pi)) - (torch.log(k) - mu) ** 2 / (2 * sigma ** 2)
+        db = torch.zeros(K, C)
+        db[1:] = shape.float().unsqueeze(1) + 0.05 * torch.randn(K - 1, C, generator=g)
+    elif name == "cfg2":
+        tr = 0.1 * torch.randn(C, C, generator=g)
+        db = 0.1 * torch.randn(1, C, generator=g)
+    else:
+        tr = 0.1 * torch.randn(C, C, generator=g)
+        db = torch.zeros(K, C)
+        db[1:] = -0.01 * torch.arange(1, K, dtype=torch.float32).unsqueeze(1) + 0.05 * torch.randn(K - 1, C, generator=g)
+    cum = torch.zeros(B, T + 1, C)
+    cum[:, 1:] = torch.cumsum(em, dim=1)
+    L = torch.full((B,), T, dtype=torch.long)
+    return cfg, cum, tr, db, L
+
+
+def cpu_baseline(name, cum, tr, db, K, t_sample):
+    """The oracle (fp32 PyTorch-CPU restatement of the reference streaming path)
+    on the first t_sample positions of the same workload, forward + backward."""
+    from oracle import streaming_ref as R
+
+    threads = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
+    B = cum.shape[0]
+    c = cum[:, : t_sample + 1].contiguous()
+    L = torch.full((B,), t_sample, dtype=torch.long)
+    t0 = time.perf_counter()
+    part, ck, S = R.forward(c, tr, db, L, K, "log")
+    R.backward(c, tr, db, L, K, part, ck, S, "log")
+    dt = time.perf_counter() - t0
+    C = cum.shape[2]
+    cells = B * t_sample * K * C * C
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    model = ln.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        model = platform.processor()
+    return {
+        "value": cells / dt,
+        "unit": "cells/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{name} inputs truncated to T={t_sample} (B={B}, C={C}, K={K}), oracle fp32 forward+backward "
+                  f"once, {dt:.1f} s on {model or 'host CPU'}",
+        "seconds": dt,
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS))
+    ap.add_argument("--cpu-sample", type=int, default=2000)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch_semimarkov_amd as tsa
+    from torch_semimarkov_amd import _native as N
+
+    dev = torch.device("cuda", 0)
+    cfg, cum_h, tr_h, db_h, L_h = make_inputs(args.config)
+    B, T, C, K = cfg["B"], cfg["T"], cfg["C"], cfg["K"]
+    cum = cum_h.to(dev).requires_grad_(True)
+    tr = tr_h.to(dev).requires_grad_(True)
+    db = db_h.to(dev).requires_grad_(True)
+    L = L_h.to(dev)
+    plan = N.plan_info(B, T, C, K)
+
+    ev = []
+
+    def step(record):
+        cum.grad = tr.grad = db.grad = None
+        if record:
+            e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+            e0.record()
+        part = tsa.semi_crf_streaming_forward(cum, tr, db, L, K)
+        if record:
+            e1.record()
+        part.sum().backward()
+        if record:
+            e2.record()
+            ev.append((e0, e1, e2))
+        return part
+
+    for _ in range(args.warmup):
+        step(False)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        part = step(True)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    ms_step = dt * 1e3 / args.steps
+    fwd_ms = statistics.mean(a.elapsed_time(b) for a, b, _ in ev)
+    bwd_ms = statistics.mean(b.elapsed_time(c) for _, b, c in ev)
+
+    cells = B * T * K * C * C
+    value = cells / (ms_step / 1e3)
+    # dominant op: the one with the larger share of the step
+    dom_kind, dom_ms, dom_name = (("bwd_log", bwd_ms, "backward (beta scan + fixup + marginals + finalize)")
+                                  if bwd_ms >= fwd_ms else ("fwd_log", fwd_ms, "forward (alpha scan + fixup)"))
+    achieved = cells * valu_equiv_ops_per_cell(dom_kind) / (dom_ms / 1e3) / 1e12
+    peak = V_PEAK / 1e12
+    out = {
+        "metric": "fwd+bwd scan cells/s (B*T*K*C^2), 1 GPU",
+        "value": value,
+        "unit": "cells/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": f"{args.config}: streaming semi-CRF fwd+bwd, log semiring",
+            "B": B, "T": T, "C": C, "K": K, "seed": cfg["seed"],
+        },
+        "roofline": {
+            "bound": "valu",
+            "kernel": dom_name,
+            "achieved": achieved,
+            "peak": peak,
+            "unit": "TFLOP/s",
+            "frac": achieved / peak,
+            "traffic": None,
+            "note": "VALU-equivalent lane-ops of the direct recursion (nominal; the kernels execute the "
+                    "exact label factorisation, ~K*C^2/(K*C+C^2) times less work)",
+        },
+        "nominal_roofline_frac_fwdbwd": value / roofline_cells_per_s("fwdbwd_log"),
+        "fwd_ms": fwd_ms,
+        "bwd_ms": bwd_ms,
+        "plan": plan,
+        "logZ": float(part.detach()[0]),
+    }
+    if not args.no_cpu and args.cpu_sample > 0:
+        out["cpu_baseline"] = cpu_baseline(args.config, cum_h, tr_h, db_h, K, min(args.cpu_sample, T))
+        out["speedup_vs_cpu"] = value / out["cpu_baseline"]["value"]
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

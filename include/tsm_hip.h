@@ -1,0 +1,135 @@
+/*
+ * tsm_hip.h -- C ABI of libtsm_hip.so, the MI355X (gfx950) streaming
+ * semi-Markov CRF scan.
+ *
+ * All pointers are device pointers (HIP) unless stated otherwise; all arrays
+ * are dense row-major fp32 / int64 / fp64 as documented.  No entry point
+ * allocates memory: callers pass a workspace of at least the size reported by
+ * the matching *_workspace() query.  Work is enqueued on `stream` (a
+ * hipStream_t, may be NULL for the default stream) and is asynchronous.
+ * Every function returns 0 on success or a TSM_ERR_* code; the message of the
+ * last failure on the calling thread is available from tsm_last_error().
+ *
+ * Conventions (reference: biobenkj/torch-semimarkov README.md:96-125,
+ * src/torch_semimarkov/streaming/pytorch_reference.py:86-111):
+ *   cum_scores      (B, T+1, C)  cumulative projected scores, row 0 = 0
+ *   transition      (C, C)       transition[c_src][c_dst]
+ *   duration_bias   (K, C)       K = max_duration; durations 1..K-1 use row
+ *                                min(k, K-1); K = 1 uses duration 1, row 0
+ *   lengths         (B,) int64   0 <= lengths[b] <= T (clamped on device)
+ *   proj_start/end  (B, T, C) or NULL   boundary scores at segment start / end
+ *   semiring        TSM_SEMIRING_LOG (logsumexp) or TSM_SEMIRING_MAX
+ */
+#ifndef TSM_HIP_H
+#define TSM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TSM_OK 0
+#define TSM_ERR_INVALID 1     /* bad argument (shape, size, null pointer) */
+#define TSM_ERR_UNSUPPORTED 2 /* valid but not implemented on this path */
+#define TSM_ERR_HIP 3         /* HIP runtime error */
+#define TSM_ERR_WORKSPACE 4   /* workspace smaller than required */
+
+#define TSM_SEMIRING_LOG 0
+#define TSM_SEMIRING_MAX 1
+
+/* Library version (major*10000 + minor*100 + patch). */
+int tsm_version(void);
+
+/* Message of the last error on the calling thread ("" if none).  Host pointer. */
+const char* tsm_last_error(void);
+
+/*
+ * Launch plan for a problem shape, for diagnostics and tests.  Fills up to
+ * `n` int64 host values: J, NT, RS, P, Lc, W, global_rings, scan_lds, NB, TB,
+ * CB, NCB, JM, NTM, marg_lds, Kmax, n_cu.
+ */
+int tsm_plan_info(int64_t B, int64_t T, int64_t C, int64_t K, int has_proj_start, int has_proj_end,
+                  int64_t* out, int n);
+
+/* ---------------------------------------------------------------------------
+ * Forward: log partition (semiring LOG) or Viterbi score of the factorised,
+ * normalised recursion (semiring MAX), per sequence.
+ * Replaces the reference's forward launchers:
+ *   streaming/triton_forward.py:554-714  launch_streaming_triton_kernel
+ *   streaming/pytorch_reference.py:116-273 semi_crf_streaming_forward_pytorch
+ * Outputs:
+ *   partition       (B,)        fp32, natural log units
+ *   log2_partition  (B,)        fp64, base-2 units (NULL allowed); the backward needs it
+ *   alpha_hat       (B, T+1, C) fp32 normalised alpha (base 2) or NULL
+ *   alpha_level     (B, T+1)    fp64 per-position level (base 2) or NULL
+ *   alpha = (alpha_hat + alpha_level) * ln 2.  Pass both non-NULL to keep the
+ *   state a later tsm_backward() call needs; pass both NULL for inference.
+ *   recomputed      (B,) int32  chunks recomputed by the verifier, or NULL
+ * ------------------------------------------------------------------------- */
+int tsm_forward_workspace(int64_t B, int64_t T, int64_t C, int64_t K, int semiring, int has_proj_start,
+                          int has_proj_end, size_t* bytes);
+int tsm_forward(const float* cum_scores, const float* transition, const float* duration_bias,
+                const int64_t* lengths, const float* proj_start, const float* proj_end, int64_t B, int64_t T,
+                int64_t C, int64_t K, int semiring, float* partition, double* log2_partition,
+                float* alpha_hat, double* alpha_level, int32_t* recomputed, void* workspace,
+                size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Backward: gradients of sum_b grad_output[b] * partition[b].
+ * Replaces:
+ *   streaming/triton_backward.py:556-790  launch_streaming_triton_backward
+ *   streaming/pytorch_reference.py:276-525 semi_crf_streaming_backward_pytorch
+ *   streaming/autograd.py:134-150          grad_output scaling / einsum reduction
+ * Inputs alpha_hat / alpha_level / log2_partition come from tsm_forward with
+ * the same semiring (MAX gives the reference's "soft max-marginals").
+ * Outputs (all fully written):
+ *   grad_cum        (B, T+1, C)  already scaled by grad_output[b]
+ *   grad_transition (C, C)       sum_b grad_output[b] * d/dtransition
+ *   grad_duration_bias (K, C)
+ *   grad_proj_start, grad_proj_end (B, T, C) or NULL
+ * ------------------------------------------------------------------------- */
+int tsm_backward_workspace(int64_t B, int64_t T, int64_t C, int64_t K, int has_proj_start, int has_proj_end,
+                           size_t* bytes);
+int tsm_backward(const float* cum_scores, const float* transition, const float* duration_bias,
+                 const int64_t* lengths, const float* proj_start, const float* proj_end, int64_t B, int64_t T,
+                 int64_t C, int64_t K, int semiring, const float* alpha_hat, const double* alpha_level,
+                 const double* log2_partition, const float* grad_output, float* grad_cum,
+                 float* grad_transition, float* grad_duration_bias, float* grad_proj_start,
+                 float* grad_proj_end, int32_t* recomputed, void* workspace, size_t workspace_bytes,
+                 void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Exact Viterbi: the reference's fp32 max-semiring forward, bit for bit,
+ * optionally with backpointers and an on-device backtrace.
+ * Replaces:
+ *   streaming/pytorch_reference.py:116-273 (semiring="max") -> score
+ *   nn.py:444-531 SemiMarkovCRFHead._traceback_single        -> segments
+ * Outputs:
+ *   score      (B,) fp32  max over final labels of alpha[len]
+ *   seg_count  (B,) int32 number of segments (with_traceback only)
+ *   segments   (B, T, 4) int32 rows (start, end inclusive, label, previous
+ *              label), last segment first (with_traceback only)
+ * ------------------------------------------------------------------------- */
+int tsm_viterbi_workspace(int64_t B, int64_t T, int64_t C, int64_t K, int with_traceback, size_t* bytes);
+int tsm_viterbi(const float* cum_scores, const float* transition, const float* duration_bias,
+                const int64_t* lengths, const float* proj_start, const float* proj_end, int64_t B, int64_t T,
+                int64_t C, int64_t K, float* score, int with_traceback, int32_t* seg_count, int32_t* segments,
+                void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Ring checkpoints in the reference's layout (B, n_ckpt, K, C), raw alpha in
+ * natural log units, rebuilt from tsm_forward's alpha_hat/alpha_level.
+ * Replaces the ring_checkpoints output of
+ *   streaming/pytorch_reference.py:192-258 / triton_forward.py:643-648,711-712
+ * ------------------------------------------------------------------------- */
+int tsm_ring_checkpoints(const float* alpha_hat, const double* alpha_level, const int64_t* lengths, int64_t B,
+                         int64_t T, int64_t C, int64_t K, int64_t checkpoint_interval, int64_t n_checkpoints,
+                         float* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TSM_HIP_H */

@@ -1,0 +1,334 @@
+"""GPU parity tests: the HIP path (through the C ABI) against the oracle and the
+reference's golden vectors.
+
+Tolerances: log Z within 1e-5 relative; gradients
+within 1e-5 relative + 1e-4 absolute against the fp64 oracle; Viterbi scores and
+segmentations bit-exact against the fp32 restatement of the reference.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import gpu_available, load_golden
+from oracle import brute as BR
+from oracle import streaming_ref as R
+
+pytestmark = pytest.mark.gpu
+
+if gpu_available():
+    DEV = torch.device("cuda", 0)
+else:  # collected on CPU, never run there
+    DEV = None
+
+import torch_semimarkov_amd as tsa  # noqa: E402
+from torch_semimarkov_amd.streaming import launch_streaming_hip_backward, launch_streaming_hip_kernel, ops  # noqa: E402
+
+RTOL_Z = 1e-5
+GRAD_TOL = dict(rtol=1e-5, atol=1e-4)
+
+STREAM_FIXTURES = [
+    "stream_basic", "stream_varlen", "stream_k1", "stream_c24", "stream_t1", "stream_t2",
+    "stream_proj", "stream_max", "stream_nocentre", "stream_medium",
+]
+
+
+def fixture_inputs(z, requires_grad=False):
+    t = lambda k: torch.from_numpy(z[k]).to(DEV)
+    cum, tr, db = t("cum"), t("transition"), t("duration_bias")
+    L = torch.from_numpy(z["lengths"])
+    ps = t("proj_start") if "proj_start" in z else None
+    pe = t("proj_end") if "proj_end" in z else None
+    if requires_grad:
+        for x in (cum, tr, db, ps, pe):
+            if x is not None:
+                x.requires_grad_(True)
+    return cum, tr, db, L, int(z["K"]), str(z["semiring"]), ps, pe
+
+
+def rand_problem(B, T, K, C, seed, lengths=None, proj=False, centre=False, tscale=0.1, dscale=0.1):
+    g = torch.Generator().manual_seed(seed)
+    em = torch.randn(B, T, C, generator=g)
+    if centre:
+        em = em - em.mean(1, keepdim=True)
+    cum = torch.zeros(B, T + 1, C)
+    cum[:, 1:] = em.cumsum(1)
+    tr = tscale * torch.randn(C, C, generator=g)
+    db = dscale * torch.randn(K, C, generator=g)
+    L = torch.full((B,), T, dtype=torch.long) if lengths is None else torch.tensor(lengths, dtype=torch.long)
+    ps = 0.1 * torch.randn(B, T, C, generator=g) if proj else None
+    pe = 0.1 * torch.randn(B, T, C, generator=g) if proj else None
+    return cum, tr, db, L, ps, pe
+
+
+def oracle_fp64(cum, tr, db, L, K, semiring="log", ps=None, pe=None, g=None):
+    """fp64 oracle partition and grads (weighted by g)."""
+    d = lambda x: None if x is None else x.detach().cpu().double().requires_grad_(True)
+    c64, t64, b64, p64, e64 = d(cum), d(tr), d(db), d(ps), d(pe)
+    part = R.streaming_oracle(c64, t64, b64, L.cpu(), K, semiring, p64, e64)
+    gw = torch.ones_like(part) if g is None else g.double().cpu()
+    ins = [x for x in (c64, t64, b64, p64, e64) if x is not None]
+    grads = torch.autograd.grad((part * gw).sum(), ins)
+    return part.detach(), grads
+
+
+def to_dev(*xs):
+    return [None if x is None else x.to(DEV) for x in xs]
+
+
+def run_hip(cum, tr, db, L, K, semiring="log", ps=None, pe=None, g=None):
+    cum, tr, db, ps, pe = to_dev(cum, tr, db, ps, pe)
+    ins = [x.clone().requires_grad_(True) for x in (cum, tr, db, ps, pe) if x is not None]
+    it = iter(ins)
+    c, t, b = next(it), next(it), next(it)
+    p = next(it) if ps is not None else None
+    e = next(it) if pe is not None else None
+    part = tsa.semi_crf_streaming_forward(c, t, b, L, K, semiring=semiring, proj_start=p, proj_end=e)
+    gw = torch.ones_like(part) if g is None else g.to(DEV)
+    grads = torch.autograd.grad((part * gw).sum(), ins)
+    return part.detach().cpu(), [x.cpu() for x in grads]
+
+
+def assert_grads(got, want, tol=GRAD_TOL):
+    for a, b in zip(got, want):
+        np.testing.assert_allclose(a.double().numpy(), b.double().numpy(), **tol)
+
+
+# --------------------------------------------------------------------------- golden vectors
+@pytest.mark.parametrize("name", STREAM_FIXTURES)
+def test_forward_backward_match_reference_golden(name):
+    z = load_golden(name)
+    cum, tr, db, L, K, sr, ps, pe = fixture_inputs(z, requires_grad=True)
+    part = tsa.semi_crf_streaming_forward(cum, tr, db, L, K, semiring=sr, proj_start=ps, proj_end=pe)
+    want = torch.from_numpy(z["partition"])
+    np.testing.assert_allclose(part.detach().cpu().numpy(), want.numpy(), rtol=RTOL_Z, atol=1e-5)
+    g = torch.from_numpy(z["grad_output"]).to(DEV)
+    (part * g).sum().backward()
+    got = [cum.grad.cpu(), tr.grad.cpu(), db.grad.cpu()] + ([ps.grad.cpu(), pe.grad.cpu()] if ps is not None else [])
+    ref32 = [torch.from_numpy(z[k]) for k in ("grad_cum", "grad_transition", "grad_duration_bias")]
+    if ps is not None:
+        ref32 += [torch.from_numpy(z["grad_proj_start"]), torch.from_numpy(z["grad_proj_end"])]
+    if float(np.abs(z["partition"]).max()) < 1000:
+        # short sequences: the reference's fp32 gradients are accurate to ~1e-5
+        assert_grads(got, ref32)
+    else:
+        # |alpha| ~ 5e3: the reference's raw fp32 log-space values lose ~1e-3 in the
+        # marginals, so the yardstick is the fp64 oracle; the build must also be
+        # closer to it than the reference is
+        _, g64 = oracle_fp64(*(torch.from_numpy(z[k]) for k in ("cum", "transition", "duration_bias")),
+                             torch.from_numpy(z["lengths"]), K, sr, g=torch.from_numpy(z["grad_output"]))
+        assert_grads(got, g64)
+        for a, r, w in zip(got, ref32, g64):
+            assert (a.double() - w).abs().max() <= (r.double() - w).abs().max()
+
+
+@pytest.mark.parametrize("name", STREAM_FIXTURES)
+def test_inference_matches_reference_golden(name):
+    """No-grad path: log partition within tolerance; max semiring bit-exact (exact Viterbi kernel)."""
+    z = load_golden(name)
+    cum, tr, db, L, K, sr, ps, pe = fixture_inputs(z)
+    with torch.no_grad():
+        part = tsa.semi_crf_streaming_forward(cum, tr, db, L, K, semiring=sr, proj_start=ps, proj_end=pe)
+        vit = tsa.semi_crf_streaming_forward(cum, tr, db, L, K, semiring="max", proj_start=ps, proj_end=pe)
+    np.testing.assert_allclose(part.cpu().numpy(), z["partition_raw"], rtol=RTOL_Z, atol=1e-5)
+    if sr == "max":
+        assert np.array_equal(part.cpu().numpy(), z["partition_raw"])
+    want_max, _, _ = R.forward(*[torch.from_numpy(z[k]) for k in ("cum", "transition", "duration_bias", "lengths")],
+                               K, "max",
+                               torch.from_numpy(z["proj_start"]) if "proj_start" in z else None,
+                               torch.from_numpy(z["proj_end"]) if "proj_end" in z else None)
+    assert torch.equal(vit.cpu(), want_max)
+
+
+def test_duration_dependent_transitions_not_supported():
+    z = load_golden("stream_durtrans")
+    cum, tr, db, L, K, sr, ps, pe = fixture_inputs(z)
+    with pytest.raises(NotImplementedError):
+        tsa.semi_crf_streaming_forward(cum, tr, db, L, K)
+
+
+# --------------------------------------------------------------------------- fp64 oracle
+CASES = [
+    # B, T, K, C, lengths, proj, semiring
+    (2, 40, 6, 4, [40, 23], False, "log"),
+    (3, 35, 1, 5, [35, 20, 1], False, "log"),
+    (2, 50, 9, 3, [50, 50], True, "log"),
+    (1, 64, 12, 33, None, False, "log"),
+    (2, 30, 5, 1, [30, 12], False, "log"),
+    (2, 45, 7, 4, [45, 30], False, "max"),
+    (4, 25, 30, 6, [25, 24, 3, 0], False, "log"),
+]
+
+
+@pytest.mark.parametrize("B,T,K,C,lengths,proj,sr", CASES)
+def test_random_problems_vs_fp64_oracle(B, T, K, C, lengths, proj, sr):
+    cum, tr, db, L, ps, pe = rand_problem(B, T, K, C, 1000 + T + K + C, lengths, proj)
+    g = torch.linspace(0.5, 2.0, B)
+    p64, g64 = oracle_fp64(cum, tr, db, L, K, sr, ps, pe, g)
+    part, grads = run_hip(cum, tr, db, L, K, sr, ps, pe, g)
+    live = L > 0
+    np.testing.assert_allclose(part[live].double().numpy(), p64[live].numpy(), rtol=RTOL_Z, atol=1e-6)
+    assert_grads(grads, g64)
+
+
+def test_chunked_scan_vs_fp64_oracle():
+    """T long enough for several speculative chunks (warm-up + verification)."""
+    B, T, K, C = 2, 2600, 8, 4
+    cum, tr, db, L, _, _ = rand_problem(B, T, K, C, 77, lengths=[2600, 1900])
+    from torch_semimarkov_amd import _native as N
+
+    assert N.plan_info(B, T, C, K)["P"] > 1
+    p64, g64 = oracle_fp64(cum, tr, db, L, K)
+    part, grads = run_hip(cum, tr, db, L, K)
+    np.testing.assert_allclose(part.double().numpy(), p64.numpy(), rtol=RTOL_Z)
+    assert_grads(grads, g64)
+
+
+def test_verifier_recomputes_non_mixing_chunks():
+    """Sticky transitions keep early evidence alive across chunk boundaries, so
+    the warmed-up states disagree with the exact ones and chunks are recomputed
+    from the previous chunk's exact state; results still match the oracle."""
+    B, T, K, C = 1, 2400, 5, 3
+    g = torch.Generator().manual_seed(5)
+    em = 0.01 * torch.randn(B, T, C, generator=g)
+    em[:, :50, 0] += 2.0
+    cum = torch.zeros(B, T + 1, C)
+    cum[:, 1:] = em.cumsum(1)
+    tr = torch.full((C, C), -40.0)
+    tr.fill_diagonal_(0.0)
+    db = torch.zeros(K, C)
+    L = torch.tensor([T])
+    with torch.no_grad():
+        _, _, _, _, rec = ops.scan_forward(cum.to(DEV), tr.to(DEV), db.to(DEV), L.to(DEV), K, 0, None, None, False)
+    assert int(rec.sum()) > 0
+    p64, g64 = oracle_fp64(cum, tr, db, L, K)
+    part, grads = run_hip(cum, tr, db, L, K)
+    np.testing.assert_allclose(part.double().numpy(), p64.numpy(), rtol=RTOL_Z)
+    assert_grads(grads, g64)
+
+
+def test_grad_output_weighting_and_isolation():
+    """tests/test_streaming_triton.py:901-1087: shared grads are sum_b g_b * grad_b, per-sequence
+    grads are scaled, a zero weight isolates a sequence."""
+    cum, tr, db, L, _, _ = rand_problem(2, 30, 5, 4, 9, [30, 22])
+    _, ga = run_hip(cum, tr, db, L, 5, g=torch.tensor([1.0, 0.0]))
+    _, gb = run_hip(cum, tr, db, L, 5, g=torch.tensor([0.0, 1.0]))
+    _, gh = run_hip(cum, tr, db, L, 5, g=torch.tensor([0.5, 2.0]))
+    assert torch.all(ga[0][1] == 0) and torch.all(gb[0][0] == 0)
+    for i in range(3):
+        torch.testing.assert_close(gh[i], 0.5 * ga[i] + 2.0 * gb[i], rtol=1e-5, atol=1e-6)
+
+
+def test_deterministic_bitwise():
+    cum, tr, db, L, ps, pe = rand_problem(3, 300, 10, 6, 3, [300, 250, 10], proj=True)
+    a = run_hip(cum, tr, db, L, 10, ps=ps, pe=pe)
+    b = run_hip(cum, tr, db, L, 10, ps=ps, pe=pe)
+    assert torch.equal(a[0], b[0])
+    for x, y in zip(a[1], b[1]):
+        assert torch.equal(x, y)
+
+
+def test_k1_full_size_config2_vs_hmm():
+    """BASELINE config 2 (B=32, T=10^4, C=8, K=1) against a probability-space HMM in fp64."""
+    B, T, C, K = 32, 10_000, 8, 1
+    g = torch.Generator().manual_seed(20261202)
+    em = torch.randn(B, T, C, generator=g)
+    tr = 0.1 * torch.randn(C, C, generator=g)
+    db = 0.1 * torch.randn(1, C, generator=g)
+    cum = torch.zeros(B, T + 1, C)
+    cum[:, 1:] = em.cumsum(1)
+    L = torch.full((B,), T)
+    part, grads = run_hip(cum, tr, db, L, K)
+    cum64 = cum.double().numpy()
+    for b in range(0, B, 8):
+        logZ, state_post, trans_counts, _ = BR.hmm_forward_backward(cum64[b], tr.double().numpy(),
+                                                                    db[0].double().numpy(), T)
+        assert abs(part[b].item() - logZ) <= RTOL_Z * abs(logZ)
+        want = np.zeros((T + 1, C))
+        want[1:] += state_post
+        want[:-1] -= state_post
+        np.testing.assert_allclose(grads[0][b].double().numpy(), want, rtol=1e-5, atol=1e-4)
+
+
+# --------------------------------------------------------------------------- exact Viterbi
+@pytest.mark.parametrize("B,T,K,C,lengths", [(3, 120, 10, 6, [120, 77, 5]), (2, 60, 1, 4, [60, 31]),
+                                             (2, 200, 64, 32, [200, 150])])
+def test_viterbi_scores_and_segments_exact(B, T, K, C, lengths):
+    cum, tr, db, L, _, _ = rand_problem(B, T, K, C, 31 + C, lengths, tscale=0.5, dscale=0.5)
+    score, cnt, segs = ops.viterbi(cum.to(DEV), tr.to(DEV), db.to(DEV), L.to(DEV), K, None, None, True)
+    want, _, _ = R.forward(cum, tr, db, L, K, "max")
+    assert torch.equal(score.cpu(), want)
+    cnt = cnt.cpu()
+    segs = segs.cpu()
+    for b in range(B):
+        ref_segs, best = R.viterbi_traceback_single(cum[b], tr, db, K, int(L[b]))
+        got = [tuple(int(v) for v in segs[b, i]) for i in range(int(cnt[b]) - 1, -1, -1)]
+        assert got == [tuple(s) for s in ref_segs]
+
+
+# --------------------------------------------------------------------------- head
+@pytest.mark.parametrize("name", ["head_small", "head_proj"])
+def test_head_matches_reference_golden(name):
+    z = load_golden(name)
+    C, K = int(z["C"]), int(z["K"])
+    H = z["hidden"].shape[-1]
+    head = tsa.SemiMarkovCRFHead(C, K, hidden_dim=H if "proj_weight" in z else None).to(DEV)
+    with torch.no_grad():
+        head.transition.copy_(torch.from_numpy(z["transition"]))
+        head.duration_dist.duration_bias.copy_(torch.from_numpy(z["duration_bias"]))
+        if head.projection is not None:
+            head.projection.weight.copy_(torch.from_numpy(z["proj_weight"]))
+            head.projection.bias.copy_(torch.from_numpy(z["proj_bias"]))
+    hidden = torch.from_numpy(z["hidden"]).to(DEV)
+    L = torch.from_numpy(z["lengths"]).to(DEV)
+    labels = torch.from_numpy(z["labels"]).to(DEV)
+    loss = head.compute_loss(hidden, L, labels, reduction="none")
+    np.testing.assert_allclose(loss.detach().cpu().numpy(), z["loss"], rtol=1e-5, atol=1e-4)
+    loss.sum().backward()
+    np.testing.assert_allclose(head.transition.grad.cpu().numpy(), z["grad_transition"], **GRAD_TOL)
+    np.testing.assert_allclose(head.duration_dist.duration_bias.grad.cpu().numpy(), z["grad_duration_bias"],
+                               **GRAD_TOL)
+    if head.projection is not None:
+        np.testing.assert_allclose(head.projection.weight.grad.cpu().numpy(), z["grad_proj_weight"],
+                                   rtol=1e-5, atol=2e-4)
+    with torch.no_grad():
+        part = head(hidden, L)["partition"]
+        vit = head.decode(hidden, L)
+        res = head.decode_with_traceback(hidden, L, int(z["max_traceback_length"]))
+    np.testing.assert_allclose(part.cpu().numpy(), z["partition"], rtol=1e-5, atol=1e-5)
+    # the head builds cum_scores with the GPU's cumsum/Linear, whose fp32 rounding differs
+    # from the reference's CPU run, so head-level scores agree to 1e-5 (the scan itself is
+    # bit-exact for identical cum_scores, see test_inference_matches_reference_golden)
+    np.testing.assert_allclose(vit.cpu().numpy(), z["viterbi"], rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(res.scores.cpu().numpy(), z["traceback_scores"], rtol=1e-5, atol=1e-5)
+    assert torch.equal(res.scores, vit)
+    got = [(b, s.start, s.end, s.label) for b, sl in enumerate(res.segments) for s in sl]
+    np.testing.assert_array_equal(np.array(got, dtype=np.int64).reshape(-1, 4), z["segments"])
+    sc = np.array([s.score for sl in res.segments for s in sl])
+    np.testing.assert_allclose(sc, z["segment_scores"], rtol=1e-5, atol=1e-5)
+    for b, sl in enumerate(res.segments):
+        assert abs(sum(s.score for s in sl) - res.scores[b].item()) < 1e-4
+
+
+def test_traceback_skips_long_sequences():
+    head = tsa.SemiMarkovCRFHead(3, 5).to(DEV)
+    hidden = torch.randn(2, 30, 3, device=DEV)
+    res = head.decode_with_traceback(hidden, torch.tensor([30, 12], device=DEV), max_traceback_length=20)
+    assert res.segments[0] == [] and len(res.segments[1]) >= 1
+    assert res.segments[1][0].start == 0 and res.segments[1][-1].end == 11
+
+
+# --------------------------------------------------------------------------- launcher contracts
+def test_launcher_checkpoints_and_backward_contract():
+    z = load_golden("stream_varlen")
+    cum, tr, db, L, K, sr, ps, pe = fixture_inputs(z)
+    part, ck, S = launch_streaming_hip_kernel(cum, tr, db, L, K)
+    assert S == int(z["checkpoint_interval"])
+    want = torch.from_numpy(z["ring_checkpoints"])
+    assert ck.shape == want.shape
+    np.testing.assert_allclose(ck.cpu().numpy(), want.numpy(), rtol=1e-5, atol=1e-4)
+    g = torch.ones(cum.shape[0], device=DEV)
+    gc, gt, gd, gps, gpe = launch_streaming_hip_backward(cum, tr, db, L, part, ck, S, g)
+    assert gps is None and gpe is None
+    assert_grads([gc.cpu(), gt.cpu(), gd.cpu()],
+                 [torch.from_numpy(z[k]) for k in ("grad_cum", "grad_transition", "grad_duration_bias")])

@@ -1,0 +1,161 @@
+"""Host-side checks that need no GPU: the C ABI library loads and exports every
+declared symbol, plans/workspaces and error paths behave, the Python layer
+validates inputs and fails loudly off-GPU, and the device-agnostic helpers
+match the oracle."""
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import ROOT, load_golden
+from oracle import streaming_ref as R
+
+import torch_semimarkov_amd as tsa
+from torch_semimarkov_amd import _native as N
+from torch_semimarkov_amd.streaming import compute_edge_block_streaming
+
+HEADER = os.path.join(ROOT, "include", "tsm_hip.h")
+
+
+def declared_symbols():
+    txt = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(tsm_\w+)\(", txt, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = N.lib()
+    decl = declared_symbols()
+    assert len(decl) >= 10
+    for name in decl:
+        assert hasattr(lib, name), name
+    assert sorted(N.EXPORTED) == decl
+
+
+def test_version_and_error_message():
+    lib = N.lib()
+    assert lib.tsm_version() >= 100
+    out = ctypes.c_size_t(0)
+    rc = lib.tsm_forward_workspace(0, 10, 4, 3, 0, 0, 0, ctypes.byref(out))
+    assert rc == 1
+    assert b"B, T, C, K" in lib.tsm_last_error()
+    rc = lib.tsm_forward_workspace(1, 10, 4, 3, 7, 0, 0, ctypes.byref(out))
+    assert rc == 1 and b"semiring" in lib.tsm_last_error()
+
+
+def test_plan_and_workspace_queries_without_gpu():
+    p = N.plan_info(1, 1_000_000, 24, 300)
+    assert p["Kmax"] == 299 and p["J"] == 16 and p["NT"] == 384
+    assert p["RS"] >= p["Kmax"] + 2 and p["RS"] % 32 == 16
+    assert p["P"] > 1 and p["Lc"] * p["P"] >= 1_000_000 and p["Lc"] >= 4 * p["W"]
+    assert p["TB"] >= p["Kmax"] and p["NB"] * p["TB"] >= 1_000_000
+    # small problems run exactly in one chunk
+    assert N.plan_info(4, 1000, 24, 100)["P"] == 1
+    # large label spaces split the marginal kernel into label blocks
+    q = N.plan_info(8, 50_000, 128, 500)
+    assert q["CB"] * q["NCB"] >= 128 and q["marg_lds"] <= 160 * 1024
+    for fn, args in (
+        (N.lib().tsm_forward_workspace, (2, 100, 8, 5, 0, 0, 0)),
+        (N.lib().tsm_backward_workspace, (2, 100, 8, 5, 1, 1)),
+        (N.lib().tsm_viterbi_workspace, (2, 100, 8, 5, 1)),
+    ):
+        out = ctypes.c_size_t(0)
+        assert fn(*args, ctypes.byref(out)) == 0 and out.value > 0
+
+
+def test_c_abi_rejects_bad_calls_without_touching_the_device():
+    lib = N.lib()
+    # missing required pointers
+    rc = lib.tsm_forward(None, None, None, None, None, None, 1, 10, 4, 3, 0, None, None, None, None, None,
+                         None, 0, None)
+    assert rc == 1
+    # workspace too small is reported before any launch
+    buf = ctypes.create_string_buffer(16)
+    fake = ctypes.addressof(buf)
+    rc = lib.tsm_forward(fake, fake, fake, fake, None, None, 1, 10, 4, 3, 0, fake, None, None, None, None,
+                         fake, 1, None)
+    assert rc == 4 and b"workspace" in lib.tsm_last_error()
+    rc = lib.tsm_forward(fake, fake, fake, fake, None, None, 1, 10, 4, 3, 0, fake, None, fake, None, None,
+                         fake, 10**9, None)
+    assert rc == 1 and b"alpha_hat and alpha_level" in lib.tsm_last_error()
+    rc = lib.tsm_plan_info(1, 10, 600, 3, 0, 0, None, 0)
+    assert rc == 2
+
+
+def test_python_api_fails_loudly_off_gpu():
+    cum = torch.zeros(1, 6, 3)
+    tr = torch.zeros(3, 3)
+    db = torch.zeros(4, 3)
+    L = torch.tensor([5])
+    with pytest.raises(ValueError, match="semiring"):
+        tsa.semi_crf_streaming_forward(cum, tr, db, L, 4, semiring="sum")
+    with pytest.raises(RuntimeError, match="AMD GPU"):
+        tsa.semi_crf_streaming_forward(cum, tr, db, L, 4)
+    head = tsa.SemiMarkovCRFHead(3, 4)
+    with pytest.raises(RuntimeError, match="AMD GPU"):
+        head(torch.zeros(1, 5, 3), L)
+
+
+def test_reference_head_initialisation_order():
+    """Seeded init draws transition, then duration bias, then the projection (nn.py:146-162)."""
+    z = load_golden("head_proj")
+    torch.manual_seed(202)
+    head = tsa.SemiMarkovCRFHead(num_classes=6, max_duration=12, hidden_dim=16)
+    np.testing.assert_array_equal(head.transition.detach().numpy(), z["transition"])
+    np.testing.assert_array_equal(head.duration_bias.detach().numpy(), z["duration_bias"])
+    np.testing.assert_array_equal(head.projection.weight.detach().numpy(), z["proj_weight"])
+    assert "max_duration=12" in repr(head)
+
+
+@pytest.mark.parametrize("seed,B,T,C,K", [(1, 3, 17, 4, 5), (2, 2, 9, 3, 1), (3, 4, 30, 5, 40), (4, 2, 1, 3, 4)])
+def test_score_gold_matches_oracle(seed, B, T, C, K):
+    g = torch.Generator().manual_seed(seed)
+    cum = torch.zeros(B, T + 1, C)
+    cum[:, 1:] = torch.randn(B, T, C, generator=g).cumsum(1)
+    tr = torch.randn(C, C, generator=g)
+    db = torch.randn(max(K, 2), C, generator=g)[:K] if K > 1 else torch.randn(2, C, generator=g)
+    labels = torch.randint(0, C, (B, T), generator=g)
+    labels[:, T // 3: T // 2] = 1  # long runs
+    lengths = torch.randint(1, T + 1, (B,), generator=g)
+    lengths[0] = T
+    want = R.score_gold(cum, labels, lengths, tr, db, K)
+    got = tsa.score_gold_vectorized(cum, labels, lengths, tr, db, K)
+    torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-4)
+
+
+def test_score_gold_matches_reference_loss_fixture():
+    z = load_golden("head_small")
+    C, K = int(z["C"]), int(z["K"])
+    hidden = torch.from_numpy(z["hidden"])
+    cum = torch.zeros(hidden.shape[0], hidden.shape[1] + 1, C)
+    cum[:, 1:] = torch.cumsum(hidden, 1)
+    L = torch.from_numpy(z["lengths"])
+    tr = torch.from_numpy(z["transition"])
+    db = torch.from_numpy(z["duration_bias"])
+    part, _, _ = R.forward(cum, tr, db, L, K)
+    gold = tsa.score_gold_vectorized(cum, torch.from_numpy(z["labels"]), L, tr, db, K)
+    np.testing.assert_allclose((part - gold).numpy(), z["loss"], rtol=1e-5, atol=1e-4)
+
+
+def test_compute_edge_block_matches_oracle():
+    g = torch.Generator().manual_seed(5)
+    B, T, C, K = 2, 20, 3, 6
+    cum = torch.randn(B, T + 1, C, generator=g).cumsum(1)
+    tr = torch.randn(C, C, generator=g)
+    db = torch.randn(K, C, generator=g)
+    ps = torch.randn(B, T, C, generator=g)
+    pe = torch.randn(B, T, C, generator=g)
+    for t, k in [(3, 2), (10, 5), (0, 1)]:
+        got = compute_edge_block_streaming(cum, tr, db, t, k, ps, pe)
+        want = R.edge_blocks(cum, tr, db, torch.tensor([t]), torch.tensor([k]), ps, pe)[:, 0]
+        assert torch.equal(got, want)
+
+
+def test_segment_dataclass():
+    s = tsa.Segment(start=3, end=7, label=2, score=1.5)
+    assert s.duration == 5
+    r = tsa.ViterbiResult(scores=torch.zeros(1), segments=[[s]])
+    assert r.segments[0][0].label == 2

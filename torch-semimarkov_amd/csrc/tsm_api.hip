@@ -1,0 +1,466 @@
+// C ABI of libtsm_hip.so (declarations and documentation in include/tsm_hip.h).
+// Host side only: validation, launch plan, workspace carving, kernel launches.
+// Nothing here allocates device memory; all state lives in caller buffers.
+
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <string>
+
+#include "../../include/tsm_hip.h"
+#include "tsm_internal.hpp"
+
+namespace tsm {
+size_t viterbi_lds_bytes(int C, int Kmax, int RS, int has_ps);
+}
+
+namespace {
+
+using tsm::Plan;
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int hip_fail(int e, const char* where) {
+  return fail(TSM_ERR_HIP, "%s: HIP error %d (%s)", where, e, hipGetErrorString((hipError_t)e));
+}
+
+struct DeviceInfo {
+  int n_cu = 256;
+  int max_lds = 160 * 1024;
+};
+
+DeviceInfo device_info() {
+  DeviceInfo d;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return d;
+  }
+  int v = 0;
+  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) d.n_cu = v;
+  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess && v > 0)
+    d.max_lds = v;
+  (void)hipGetLastError();
+  return d;
+}
+
+int pow2_lanes(int C) {
+  int J = 64;
+  while (J > 1 && (int64_t)C * J > 512) J >>= 1;
+  return J;
+}
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Thread mapping, rings, chunking and marginal blocking for a problem shape.
+int make_plan(int64_t B, int64_t T, int64_t C, int64_t K, int has_ps, int has_pe, Plan* out) {
+  if (B < 1 || T < 1 || C < 1 || K < 1) return fail(TSM_ERR_INVALID, "need B, T, C, K >= 1 (got %lld, %lld, %lld, %lld)",
+                                                    (long long)B, (long long)T, (long long)C, (long long)K);
+  if (C > 512) return fail(TSM_ERR_UNSUPPORTED, "num_classes C=%lld > 512 is not supported", (long long)C);
+  if (K > 65535) return fail(TSM_ERR_UNSUPPORTED, "max_duration K=%lld > 65535 is not supported", (long long)K);
+  if (T > (int64_t)1 << 30) return fail(TSM_ERR_UNSUPPORTED, "T=%lld is too long", (long long)T);
+  const DeviceInfo di = device_info();
+  Plan p{};
+  p.B = (int)B;
+  p.T = (int)T;
+  p.C = (int)C;
+  p.K = (int)K;
+  p.Kmax = (int)std::max<int64_t>(K - 1, 1);
+  p.has_ps = has_ps;
+  p.has_pe = has_pe;
+  p.J = pow2_lanes(p.C);
+  p.NT = (int)cdiv((int64_t)p.C * p.J, 64) * 64;
+  // ring length: >= Kmax+2; RS % 32 == J % 32 spreads label groups over LDS banks
+  int rs = p.Kmax + 2;
+  while (rs % 32 != p.J % 32) ++rs;
+  p.RS = rs;
+  const int has_proj = (has_ps || has_pe) ? 1 : 0;
+  size_t lds = tsm::scan_lds_layout(p.C, p.Kmax, p.RS, has_proj, 0).total;
+  p.global_rings = 0;
+  if (lds > (size_t)di.max_lds) {
+    p.global_rings = 1;
+    lds = tsm::scan_lds_layout(p.C, p.Kmax, p.RS, has_proj, 1).total;
+    if (lds > (size_t)di.max_lds)
+      return fail(TSM_ERR_UNSUPPORTED, "C=%d needs %zu bytes of LDS (> %d)", p.C, lds, di.max_lds);
+  }
+  p.scan_lds = lds;
+  // chunking: about one work item per CU; chunks long enough that the warm-up
+  // (W steps) costs at most ~25%.
+  p.W = p.Kmax + 64;
+  const int64_t min_lc = std::max<int64_t>(4 * (int64_t)p.W, 512);
+  int64_t P = cdiv(di.n_cu, B);
+  P = std::min<int64_t>(P, std::max<int64_t>(1, T / min_lc));
+  P = std::max<int64_t>(P, 1);
+  p.P = (int)P;
+  p.Lc = (int)cdiv(T, P);
+  // marginal kernel: label blocks so the rings fit in LDS
+  int CB = p.C;
+  for (;;) {
+    const int JM = pow2_lanes(CB);
+    const size_t ml = tsm::marg_lds_layout(p.C, CB, p.Kmax, p.RS, has_pe).total;
+    if (ml <= (size_t)di.max_lds) {
+      p.CB = CB;
+      p.JM = JM;
+      p.NTM = (int)cdiv((int64_t)CB * JM, 64) * 64;
+      p.marg_lds = ml;
+      break;
+    }
+    if (CB == 1) return fail(TSM_ERR_UNSUPPORTED, "marginal kernel does not fit LDS (K=%d)", p.K);
+    CB = (CB + 1) / 2;
+  }
+  p.NCB = (int)cdiv(p.C, p.CB);
+  int64_t NB = cdiv(2 * (int64_t)di.n_cu, B * p.NCB);
+  NB = std::min<int64_t>(NB, std::max<int64_t>(1, T / std::max(p.Kmax, 64)));
+  NB = std::max<int64_t>(NB, 1);
+  int64_t TB = cdiv(T, NB);
+  if (TB < p.Kmax) {
+    TB = p.Kmax;
+    NB = cdiv(T, TB);
+  }
+  p.NB = (int)NB;
+  p.TB = (int)TB;
+  *out = p;
+  return TSM_OK;
+}
+
+// Bump allocator over the caller's workspace (256-byte aligned pieces).
+struct Carver {
+  char* base;
+  size_t off = 0;
+  explicit Carver(void* b) : base(static_cast<char*>(b)) {}
+  template <typename T>
+  T* take(size_t n) {
+    off = (off + 255) & ~size_t(255);
+    T* p = base ? reinterpret_cast<T*>(base + off) : nullptr;
+    off += n * sizeof(T);
+    return p;
+  }
+};
+
+struct ScanWs {
+  float *st_spec, *st_end, *fin, *gring;
+  double *lv_spec, *lv_end, *offs, *fin_lvl, *z2;
+  int* status;
+};
+
+ScanWs carve_scan(Carver& cv, const Plan& p) {
+  ScanWs w;
+  const size_t items = (size_t)p.B * p.P;
+  w.st_spec = cv.take<float>(items * p.Kmax * p.C);
+  w.st_end = cv.take<float>(items * p.Kmax * p.C);
+  w.lv_spec = cv.take<double>(items * p.Kmax);
+  w.lv_end = cv.take<double>(items * p.Kmax);
+  w.offs = cv.take<double>(items);
+  w.status = cv.take<int>(items);
+  w.fin = cv.take<float>((size_t)p.B * p.C);
+  w.fin_lvl = cv.take<double>(p.B);
+  w.z2 = cv.take<double>(p.B);
+  w.gring = p.global_rings ? cv.take<float>(items * tsm::scan_gring_floats(p.C, p.Kmax, p.RS)) : nullptr;
+  return w;
+}
+
+tsm::ScanParams scan_params(const Plan& pl, const ScanWs& w, const float* cum, const float* tr, const float* db,
+                            const int64_t* len, const float* ps, const float* pe) {
+  tsm::ScanParams p{};
+  p.cum = cum;
+  p.trans = tr;
+  p.db = db;
+  p.lengths = len;
+  p.ps = ps;
+  p.pe = pe;
+  p.B = pl.B;
+  p.T = pl.T;
+  p.C = pl.C;
+  p.K = pl.K;
+  p.Kmax = pl.Kmax;
+  p.RS = pl.RS;
+  p.P = pl.P;
+  p.Lc = pl.Lc;
+  p.W = pl.W;
+  p.tol = 2.0e-4f;
+  p.st_spec = w.st_spec;
+  p.st_end = w.st_end;
+  p.lv_spec = w.lv_spec;
+  p.lv_end = w.lv_end;
+  p.offs = w.offs;
+  p.status = w.status;
+  p.fin = w.fin;
+  p.fin_lvl = w.fin_lvl;
+  p.z2 = w.z2;
+  p.gring = w.gring;
+  return p;
+}
+
+int check_common(const float* cum, const float* tr, const float* db, const int64_t* len, int semiring) {
+  if (!cum || !tr || !db || !len) return fail(TSM_ERR_INVALID, "cum_scores, transition, duration_bias and lengths are required");
+  if (semiring != TSM_SEMIRING_LOG && semiring != TSM_SEMIRING_MAX)
+    return fail(TSM_ERR_INVALID, "semiring must be TSM_SEMIRING_LOG (0) or TSM_SEMIRING_MAX (1), got %d", semiring);
+  return TSM_OK;
+}
+
+size_t forward_ws_bytes(const Plan& pl) {
+  Carver cv(nullptr);
+  carve_scan(cv, pl);
+  return cv.off + 256;
+}
+
+size_t backward_ws_bytes(const Plan& pl) {
+  Carver cv(nullptr);
+  const size_t rows = (size_t)pl.B * (pl.T + 1);
+  cv.take<float>(rows * pl.C);   // beta-hat
+  cv.take<double>(rows);         // beta levels
+  carve_scan(cv, pl);
+  cv.take<float>(rows * pl.C);   // e_own
+  cv.take<float>(rows * pl.C);   // s_out
+  cv.take<float>((size_t)pl.B * pl.NB * pl.Kmax * pl.C);   // halo
+  cv.take<double>((size_t)pl.B * pl.NB * pl.Kmax * pl.C);  // db_part
+  cv.take<double>((size_t)pl.B * pl.NB * pl.C * pl.C);     // tr_part
+  return cv.off + 256;
+}
+
+size_t viterbi_ws_bytes(const Plan& pl, int with_tb) {
+  Carver cv(nullptr);
+  if (with_tb) cv.take<int32_t>((size_t)pl.B * (pl.T + 1) * pl.C);
+  cv.take<int32_t>(pl.B);
+  return cv.off + 256;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tsm_version(void) { return 100; }
+
+const char* tsm_last_error(void) { return g_err.c_str(); }
+
+int tsm_plan_info(int64_t B, int64_t T, int64_t C, int64_t K, int has_ps, int has_pe, int64_t* out, int n) {
+  Plan p;
+  int rc = make_plan(B, T, C, K, has_ps, has_pe, &p);
+  if (rc) return rc;
+  if (!out) return fail(TSM_ERR_INVALID, "out is NULL");
+  const DeviceInfo di = device_info();
+  const int64_t vals[] = {p.J, p.NT, p.RS, p.P, p.Lc, p.W, p.global_rings, (int64_t)p.scan_lds, p.NB, p.TB,
+                          p.CB, p.NCB, p.JM, p.NTM, (int64_t)p.marg_lds, p.Kmax, di.n_cu};
+  const int m = (int)(sizeof(vals) / sizeof(vals[0]));
+  for (int i = 0; i < n && i < m; ++i) out[i] = vals[i];
+  return TSM_OK;
+}
+
+int tsm_forward_workspace(int64_t B, int64_t T, int64_t C, int64_t K, int semiring, int has_ps, int has_pe,
+                          size_t* bytes) {
+  if (!bytes) return fail(TSM_ERR_INVALID, "bytes is NULL");
+  if (semiring != TSM_SEMIRING_LOG && semiring != TSM_SEMIRING_MAX) return fail(TSM_ERR_INVALID, "bad semiring %d", semiring);
+  Plan p;
+  int rc = make_plan(B, T, C, K, has_ps, has_pe, &p);
+  if (rc) return rc;
+  *bytes = forward_ws_bytes(p);
+  return TSM_OK;
+}
+
+int tsm_forward(const float* cum, const float* tr, const float* db, const int64_t* len, const float* ps,
+                const float* pe, int64_t B, int64_t T, int64_t C, int64_t K, int semiring, float* partition,
+                double* log2_partition, float* alpha_hat, double* alpha_level, int32_t* recomputed,
+                void* workspace, size_t ws_bytes, void* stream) {
+  int rc = check_common(cum, tr, db, len, semiring);
+  if (rc) return rc;
+  if (!partition) return fail(TSM_ERR_INVALID, "partition output is required");
+  if ((alpha_hat == nullptr) != (alpha_level == nullptr))
+    return fail(TSM_ERR_INVALID, "alpha_hat and alpha_level must both be given or both be NULL");
+  Plan pl;
+  rc = make_plan(B, T, C, K, ps != nullptr, pe != nullptr, &pl);
+  if (rc) return rc;
+  const size_t need = forward_ws_bytes(pl);
+  if (!workspace || ws_bytes < need)
+    return fail(TSM_ERR_WORKSPACE, "forward workspace too small: %zu < %zu bytes", ws_bytes, need);
+  Carver cv(workspace);
+  ScanWs w = carve_scan(cv, pl);
+  tsm::ScanParams p = scan_params(pl, w, cum, tr, db, len, ps, pe);
+  p.val = alpha_hat;
+  p.lvl = alpha_level;
+  if (log2_partition) p.z2 = log2_partition;
+  p.zout = partition;
+  p.recomputed = recomputed;
+  const int e = tsm::launch_scan_forward(pl, p, semiring, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "tsm_forward");
+  return TSM_OK;
+}
+
+int tsm_backward_workspace(int64_t B, int64_t T, int64_t C, int64_t K, int has_ps, int has_pe, size_t* bytes) {
+  if (!bytes) return fail(TSM_ERR_INVALID, "bytes is NULL");
+  Plan p;
+  int rc = make_plan(B, T, C, K, has_ps, has_pe, &p);
+  if (rc) return rc;
+  *bytes = backward_ws_bytes(p);
+  return TSM_OK;
+}
+
+int tsm_backward(const float* cum, const float* tr, const float* db, const int64_t* len, const float* ps,
+                 const float* pe, int64_t B, int64_t T, int64_t C, int64_t K, int semiring, const float* alpha_hat,
+                 const double* alpha_level, const double* log2_partition, const float* grad_output,
+                 float* grad_cum, float* grad_tr, float* grad_db, float* grad_ps, float* grad_pe,
+                 int32_t* recomputed, void* workspace, size_t ws_bytes, void* stream) {
+  int rc = check_common(cum, tr, db, len, semiring);
+  if (rc) return rc;
+  if (!alpha_hat || !alpha_level || !log2_partition || !grad_output || !grad_cum || !grad_tr || !grad_db)
+    return fail(TSM_ERR_INVALID, "alpha_hat, alpha_level, log2_partition, grad_output and the gradient outputs are required");
+  if ((ps != nullptr) != (grad_ps != nullptr) || (pe != nullptr) != (grad_pe != nullptr))
+    return fail(TSM_ERR_INVALID, "a projection gradient buffer is needed exactly when the projection is given");
+  Plan pl;
+  rc = make_plan(B, T, C, K, ps != nullptr, pe != nullptr, &pl);
+  if (rc) return rc;
+  const size_t need = backward_ws_bytes(pl);
+  if (!workspace || ws_bytes < need)
+    return fail(TSM_ERR_WORKSPACE, "backward workspace too small: %zu < %zu bytes", ws_bytes, need);
+  hipStream_t st = (hipStream_t)stream;
+  Carver cv(workspace);
+  const size_t rows = (size_t)pl.B * (pl.T + 1);
+  float* bval = cv.take<float>(rows * pl.C);
+  double* blvl = cv.take<double>(rows);
+  ScanWs w = carve_scan(cv, pl);
+  float* e_own = cv.take<float>(rows * pl.C);
+  float* s_out = cv.take<float>(rows * pl.C);
+  float* halo = cv.take<float>((size_t)pl.B * pl.NB * pl.Kmax * pl.C);
+  double* db_part = cv.take<double>((size_t)pl.B * pl.NB * pl.Kmax * pl.C);
+  double* tr_part = cv.take<double>((size_t)pl.B * pl.NB * pl.C * pl.C);
+
+  tsm::ScanParams p = scan_params(pl, w, cum, tr, db, len, ps, pe);
+  p.val = bval;
+  p.lvl = blvl;
+  p.zout = nullptr;
+  p.recomputed = recomputed;
+  int e = tsm::launch_scan_backward(pl, p, semiring, st);
+  if (e != hipSuccess) return hip_fail(e, "tsm_backward (beta scan)");
+
+  tsm::MargParams q{};
+  q.cum = cum;
+  q.trans = tr;
+  q.db = db;
+  q.lengths = len;
+  q.ps = ps;
+  q.pe = pe;
+  q.B = pl.B;
+  q.T = pl.T;
+  q.C = pl.C;
+  q.K = pl.K;
+  q.Kmax = pl.Kmax;
+  q.RS = pl.RS;
+  q.NB = pl.NB;
+  q.TB = pl.TB;
+  q.CB = pl.CB;
+  q.NCB = pl.NCB;
+  q.aval = alpha_hat;
+  q.alvl = alpha_level;
+  q.bval = bval;
+  q.blvl = blvl;
+  q.z2 = log2_partition;
+  q.e_own = e_own;
+  q.s_out = s_out;
+  q.halo = halo;
+  q.db_part = db_part;
+  q.tr_part = tr_part;
+  e = tsm::launch_marginals(pl, q, st);
+  if (e != hipSuccess) return hip_fail(e, "tsm_backward (marginals)");
+
+  tsm::FinalParams f{};
+  f.lengths = len;
+  f.B = pl.B;
+  f.T = pl.T;
+  f.C = pl.C;
+  f.K = pl.K;
+  f.Kmax = pl.Kmax;
+  f.NB = pl.NB;
+  f.TB = pl.TB;
+  f.e_own = e_own;
+  f.s_out = s_out;
+  f.halo = halo;
+  f.db_part = db_part;
+  f.tr_part = tr_part;
+  f.grad_output = grad_output;
+  f.grad_cum = grad_cum;
+  f.grad_ps = grad_ps;
+  f.grad_pe = grad_pe;
+  f.grad_tr = grad_tr;
+  f.grad_db = grad_db;
+  e = tsm::launch_finalize(pl, f, st);
+  if (e != hipSuccess) return hip_fail(e, "tsm_backward (finalize)");
+  return TSM_OK;
+}
+
+int tsm_viterbi_workspace(int64_t B, int64_t T, int64_t C, int64_t K, int with_tb, size_t* bytes) {
+  if (!bytes) return fail(TSM_ERR_INVALID, "bytes is NULL");
+  Plan p;
+  int rc = make_plan(B, T, C, K, 0, 0, &p);
+  if (rc) return rc;
+  *bytes = viterbi_ws_bytes(p, with_tb);
+  return TSM_OK;
+}
+
+int tsm_viterbi(const float* cum, const float* tr, const float* db, const int64_t* len, const float* ps,
+                const float* pe, int64_t B, int64_t T, int64_t C, int64_t K, float* score, int with_tb,
+                int32_t* seg_count, int32_t* segments, void* workspace, size_t ws_bytes, void* stream) {
+  int rc = check_common(cum, tr, db, len, TSM_SEMIRING_MAX);
+  if (rc) return rc;
+  if (!score) return fail(TSM_ERR_INVALID, "score output is required");
+  if (with_tb && (!seg_count || !segments)) return fail(TSM_ERR_INVALID, "traceback needs seg_count and segments");
+  Plan pl;
+  rc = make_plan(B, T, C, K, ps != nullptr, pe != nullptr, &pl);
+  if (rc) return rc;
+  const DeviceInfo di = device_info();
+  const size_t lds = tsm::viterbi_lds_bytes(pl.C, pl.Kmax, pl.RS, ps != nullptr);
+  if (lds > (size_t)di.max_lds)
+    return fail(TSM_ERR_UNSUPPORTED, "Viterbi ring (C=%d, K=%d) needs %zu bytes of LDS (> %d)", pl.C, pl.K, lds,
+                di.max_lds);
+  const size_t need = viterbi_ws_bytes(pl, with_tb);
+  if (!workspace || ws_bytes < need)
+    return fail(TSM_ERR_WORKSPACE, "viterbi workspace too small: %zu < %zu bytes", ws_bytes, need);
+  Carver cv(workspace);
+  tsm::ViterbiParams v{};
+  v.bp = with_tb ? cv.take<int32_t>((size_t)pl.B * (pl.T + 1) * pl.C) : nullptr;
+  v.final_c = cv.take<int32_t>(pl.B);
+  v.cum = cum;
+  v.trans = tr;
+  v.db = db;
+  v.lengths = len;
+  v.ps = ps;
+  v.pe = pe;
+  v.B = pl.B;
+  v.T = pl.T;
+  v.C = pl.C;
+  v.K = pl.K;
+  v.Kmax = pl.Kmax;
+  v.RS = pl.RS;
+  v.score = score;
+  v.seg_count = seg_count;
+  v.segs = segments;
+  const int e = tsm::launch_viterbi(pl, v, with_tb, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "tsm_viterbi");
+  return TSM_OK;
+}
+
+int tsm_ring_checkpoints(const float* alpha_hat, const double* alpha_level, const int64_t* len, int64_t B,
+                         int64_t T, int64_t C, int64_t K, int64_t S, int64_t n_ckpt, float* out, void* stream) {
+  if (!alpha_hat || !alpha_level || !len || !out) return fail(TSM_ERR_INVALID, "null pointer argument");
+  if (B < 1 || T < 1 || C < 1 || K < 1 || S < 1 || n_ckpt < 0) return fail(TSM_ERR_INVALID, "bad sizes");
+  if (n_ckpt == 0) return TSM_OK;
+  const int e = tsm::launch_checkpoints(alpha_hat, alpha_level, len, (int)B, (int)T, (int)C, (int)K, (int)S,
+                                        (int)n_ckpt, out, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "tsm_ring_checkpoints");
+  return TSM_OK;
+}
+
+}  // extern "C"

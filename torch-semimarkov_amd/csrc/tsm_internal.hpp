@@ -1,0 +1,107 @@
+// Kernel parameter blocks and host-side launchers (internal to libtsm_hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "tsm_plan.hpp"
+
+namespace tsm {
+
+enum Semiring : int { kLog = 0, kMax = 1 };
+
+// Forward / backward chunked scan over one direction of the recursion.
+struct ScanParams {
+  // problem
+  const float* cum;        // (B, T+1, C)
+  const float* trans;      // (C, C)  transition[c_src][c_dst], natural log units
+  const float* db;         // (K, C)  duration bias
+  const int64_t* lengths;  // (B,)
+  const float* ps;         // (B, T, C) proj_start or null
+  const float* pe;         // (B, T, C) proj_end or null
+  int B, T, C, K, Kmax, RS;
+  int P, Lc, W;            // chunks per sequence, chunk length, warm-up
+  float tol;               // verification tolerance, log2 units
+  // per-position output (normalised log2 values and fp64 levels), may be null
+  float* val;              // (B, T+1, C)
+  double* lvl;             // (B, T+1)
+  // chunk boundary states
+  float* st_spec;          // (B*P, Kmax, C)
+  double* lv_spec;         // (B*P, Kmax)
+  float* st_end;           // (B*P, Kmax, C)
+  double* lv_end;          // (B*P, Kmax)
+  double* offs;            // (B*P) frame offsets (log2 units)
+  int* status;             // (B*P) 0 exact, 1 speculative+verified, 2 recomputed
+  int32_t* recomputed;     // (B) number of recomputed chunks, or null
+  // forward only: final row at position len, partition
+  float* fin;              // (B, C)
+  double* fin_lvl;         // (B)
+  double* z2;              // (B) log2 partition
+  float* zout;             // (B) partition in natural log units
+  // rings in global memory when LDS is too small
+  float* gring;            // (B*P, scan_gring_floats)
+};
+
+struct MargParams {
+  const float* cum;
+  const float* trans;
+  const float* db;
+  const int64_t* lengths;
+  const float* ps;
+  const float* pe;
+  int B, T, C, K, Kmax, RS;
+  int NB, TB, CB, NCB;
+  const float* aval;       // (B, T+1, C) alpha-hat (log2)
+  const double* alvl;      // (B, T+1) alpha levels (global frame)
+  const float* bval;       // (B, T+1, C) beta-hat (log2)
+  const double* blvl;      // (B, T+1) beta levels (global frame)
+  const double* z2;        // (B) log2 partition
+  float* e_own;            // (B, T+1, C) end sums from starts inside the owning block
+  float* s_out;            // (B, T+1, C) start sums
+  float* halo;             // (B, NB, Kmax, C) end sums spilling into the next block
+  double* db_part;         // (B, NB, Kmax, C)  duration-bias gradient partials
+  double* tr_part;         // (B, NB, C, C)     transition gradient partials [c_src][c_dst]
+};
+
+struct FinalParams {
+  const int64_t* lengths;
+  int B, T, C, K, Kmax, NB, TB;
+  const float* e_own;
+  const float* s_out;
+  const float* halo;
+  const double* db_part;
+  const double* tr_part;
+  const float* grad_output;  // (B)
+  float* grad_cum;           // (B, T+1, C)
+  float* grad_ps;            // (B, T, C) or null
+  float* grad_pe;            // (B, T, C) or null
+  float* grad_tr;            // (C, C)
+  float* grad_db;            // (K, C)
+};
+
+struct ViterbiParams {
+  const float* cum;
+  const float* trans;
+  const float* db;
+  const int64_t* lengths;
+  const float* ps;
+  const float* pe;
+  int B, T, C, K, Kmax, RS;
+  float* score;        // (B) Viterbi score (max over final labels)
+  int32_t* bp;         // (B, T+1, C) packed backpointer (k << 16 | c_src), or null
+  int32_t* final_c;    // (B) first argmax label at position len
+  // backtrace output
+  int32_t* seg_count;  // (B)
+  int32_t* segs;       // (B, T, 4): start, end, label, prev label (reverse order)
+};
+
+// launchers (return hipError_t as int)
+int launch_scan_forward(const Plan& pl, const ScanParams& p, int semiring, hipStream_t s);
+int launch_scan_backward(const Plan& pl, const ScanParams& p, int semiring, hipStream_t s);
+int launch_marginals(const Plan& pl, const MargParams& q, hipStream_t s);
+int launch_finalize(const Plan& pl, const FinalParams& f, hipStream_t s);
+int launch_viterbi(const Plan& pl, const ViterbiParams& v, int with_traceback, hipStream_t s);
+int launch_checkpoints(const float* aval, const double* alvl, const int64_t* lengths, int B, int T,
+                       int C, int K, int S, int n_ckpt, float* out, hipStream_t s);
+
+}  // namespace tsm

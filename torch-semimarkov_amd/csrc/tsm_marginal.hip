@@ -1,0 +1,360 @@
+// Segment marginals and gradients (after both scans), for gfx950.
+//
+// For a segment starting at t with duration k and label c (any predecessor):
+//   P(t,k,c) = exp( u[t,c] + seg(t,k,c) + beta[t+k,c] - logZ ),
+//   u[t,c]   = LSE_{c'} alpha[t,c'] + trans[c',c]
+// and the reference's gradients (streaming/pytorch_reference.py:456-499) are
+//   d cum[t+k,c] += P, d cum[t,c] -= P, d db[min(k,K-1),c] += P,
+//   d proj_start[t,c] += P, d proj_end[t+k-1,c] += P,
+//   d trans[c',c] += exp(alpha[t,c'] + trans[c',c] - u[t,c]) * sum_k P(t,k,c).
+// (For the max semiring the same formulas with max-alpha/beta give the
+// reference's "soft max-marginals", pytorch_reference.py:458-467.)
+//
+// One workgroup handles TB consecutive start positions of one sequence; all
+// blocks are independent.  End sums E[r,c] = sum_k P(r-k,k,c) accumulate in an
+// LDS ring and are flushed row by row; rows that belong to the next block
+// ("halo", at most Kmax-1 rows) go to a side buffer that the finalize kernel
+// adds.  Nothing uses atomics: every output element has exactly one writer.
+
+#include "tsm_device.hpp"
+#include "tsm_internal.hpp"
+
+namespace tsm {
+namespace {
+
+constexpr int kTRegMax = 8;  // register accumulators per lane for the transition gradient
+
+__device__ inline int mlen(const int64_t* lengths, int b, int T) {
+  int64_t L = lengths[b];
+  if (L < 0) L = 0;
+  if (L > T) L = T;
+  return (int)L;
+}
+
+// Block (b, position block blk, label block cbk): start positions
+// [t0, t0+TB) of sequence b, destination labels [cb0, cb0+CB).
+template <int J>
+__global__ void __launch_bounds__(512) marginal_kernel(MargParams q) {
+  extern __shared__ __align__(16) char smem[];
+  const int cbk = blockIdx.x % q.NCB;
+  const int blk = (blockIdx.x / q.NCB) % q.NB;
+  const int b = blockIdx.x / (q.NCB * q.NB);
+  const int C = q.C, CB = q.CB, Kmax = q.Kmax, RS = q.RS, T = q.T, K = q.K;
+  const int cb0 = cbk * CB;
+  const int len = mlen(q.lengths, b, T);
+  const int t0 = blk * q.TB;
+  const int tid = threadIdx.x, NT = blockDim.x;
+  const int cl_raw = tid / J, lj = tid % J;
+  const bool cval = cl_raw < CB && cb0 + cl_raw < C;
+  const int cl = cval ? cl_raw : 0;       // local label
+  const int c = cb0 + cl;                 // global label
+  const int ncl = min(CB, C - cb0);       // labels in this block
+  float* e_own_b = q.e_own + (size_t)b * (T + 1) * C;
+  if (t0 >= len) {
+    // no starts here: zero this block's gradient partials (they are summed over
+    // all blocks) and the end-sum row at len when the block begins there
+    double* dbz = q.db_part + ((size_t)b * q.NB + blk) * Kmax * C;
+    double* trz = q.tr_part + ((size_t)b * q.NB + blk) * C * C;
+    for (int idx = tid; idx < Kmax * ncl; idx += NT) dbz[(size_t)(idx / ncl) * C + cb0 + idx % ncl] = 0.0;
+    for (int idx = tid; idx < C * ncl; idx += NT) trz[(size_t)(idx / ncl) * C + cb0 + idx % ncl] = 0.0;
+    if (t0 == len)
+      for (int i = tid; i < ncl; i += NT) e_own_b[(size_t)len * C + cb0 + i] = 0.0f;
+    return;
+  }
+  const int t1 = min(t0 + q.TB, len);
+  const bool has_ps = q.ps != nullptr, has_pe = q.pe != nullptr;
+
+  const MargLds L = marg_lds_layout(C, CB, Kmax, RS, has_pe);
+  double* lvb = reinterpret_cast<double*>(smem + L.lvb);
+  float* brng = reinterpret_cast<float*>(smem + L.brng);
+  float* crng = reinterpret_cast<float*>(smem + L.crng);
+  float* prng = reinterpret_cast<float*>(smem + L.prng);
+  float* erng = reinterpret_cast<float*>(smem + L.erng);
+  float* dbt = reinterpret_cast<float*>(smem + L.dbt);
+  float* dacc = reinterpret_cast<float*>(smem + L.dacc);
+  float* trt = reinterpret_cast<float*>(smem + L.trt);
+  float* row = reinterpret_cast<float*>(smem + L.row);
+  float* bk = reinterpret_cast<float*>(smem + L.bk);
+
+  const float* cum_b = q.cum + (size_t)b * (T + 1) * C;
+  const float* ps_b = has_ps ? q.ps + (size_t)b * T * C : nullptr;
+  const float* pe_b = has_pe ? q.pe + (size_t)b * T * C : nullptr;
+  const float* av_b = q.aval + (size_t)b * (T + 1) * C;
+  const double* al_b = q.alvl + (size_t)b * (T + 1);
+  const float* bv_b = q.bval + (size_t)b * (T + 1) * C;
+  const double* bl_b = q.blvl + (size_t)b * (T + 1);
+  const double z2 = q.z2[b];
+  double* dbp = q.db_part + ((size_t)b * q.NB + blk) * Kmax * C;
+  double* trp = q.tr_part + ((size_t)b * q.NB + blk) * C * C;
+
+  // ---- constants, initial rings, zeroed partials (this block's labels) ----
+  for (int idx = tid; idx < ncl * (Kmax + 1); idx += NT) {
+    const int l = idx / (Kmax + 1), k = idx % (Kmax + 1);
+    const int di = k < K - 1 ? k : K - 1;
+    dbt[idx] = (k == 0) ? 0.0f : q.db[(size_t)di * C + cb0 + l] * kLog2e;
+  }
+  for (int idx = tid; idx < ncl * C; idx += NT) {
+    const int l = idx / C, cs = idx % C;
+    trt[idx] = q.trans[(size_t)cs * C + cb0 + l] * kLog2e;  // [c_dst local][c_src]
+  }
+  for (int idx = tid; idx < CB * RS; idx += NT) erng[idx] = 0.0f;
+  for (int idx = tid; idx < CB * (Kmax + 1); idx += NT) dacc[idx] = 0.0f;
+  for (int idx = tid; idx < Kmax * ncl; idx += NT) {
+    const int i = idx / ncl, l = idx % ncl;
+    const int pos = t0 + 1 + i;  // beta / cum positions [t0+1, t0+Kmax]
+    if (pos <= len) {
+      brng[l * RS + pos % RS] = bv_b[(size_t)pos * C + cb0 + l];
+      crng[l * RS + pos % RS] = cum_b[(size_t)pos * C + cb0 + l];
+    }
+    const int ppos = t0 + i;  // proj_end positions [t0, t0+Kmax-1]
+    if (has_pe && ppos < len) prng[l * RS + ppos % RS] = pe_b[(size_t)ppos * C + cb0 + l] * kLog2e;
+    dbp[(size_t)i * C + cb0 + l] = 0.0;
+  }
+  for (int i = tid; i < Kmax; i += NT) {
+    const int pos = t0 + 1 + i;
+    if (pos <= len) lvb[pos % RS] = bl_b[pos];
+  }
+  for (int idx = tid; idx < C * ncl; idx += NT) trp[(size_t)(idx / ncl) * C + cb0 + idx % ncl] = 0.0;
+  if (cval && lj == 0) e_own_b[(size_t)t0 * C + c] = 0.0f;
+
+  float tacc[kTRegMax];
+#pragma unroll
+  for (int r = 0; r < kTRegMax; ++r) tacc[r] = 0.0f;
+  __syncthreads();
+  // fp32 partial sums are folded into the fp64 block partials every 64 steps
+  auto flush_acc = [&]() {
+    if (!cval) return;
+    float* da = dacc + cl * (Kmax + 1);
+    for (int k = 1 + lj; k <= Kmax; k += J) {
+      dbp[(size_t)(k - 1) * C + c] += (double)da[k];
+      da[k] = 0.0f;
+    }
+#pragma unroll
+    for (int r = 0; r < kTRegMax; ++r) {
+      const int cs = lj + r * J;
+      if (cs < C) trp[(size_t)cs * C + c] += (double)tacc[r];
+      tacc[r] = 0.0f;
+    }
+  };
+
+  const float* br = brng + cl * RS;
+  const float* cr = crng + cl * RS;
+  const float* pr = prng + cl * RS;
+  float* er = erng + cl * RS;
+  const float* dr = dbt + cl * (Kmax + 1);
+  const float* tr = trt + cl * C;
+  for (int t = t0; t < t1; ++t) {
+    const int buf = t & 1;
+    const int kcap = min(Kmax, len - t);
+    // ---- stage per-step shared operands (double buffered) ----
+    for (int i = tid; i < C; i += NT) row[buf * C + i] = av_b[(size_t)t * C + i];
+    const double al = al_b[t];
+    for (int k = tid + 1; k <= kcap; k += NT) {
+      int slot = t % RS + k;
+      if (slot >= RS) slot -= RS;
+      bk[buf * (Kmax + 1) + k] = (float)(al + lvb[slot] - z2);
+    }
+    // ---- stage the ring entries first needed by step t+1 (position t+1+Kmax,
+    //      proj_end position t+Kmax).  With RS >= Kmax+2 their slots are not read
+    //      by step t-1, and the barrier below publishes them before step t+1. ----
+    {
+      const int pos = t + 1 + Kmax;
+      if (pos <= len) {
+        for (int i = tid; i < ncl; i += NT) {
+          brng[i * RS + pos % RS] = bv_b[(size_t)pos * C + cb0 + i];
+          crng[i * RS + pos % RS] = cum_b[(size_t)pos * C + cb0 + i];
+        }
+        if (tid == 0) lvb[pos % RS] = bl_b[pos];
+      }
+      const int ppos = t + Kmax;
+      if (has_pe && ppos < len)
+        for (int i = tid; i < ncl; i += NT) prng[i * RS + ppos % RS] = pe_b[(size_t)ppos * C + cb0 + i] * kLog2e;
+    }
+    __syncthreads();
+    const float* rw = row + buf * C;
+    const float* bkk = bk + buf * (Kmax + 1);
+    // ---- u[t,c] = LSE_{c'} alpha-hat[t,c'] + trans[c',c] ----
+    float m = kMinusInf;
+    for (int i = lj; i < C; i += J) m = fmax2(m, rw[i] + tr[i]);
+    const float M = group_max<J>(m);
+    float sm = 0.0f;
+    for (int i = lj; i < C; i += J) sm += exp2_hw(rw[i] + tr[i] - M);
+    const float S = group_sum<J>(sm);
+    const float u2 = M + log2_hw(S);
+    const float cur_cum = cum_b[(size_t)t * C + c];
+    const float head = u2 + (has_ps ? ps_b[(size_t)t * C + c] * kLog2e : 0.0f);
+    // ---- segment marginals P(t,k,c) over durations ----
+    const int base = t % RS;
+    float sp = 0.0f;
+    float* da = dacc + cl * (Kmax + 1);
+    for (int k = 1 + lj; k <= kcap; k += J) {
+      int slot = base + k;
+      if (slot >= RS) slot -= RS;
+      float rest = dr[k] + br[slot] + bkk[k];
+      if (has_pe) rest += pr[slot == 0 ? RS - 1 : slot - 1];
+      const float P = exp2_hw(head + fmaf(cr[slot] - cur_cum, kLog2e, rest));
+      if (cval) {
+        er[slot] += P;
+        da[k] += P;
+      }
+      sp += P;
+    }
+    const float St = group_sum<J>(sp);
+    // ---- transition gradient: softmax weight of each source label times St ----
+    const float invS = 1.0f / S;
+#pragma unroll
+    for (int r = 0; r < kTRegMax; ++r) {
+      const int cs = lj + r * J;
+      if (cs < C) tacc[r] += exp2_hw(rw[cs] + tr[cs] - M) * invS * St;
+    }
+    for (int cs = lj + kTRegMax * J; cs < C; cs += J)
+      if (cval) trp[(size_t)cs * C + c] += (double)(exp2_hw(rw[cs] + tr[cs] - M) * invS * St);
+    if (cval && lj == 0) {
+      q.s_out[((size_t)b * (T + 1) + t) * C + c] = St;
+      // row t+1 is complete (all its starts t+1-k >= t0 are done)
+      const int r1 = t + 1;
+      const int s1 = r1 % RS;
+      const float v = er[s1];
+      er[s1] = 0.0f;
+      if (r1 < t0 + q.TB) e_own_b[(size_t)r1 * C + c] = v;
+      else q.halo[(((size_t)b * q.NB + blk) * Kmax + (r1 - t0 - q.TB)) * C + c] = v;
+    }
+    if (((t - t0) & 63) == 63) flush_acc();
+  }
+  flush_acc();
+  // ---- pending end rows (t1+1 .. t1-1+Kmax), same lane that accumulated them ----
+  if (cval && lj == 0) {
+    for (int r1 = t1 + 1; r1 <= t1 - 1 + Kmax && r1 <= len; ++r1) {
+      const float v = er[r1 % RS];
+      if (r1 < t0 + q.TB) e_own_b[(size_t)r1 * C + c] = v;
+      else q.halo[(((size_t)b * q.NB + blk) * Kmax + (r1 - t0 - q.TB)) * C + c] = v;
+    }
+  }
+}
+
+// grad_cum / proj grads from the end and start sums, scaled by grad_output.
+__global__ void finalize_rows_kernel(FinalParams f) {
+  const int b = blockIdx.y;
+  const int C = f.C, T = f.T;
+  const int len = mlen(f.lengths, b, T);
+  const float g = f.grad_output[b];
+  const size_t n = (size_t)(T + 1) * C;
+  for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < n; idx += (size_t)gridDim.x * blockDim.x) {
+    const int t = (int)(idx / C), c = (int)(idx % C);
+    const size_t o = ((size_t)b * (T + 1) + t) * C + c;
+    float E = 0.0f, S = 0.0f;
+    if (t <= len) {
+      const int blk = t / f.TB, t0 = blk * f.TB;
+      if (t > 0) {
+        // own part: written by block blk (absent when t == NB*TB, i.e. t == T)
+        if (blk < f.NB) E = f.e_own[o];
+        if (blk >= 1 && t - t0 < f.Kmax) E += f.halo[(((size_t)b * f.NB + blk - 1) * f.Kmax + (t - t0)) * C + c];
+      }
+      if (t < len) S = f.s_out[o];
+    }
+    f.grad_cum[o] = g * (E - S);
+    if (f.grad_ps != nullptr && t < T) f.grad_ps[((size_t)b * T + t) * C + c] = g * S;
+    if (f.grad_pe != nullptr && t >= 1) f.grad_pe[((size_t)b * T + t - 1) * C + c] = g * E;
+  }
+}
+
+// Shared gradients: sum over sequences (weighted by grad_output) and blocks, in fp64.
+__global__ void finalize_shared_kernel(FinalParams f) {
+  const int C = f.C, K = f.K, Kmax = f.Kmax;
+  const int n_tr = C * C, n_db = K * C;
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx < n_tr) {
+    double acc = 0.0;
+    for (int b = 0; b < f.B; ++b) {
+      double s = 0.0;
+      for (int i = 0; i < f.NB; ++i) s += f.tr_part[((size_t)b * f.NB + i) * C * C + idx];
+      acc += (double)f.grad_output[b] * s;
+    }
+    f.grad_tr[idx] = (float)acc;
+  } else if (idx < n_tr + n_db) {
+    const int e = idx - n_tr;
+    const int k = e / C, c = e % C;
+    // durations mapping to duration-bias row k: k itself (K >= 2, k >= 1) or 1 (K == 1)
+    const int dur = (K == 1) ? 1 : k;
+    double acc = 0.0;
+    if (dur >= 1 && dur <= Kmax) {
+      for (int b = 0; b < f.B; ++b) {
+        double s = 0.0;
+        for (int i = 0; i < f.NB; ++i) s += f.db_part[(((size_t)b * f.NB + i) * Kmax + dur - 1) * C + c];
+        acc += (double)f.grad_output[b] * s;
+      }
+    }
+    f.grad_db[e] = (float)acc;
+  }
+}
+
+// Raw (natural-log) ring checkpoints in the reference's layout, rebuilt from
+// the normalised alpha table: ring slot s at checkpoint n holds alpha at the
+// position p in (nS-K, nS] with p % K == s (streaming/pytorch_reference.py:192-258).
+__global__ void checkpoints_kernel(const float* aval, const double* alvl, const int64_t* lengths, int B, int T,
+                                   int C, int K, int S, int n_ckpt, float* out) {
+  const size_t total = (size_t)B * n_ckpt * K * C;
+  for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (size_t)gridDim.x * blockDim.x) {
+    const int c = (int)(idx % C);
+    const int s = (int)((idx / C) % K);
+    const int n = (int)((idx / ((size_t)C * K)) % n_ckpt);
+    const int b = (int)(idx / ((size_t)C * K * n_ckpt));
+    const int len = mlen(lengths, b, T);
+    const int tn = n * S;
+    float v = kNegInf;
+    if (tn <= len || n == 0) {
+      const int pos = tn - ((tn - s) % K + K) % K;
+      if (pos >= 0 && pos <= len) {
+        const size_t o = (size_t)b * (T + 1) + pos;
+        v = (float)(((double)aval[o * C + c] + alvl[o]) * kLn2);
+      }
+    }
+    out[idx] = v;
+  }
+}
+
+template <int J>
+int launch_marg_j(const Plan& pl, const MargParams& q, hipStream_t st) {
+  auto k = marginal_kernel<J>;
+  hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)pl.marg_lds);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(k, dim3(pl.B * pl.NB * pl.NCB), dim3(pl.NTM), pl.marg_lds, st, q);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+int launch_marginals(const Plan& pl, const MargParams& q, hipStream_t s) {
+  switch (pl.JM) {
+    case 1: return launch_marg_j<1>(pl, q, s);
+    case 2: return launch_marg_j<2>(pl, q, s);
+    case 4: return launch_marg_j<4>(pl, q, s);
+    case 8: return launch_marg_j<8>(pl, q, s);
+    case 16: return launch_marg_j<16>(pl, q, s);
+    case 32: return launch_marg_j<32>(pl, q, s);
+    case 64: return launch_marg_j<64>(pl, q, s);
+    default: return (int)hipErrorInvalidValue;
+  }
+}
+
+int launch_finalize(const Plan& pl, const FinalParams& f, hipStream_t s) {
+  int gx = (int)(((size_t)(pl.T + 1) * pl.C + 255) / 256);
+  if (gx > 4096) gx = 4096;
+  hipLaunchKernelGGL(finalize_rows_kernel, dim3(gx, pl.B), dim3(256), 0, s, f);
+  const int n = pl.C * pl.C + pl.K * pl.C;
+  hipLaunchKernelGGL(finalize_shared_kernel, dim3((n + 255) / 256), dim3(256), 0, s, f);
+  return hipGetLastError();
+}
+
+int launch_checkpoints(const float* aval, const double* alvl, const int64_t* lengths, int B, int T, int C, int K,
+                       int S, int n_ckpt, float* out, hipStream_t s) {
+  const size_t total = (size_t)B * n_ckpt * K * C;
+  int g = (int)((total + 255) / 256);
+  if (g > 8192) g = 8192;
+  if (g < 1) g = 1;
+  hipLaunchKernelGGL(checkpoints_kernel, dim3(g), dim3(256), 0, s, aval, alvl, lengths, B, T, C, K, S, n_ckpt, out);
+  return hipGetLastError();
+}
+
+}  // namespace tsm

@@ -1,0 +1,230 @@
+// Exact Viterbi (max semiring) with backpointers and on-device backtrace.
+//
+// This kernel reproduces the reference's fp32 arithmetic operation for
+// operation, so scores are bit-identical and segmentations match exactly:
+//   edge  = (((cum[t,c]-cum[s,c]) + db[min(k,K-1),c]) (+ps[s,c]) (+pe[t-1,c])) + trans[c',c]
+//   score = alpha[s,c'] + edge                       (streaming/pytorch_reference.py:86-111, 229)
+//   alpha[t,c] = max_k max_c' score                  (:240-241)
+// Ties follow nn.py:472-501: the smallest duration wins (strict '>' over k in
+// ascending order), then the first source label (torch.max), and the
+// backtrace starts from the first maximising final label (argmax).
+// Raw (un-normalised) fp32 alpha values are kept, exactly as the reference.
+//
+// One workgroup per sequence; the K x C alpha ring lives in LDS.  Lanes of a
+// label group split the durations; the transition row of the label sits in
+// registers when it is short enough (CMAX > 0).
+
+#include "tsm_device.hpp"
+#include "tsm_internal.hpp"
+
+namespace tsm {
+namespace {
+
+struct VLds {
+  size_t araw, crng, prng, dbn, trn, red, total;
+};
+
+__host__ __device__ inline VLds vit_lds_layout(int C, int Kmax, int RS, int has_ps) {
+  VLds L;
+  size_t o = 0;
+  const size_t ring = sizeof(float) * (size_t)C * RS;
+  L.araw = o; o = align16(o + ring);
+  L.crng = o; o = align16(o + ring);
+  L.prng = o; o = align16(o + (has_ps ? ring : 0));
+  L.dbn = o; o = align16(o + sizeof(float) * (size_t)C * (Kmax + 1));
+  L.trn = o; o = align16(o + sizeof(float) * (size_t)C * C);
+  L.red = o; o = align16(o + sizeof(float) * 64 + sizeof(int) * 64);
+  L.total = o;
+  return L;
+}
+
+template <int J, int CMAX>
+__global__ void __launch_bounds__(512) viterbi_kernel(ViterbiParams v) {
+  extern __shared__ __align__(16) char smem[];
+  const int b = blockIdx.x;
+  const int C = v.C, K = v.K, Kmax = v.Kmax, RS = v.RS, T = v.T;
+  int64_t L64 = v.lengths[b];
+  const int len = (int)(L64 < 0 ? 0 : (L64 > T ? T : L64));
+  const bool has_ps = v.ps != nullptr, has_pe = v.pe != nullptr;
+  const VLds Ly = vit_lds_layout(C, Kmax, RS, has_ps);
+  float* araw = reinterpret_cast<float*>(smem + Ly.araw);
+  float* crng = reinterpret_cast<float*>(smem + Ly.crng);
+  float* prng = reinterpret_cast<float*>(smem + Ly.prng);
+  float* dbn = reinterpret_cast<float*>(smem + Ly.dbn);
+  float* trn = reinterpret_cast<float*>(smem + Ly.trn);
+  float* redv = reinterpret_cast<float*>(smem + Ly.red);
+  int* redi = reinterpret_cast<int*>(smem + Ly.red + sizeof(float) * 64);
+
+  const int tid = threadIdx.x, NT = blockDim.x;
+  const int c_raw = tid / J, lj = tid % J;
+  const bool cval = c_raw < C;
+  const int c = cval ? c_raw : C - 1;
+  const float* cum_b = v.cum + (size_t)b * (T + 1) * C;
+  const float* ps_b = has_ps ? v.ps + (size_t)b * T * C : nullptr;
+  const float* pe_b = has_pe ? v.pe + (size_t)b * T * C : nullptr;
+
+  for (int idx = tid; idx < C * (Kmax + 1); idx += NT) {
+    const int cc = idx / (Kmax + 1), k = idx % (Kmax + 1);
+    const int di = k < K - 1 ? k : K - 1;
+    dbn[idx] = v.db[(size_t)di * C + cc];
+  }
+  for (int idx = tid; idx < C * C; idx += NT) {
+    const int cd = idx / C, cs = idx % C;
+    trn[idx] = v.trans[(size_t)cs * C + cd];  // [c_dst][c_src]
+  }
+  for (int cc = tid; cc < C; cc += NT) {
+    araw[cc * RS] = 0.0f;  // alpha[0, :] = 0
+    crng[cc * RS] = cum_b[cc];
+    if (has_ps && T > 0) prng[cc * RS] = ps_b[cc];
+  }
+  __syncthreads();
+  float tr_reg[CMAX > 0 ? CMAX : 1];
+  if constexpr (CMAX > 0) {
+#pragma unroll
+    for (int i = 0; i < CMAX; ++i) tr_reg[i] = (i < C) ? trn[c * C + i] : 0.0f;
+  }
+  const float* dr = dbn + c * (Kmax + 1);
+  const float* cr = crng + c * RS;
+  const float* pr = prng + c * RS;
+
+  for (int t = 1; t <= len; ++t) {
+    const int kcap = (K == 1) ? 1 : min(K - 1, t);
+    const int base = t % RS;
+    const float cur_cum = cum_b[(size_t)t * C + c];
+    const float pe_t = has_pe ? pe_b[(size_t)(t - 1) * C + c] : 0.0f;
+    float bv = kMinusInf;
+    int bk = 0;
+    for (int k = 1 + lj; k <= kcap; k += J) {
+      const int slot = wrap_slot(base - k, RS);
+      float e1 = (cur_cum - cr[slot]) + dr[k];
+      if (has_ps) e1 = e1 + pr[slot];
+      if (has_pe) e1 = e1 + pe_t;
+      float m = kMinusInf;
+      if constexpr (CMAX > 0) {
+#pragma unroll
+        for (int i = 0; i < CMAX; ++i)
+          if (i < C) m = fmax2(m, araw[i * RS + slot] + (e1 + tr_reg[i]));
+      } else {
+        const float* trow = trn + c * C;
+        for (int i = 0; i < C; ++i) m = fmax2(m, araw[i * RS + slot] + (e1 + trow[i]));
+      }
+      if (m > bv) {
+        bv = m;
+        bk = k;
+      }
+    }
+    ValIdx best = group_argmax_first<J>(ValIdx{bv, bk == 0 ? 0x7fffffff : bk});
+    if (v.bp != nullptr) {
+      // first source label attaining the max at the winning duration
+      const int ks = best.i;
+      const int slot = wrap_slot(base - ks, RS);
+      float e1 = (cur_cum - cr[slot]) + dr[ks];
+      if (has_ps) e1 = e1 + pr[slot];
+      if (has_pe) e1 = e1 + pe_t;
+      float cv = kMinusInf;
+      int ci = 0x7fffffff;
+      for (int i = lj; i < C; i += J) {
+        const float x = araw[i * RS + slot] + (e1 + trn[c * C + i]);
+        if (x > cv) {
+          cv = x;
+          ci = i;
+        }
+      }
+      const ValIdx cs = group_argmax_first<J>(ValIdx{cv, ci});
+      if (cval && lj == 0) v.bp[((size_t)b * (T + 1) + t) * C + c] = (ks << 16) | cs.i;
+    }
+    // slot t % RS holds position t - RS, which step t never reads (RS >= Kmax+1),
+    // so the ring can be updated without waiting for the other labels' reads.
+    if (cval && lj == 0) {
+      araw[c * RS + base] = best.v;
+      crng[c * RS + base] = cur_cum;
+      if (has_ps && t < T) prng[c * RS + base] = ps_b[(size_t)t * C + c];
+    }
+    __syncthreads();
+  }
+  // ---- score = max over labels of alpha[len]; first maximising label ----
+  {
+    const int slot = len % RS;
+    float mv = kMinusInf;
+    int mi = 0x7fffffff;
+    for (int cc = tid; cc < C; cc += NT) {
+      const float x = araw[cc * RS + slot];
+      if (x > mv || (x == mv && cc < mi)) {
+        mv = x;
+        mi = cc;
+      }
+    }
+    ValIdx r = group_argmax_first<64>(ValIdx{mv, mi});
+    if ((tid & 63) == 0) {
+      redv[tid >> 6] = r.v;
+      redi[tid >> 6] = r.i;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      ValIdx a{redv[0], redi[0]};
+      for (int w = 1; w < (NT + 63) / 64; ++w)
+        if (redv[w] > a.v || (redv[w] == a.v && redi[w] < a.i)) a = ValIdx{redv[w], redi[w]};
+      if (len == 0) {
+        v.score[b] = kNegInf;  // reference: the final alpha is never written
+        v.final_c[b] = 0;
+      } else {
+        v.score[b] = a.v;
+        v.final_c[b] = a.i;
+      }
+    }
+  }
+}
+
+// One thread per sequence walks the backpointers from (len, final label).
+__global__ void backtrace_kernel(ViterbiParams v) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= v.B) return;
+  const int C = v.C, T = v.T;
+  int64_t L64 = v.lengths[b];
+  const int len = (int)(L64 < 0 ? 0 : (L64 > T ? T : L64));
+  int t = len, c = v.final_c[b], n = 0;
+  int32_t* out = v.segs + (size_t)b * T * 4;
+  while (t > 0 && n < T) {
+    const int32_t w = v.bp[((size_t)b * (T + 1) + t) * C + c];
+    const int k = w >> 16, cp = w & 0xffff;
+    if (k <= 0 || k > t) break;
+    out[4 * n + 0] = t - k;
+    out[4 * n + 1] = t - 1;
+    out[4 * n + 2] = c;
+    out[4 * n + 3] = cp;
+    ++n;
+    t -= k;
+    c = cp;
+  }
+  v.seg_count[b] = n;
+}
+
+template <int J, int CMAX>
+int launch_vit_j(const Plan& pl, const ViterbiParams& v, int with_tb, hipStream_t st) {
+  const VLds L = vit_lds_layout(pl.C, pl.Kmax, pl.RS, v.ps != nullptr);
+  auto k = viterbi_kernel<J, CMAX>;
+  hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)L.total);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(k, dim3(pl.B), dim3(pl.NT), L.total, st, v);
+  if (with_tb) hipLaunchKernelGGL(backtrace_kernel, dim3((pl.B + 63) / 64), dim3(64), 0, st, v);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+size_t viterbi_lds_bytes(int C, int Kmax, int RS, int has_ps) { return vit_lds_layout(C, Kmax, RS, has_ps).total; }
+
+int launch_viterbi(const Plan& pl, const ViterbiParams& v, int with_traceback, hipStream_t s) {
+  switch (pl.J) {
+    case 1: return launch_vit_j<1, 0>(pl, v, with_traceback, s);
+    case 2: return launch_vit_j<2, 0>(pl, v, with_traceback, s);
+    case 4: return launch_vit_j<4, 0>(pl, v, with_traceback, s);
+    case 8: return launch_vit_j<8, 64>(pl, v, with_traceback, s);
+    case 16: return launch_vit_j<16, 32>(pl, v, with_traceback, s);
+    case 32: return launch_vit_j<32, 16>(pl, v, with_traceback, s);
+    case 64: return launch_vit_j<64, 8>(pl, v, with_traceback, s);
+    default: return (int)hipErrorInvalidValue;
+  }
+}
+
+}  // namespace tsm

@@ -1,0 +1,38 @@
+"""torch_semimarkov_amd -- the streaming semi-Markov CRF scan of torch-semimarkov,
+built for AMD Instinct MI355X (gfx950) with hand-written HIP kernels.
+
+Public API (same names and meanings as the reference package for this path):
+
+* :func:`semi_crf_streaming_forward` -- log partition / Viterbi score with autograd
+* :class:`SemiMarkovCRFHead` -- ``forward`` / ``compute_loss`` / ``decode`` /
+  ``decode_with_traceback``
+* :class:`Segment`, :class:`ViterbiResult`, :func:`score_gold_vectorized`
+* :func:`compute_edge_block_streaming`, :class:`SemiCRFStreamingHIP`
+"""
+
+from .duration import DurationDistribution, LearnedDuration
+from .helpers import Segment, ViterbiResult, score_gold_vectorized
+from .nn import SemiMarkovCRFHead
+from .streaming import (
+    HAS_HIP,
+    NEG_INF,
+    SemiCRFStreamingHIP,
+    compute_edge_block_streaming,
+    semi_crf_streaming_forward,
+)
+
+__version__ = "0.1.0"
+
+__all__ = [
+    "semi_crf_streaming_forward",
+    "SemiCRFStreamingHIP",
+    "compute_edge_block_streaming",
+    "SemiMarkovCRFHead",
+    "Segment",
+    "ViterbiResult",
+    "score_gold_vectorized",
+    "DurationDistribution",
+    "LearnedDuration",
+    "NEG_INF",
+    "HAS_HIP",
+]

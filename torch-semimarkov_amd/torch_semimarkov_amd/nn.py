@@ -1,0 +1,171 @@
+"""CRF head module on the HIP streaming scan.
+
+:class:`SemiMarkovCRFHead` has the constructor, parameters, initialisation
+order and methods of the reference's ``SemiMarkovCRFHead`` (``nn.py:55-565``):
+``forward`` / ``compute_loss`` / ``decode`` / ``decode_with_traceback``.  The
+scan always runs on the GPU through :func:`semi_crf_streaming_forward`;
+``decode_with_traceback`` uses the exact Viterbi kernel with an on-device
+backtrace instead of the reference's per-sequence Python loop.
+"""
+
+from __future__ import annotations
+
+from typing import Optional, Union
+
+import numpy as np
+import torch
+import torch.nn as nn
+from torch import Tensor
+
+from .duration import DurationDistribution, LearnedDuration
+from .helpers import Segment, ViterbiResult, score_gold_vectorized
+from .streaming import ops
+from .streaming.autograd import prepare_inputs, semi_crf_streaming_forward
+
+
+class SemiMarkovCRFHead(nn.Module):
+    r"""Semi-Markov CRF head: projection -> fp32 cumulative scores -> streaming scan.
+
+    Args:
+        num_classes (int): number of labels C.
+        max_duration (int): K; segments have durations 1..K-1 (K=1: unit segments).
+        hidden_dim (int, optional): adds ``nn.Linear(hidden_dim, C)`` when given.
+        init_scale (float): std of the ``transition`` / duration-bias initialisation.
+        duration_distribution: ``None`` / ``"learned"`` (default) or an ``nn.Module``
+            whose ``forward()`` returns a ``(K, C)`` tensor.  The reference's other
+            named distributions are not provided by this package.
+
+    Parameters are created in the reference's order (``nn.py:146-162``):
+    ``transition = randn(C, C) * init_scale``, then ``LearnedDuration``
+    (``randn(K, C) * init_scale``), then the projection, so seeded runs draw the
+    same values.
+    """
+
+    def __init__(
+        self,
+        num_classes: int,
+        max_duration: int,
+        hidden_dim: Optional[int] = None,
+        init_scale: float = 0.1,
+        duration_distribution: Optional[Union[str, DurationDistribution, nn.Module]] = None,
+    ):
+        super().__init__()
+        self.num_classes = num_classes
+        self.max_duration = max_duration
+        self.transition = nn.Parameter(torch.randn(num_classes, num_classes) * init_scale)
+        if duration_distribution is None or duration_distribution == "learned":
+            self.duration_dist = LearnedDuration(max_duration, num_classes, init_std=init_scale)
+        elif isinstance(duration_distribution, nn.Module):
+            self.duration_dist = duration_distribution
+        else:
+            raise NotImplementedError(
+                f"duration_distribution={duration_distribution!r}: only 'learned' or an nn.Module "
+                "producing a (K, C) tensor are supported"
+            )
+        self.projection = nn.Linear(hidden_dim, num_classes) if hidden_dim is not None else None
+
+    @property
+    def duration_bias(self) -> Tensor:
+        """The ``(K, C)`` duration bias (``self.duration_dist()``)."""
+        return self.duration_dist()
+
+    # ------------------------------------------------------------------ helpers
+    def _cum_scores(self, hidden_states: Tensor) -> Tensor:
+        """``(B, T+1, C)`` fp32 prefix sums of the projected scores, row 0 = 0 (``nn.py:196-209``)."""
+        B, T, _ = hidden_states.shape
+        scores = self.projection(hidden_states) if self.projection is not None else hidden_states
+        cum = torch.zeros(B, T + 1, self.num_classes, dtype=torch.float32, device=scores.device)
+        cum[:, 1:] = torch.cumsum(scores.float(), dim=1)
+        return cum
+
+    # ------------------------------------------------------------------ API
+    def forward(self, hidden_states: Tensor, lengths: Tensor, use_triton: bool = True) -> dict:
+        """``{"partition": (B,), "cum_scores": (B, T+1, C)}`` (``nn.py:173-222``)."""
+        cum = self._cum_scores(hidden_states)
+        partition = semi_crf_streaming_forward(
+            cum, self.transition, self.duration_bias, lengths, self.max_duration,
+            semiring="log", use_triton=use_triton,
+        )
+        return {"partition": partition, "cum_scores": cum}
+
+    def compute_loss(
+        self, hidden_states: Tensor, lengths: Tensor, labels: Tensor, use_triton: bool = True,
+        reduction: str = "mean",
+    ) -> Tensor:
+        """Negative log-likelihood ``log Z - score(gold)`` (``nn.py:224-271``)."""
+        res = self.forward(hidden_states, lengths, use_triton)
+        nll = res["partition"] - self._score_gold(res["cum_scores"], labels, lengths)
+        if reduction == "mean":
+            return nll.mean()
+        if reduction == "sum":
+            return nll.sum()
+        return nll
+
+    def _score_gold(self, cum_scores: Tensor, labels: Tensor, lengths: Tensor) -> Tensor:
+        return score_gold_vectorized(
+            cum_scores=cum_scores, labels=labels, lengths=lengths, transition=self.transition,
+            duration_bias=self.duration_bias, max_duration=self.max_duration,
+        )
+
+    def decode(self, hidden_states: Tensor, lengths: Tensor, use_triton: bool = True) -> Tensor:
+        """Viterbi score ``(B,)`` (``nn.py:306-358``)."""
+        cum = self._cum_scores(hidden_states)
+        return semi_crf_streaming_forward(
+            cum, self.transition, self.duration_bias, lengths, self.max_duration,
+            semiring="max", use_triton=use_triton,
+        )
+
+    def decode_with_traceback(
+        self, hidden_states: Tensor, lengths: Tensor, max_traceback_length: int = 10000
+    ) -> ViterbiResult:
+        """Best segmentation with its segments (``nn.py:360-442``).
+
+        Sequences longer than ``max_traceback_length`` (or empty) get ``[]``; their
+        scores are still computed.  Segment scores are ``content + duration bias +
+        transition`` in Python-float arithmetic on the fp32 terms, as ``nn.py:533-555``
+        computes them (the transition of the first segment comes from the best
+        virtual start label).
+        """
+        with torch.no_grad():
+            cum = self._cum_scores(hidden_states)
+            tr = self.transition.detach()
+            db = self.duration_bias.detach()
+            cum_p, tr_p, db_p, len_p, _, _ = prepare_inputs(cum, tr, db, lengths, self.max_duration)
+            score, cnt, segs = ops.viterbi(cum_p, tr_p, db_p, len_p, self.max_duration, None, None, True)
+            B = cum.shape[0]
+            lens = len_p.cpu().tolist()
+            counts = cnt.cpu().tolist()
+            want = [b for b in range(B) if 0 < lens[b] <= max_traceback_length and counts[b] > 0]
+            all_segments: list[list[Segment]] = [[] for _ in range(B)]
+            if want:
+                nmax = max(counts[b] for b in want)
+                rows = segs[:, :nmax].long()  # (B, nmax, 4), last segment first
+                # rows at or beyond a sequence's count are unwritten: zero them before gathering
+                live = torch.arange(nmax, device=cum.device).view(1, nmax) < cnt.to(cum.device).view(B, 1)
+                rows = torch.where(live.unsqueeze(-1), rows, torch.zeros_like(rows))
+                bidx = torch.arange(B, device=cum.device).view(B, 1).expand(B, nmax)
+                start, end, lab, prev = rows[..., 0], rows[..., 1], rows[..., 2], rows[..., 3]
+                # fp32 content exactly as (cum[end+1, l] - cum[start, l])
+                content = cum[bidx, (end + 1).clamp(max=cum.shape[1] - 1), lab] - cum[bidx, start, lab]
+                K = self.max_duration
+                dur_idx = torch.clamp(end - start + 1, max=K - 1)
+                dscore = db[dur_idx, lab]
+                tscore = tr[prev, lab]
+                host = torch.stack([content, dscore, tscore], dim=-1).cpu().numpy().astype(np.float64)
+                rows_h = rows.cpu().numpy()
+                for b in want:
+                    n = counts[b]
+                    out = []
+                    for i in range(n - 1, -1, -1):
+                        c_, d_, t_ = host[b, i]
+                        out.append(Segment(start=int(rows_h[b, i, 0]), end=int(rows_h[b, i, 1]),
+                                           label=int(rows_h[b, i, 2]), score=float((c_ + d_) + t_)))
+                    all_segments[b] = out
+        return ViterbiResult(scores=score, segments=all_segments)
+
+    def extra_repr(self) -> str:
+        parts = [f"num_classes={self.num_classes}", f"max_duration={self.max_duration}"]
+        if self.projection is not None:
+            parts.append(f"hidden_dim={self.projection.in_features}")
+        parts.append(f"duration_dist={self.duration_dist.__class__.__name__}")
+        return ", ".join(parts)

@@ -1,0 +1,254 @@
+"""Autograd function and public entry point of the streaming semi-CRF on MI355X.
+
+Mirrors the reference's operator API (``streaming/autograd.py:270-431``):
+``semi_crf_streaming_forward(cum_scores, transition, duration_bias, lengths, K,
+semiring="log", proj_start=None, proj_end=None, use_triton=True,
+use_compile=False) -> Tensor[B]``, with the same argument meanings and the same
+``ValueError`` for an unknown semiring.  Every path runs the HIP kernels of
+``libtsm_hip.so``; there is no CPU path.  Tensors must live on an AMD GPU.
+
+Differences from the reference, all deliberate:
+
+* ``use_triton`` / ``use_compile`` are accepted for signature compatibility and
+  ignored: the HIP backend is the only backend.
+* Inference with ``semiring="max"`` runs the exact Viterbi kernel, which is
+  bit-identical to the reference's fp32 max recursion.  With gradients the max
+  semiring uses the factorised scan (soft max-marginals in the backward, as the
+  reference's CPU backward computes them, ``pytorch_reference.py:458-467``).
+* Inputs are validated up front (shapes, devices, ``0 <= lengths <= T`` when
+  ``lengths`` is on the host); the reference validates only the semiring.
+* Duration-dependent ``(K, C, C)`` transitions raise ``NotImplementedError``.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+
+from .. import _native as N
+from . import ops
+from .constants import NEG_INF
+
+SEMIRINGS = {"log": N.TSM_SEMIRING_LOG, "max": N.TSM_SEMIRING_MAX}
+
+
+def _compute_checkpoint_interval(T: int, K: int) -> int:
+    """``S = max(K, floor(sqrt(T*K)))`` (reference ``pytorch_reference.py:25-45``)."""
+    return max(K, int(math.sqrt(T * K)))
+
+
+def _as_f32(x: torch.Tensor) -> torch.Tensor:
+    return x if x.dtype == torch.float32 else x.float()
+
+
+def prepare_inputs(cum_scores, transition, duration_bias, lengths, K, proj_start=None, proj_end=None):
+    """Validate and normalise the operator inputs.
+
+    Returns ``(cum, transition, duration_bias_eff, lengths, proj_start, proj_end)`` as
+    contiguous fp32 tensors (int64 lengths) on the device of ``cum_scores``.  The
+    duration table is re-indexed to ``K`` rows when ``duration_bias.shape[0] != K``
+    so that row ``min(k, K-1)`` holds the reference's row ``min(k, duration_bias.shape[0]-1)``
+    (``pytorch_reference.py:90-92``); the re-indexing is an autograd-tracked gather.
+    """
+    if not isinstance(cum_scores, torch.Tensor) or cum_scores.dim() != 3:
+        raise ValueError("cum_scores must be a (batch, T+1, C) tensor")
+    if not cum_scores.is_cuda:
+        raise RuntimeError(
+            "torch_semimarkov_amd runs on AMD GPUs only: cum_scores is on "
+            f"{cum_scores.device}; move the inputs to a ROCm device (e.g. .to('cuda'))"
+        )
+    dev = cum_scores.device
+    B, Tp1, C = cum_scores.shape
+    T = Tp1 - 1
+    if T < 1:
+        raise ValueError("cum_scores must have at least 2 rows along dim 1 (T >= 1)")
+    K = int(K)
+    if K < 1:
+        raise ValueError(f"K (max_duration) must be >= 1, got {K}")
+    if transition.dim() == 3:
+        raise NotImplementedError(
+            "duration-dependent (K, C, C) transitions are not supported by the HIP backend yet"
+        )
+    if transition.shape != (C, C):
+        raise ValueError(f"transition must be ({C}, {C}), got {tuple(transition.shape)}")
+    if duration_bias.dim() != 2 or duration_bias.shape[1] != C or duration_bias.shape[0] < 1:
+        raise ValueError(f"duration_bias must be (K, {C}), got {tuple(duration_bias.shape)}")
+    for name, t in (("transition", transition), ("duration_bias", duration_bias)):
+        if t.device != dev:
+            raise ValueError(f"{name} is on {t.device}, cum_scores on {dev}")
+    for name, t in (("proj_start", proj_start), ("proj_end", proj_end)):
+        if t is not None:
+            if t.shape != (B, T, C):
+                raise ValueError(f"{name} must be ({B}, {T}, {C}), got {tuple(t.shape)}")
+            if t.device != dev:
+                raise ValueError(f"{name} is on {t.device}, cum_scores on {dev}")
+    if lengths.dim() != 1 or lengths.shape[0] != B:
+        raise ValueError(f"lengths must be ({B},), got {tuple(lengths.shape)}")
+    if lengths.is_floating_point():
+        raise ValueError("lengths must be an integer tensor")
+    if not lengths.is_cuda:
+        lo, hi = int(lengths.min()), int(lengths.max())
+        if lo < 0 or hi > T:
+            raise ValueError(f"lengths must lie in [0, {T}], got [{lo}, {hi}]")
+    lengths = lengths.to(device=dev, dtype=torch.int64, non_blocking=True).contiguous()
+
+    Kdb = duration_bias.shape[0]
+    db = _as_f32(duration_bias)
+    if Kdb != K:
+        if K == 1:
+            idx = torch.tensor([min(1, Kdb - 1)], device=dev)
+        else:
+            idx = torch.clamp(torch.arange(K, device=dev), max=Kdb - 1)
+        db = db.index_select(0, idx)
+    return (
+        _as_f32(cum_scores).contiguous(),
+        _as_f32(transition).contiguous(),
+        db.contiguous(),
+        lengths,
+        _as_f32(proj_start).contiguous() if proj_start is not None else None,
+        _as_f32(proj_end).contiguous() if proj_end is not None else None,
+    )
+
+
+class SemiCRFStreamingHIP(torch.autograd.Function):
+    r"""HIP forward + backward of the streaming semi-CRF.
+
+    Contract of the reference's ``SemiCRFStreamingTriton`` (``streaming/autograd.py:164-267``):
+    ``apply(cum_scores, transition, duration_bias, lengths, K, semiring, proj_start, proj_end)``
+    returns the partition ``(B,)``; the backward returns gradients for
+    ``cum_scores`` (scaled per sequence by ``grad_output``), ``transition`` and
+    ``duration_bias`` (summed over sequences weighted by ``grad_output``) and the
+    projections, and ``None`` for ``lengths``, ``K`` and ``semiring``.
+
+    Saved for the backward: the normalised alpha table ``(B, T+1, C)`` fp32 plus
+    per-position fp64 levels (O(T*C) memory) instead of the reference's
+    ``sqrt(T*K)`` ring checkpoints; it keeps the fp32 payload O(1) at any length
+    and lets every backward pass run position-parallel.
+    """
+
+    @staticmethod
+    def forward(ctx, cum_scores, transition, duration_bias, lengths, K, semiring="log",
+                proj_start=None, proj_end=None):
+        sr = SEMIRINGS[semiring]
+        part, z2, ah, al, _ = ops.scan_forward(
+            cum_scores.detach(), transition.detach(), duration_bias.detach(), lengths, int(K), sr,
+            proj_start.detach() if proj_start is not None else None,
+            proj_end.detach() if proj_end is not None else None, True,
+        )
+        ctx.save_for_backward(cum_scores, transition, duration_bias, lengths, proj_start, proj_end, ah, al, z2)
+        ctx.K = int(K)
+        ctx.semiring = sr
+        return part
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        cum, tr, db, lengths, ps, pe, ah, al, z2 = ctx.saved_tensors
+        g = grad_output.detach().to(torch.float32).contiguous()
+        g_cum, g_tr, g_db, g_ps, g_pe, _ = ops.scan_backward(
+            cum.detach(), tr.detach(), db.detach(), lengths, ctx.K, ctx.semiring,
+            ps.detach() if ps is not None else None, pe.detach() if pe is not None else None,
+            ah, al, z2, g,
+        )
+        return (
+            g_cum, g_tr, g_db, None, None, None,
+            g_ps if ps is not None else None,
+            g_pe if pe is not None else None,
+        )
+
+
+def semi_crf_streaming_forward(
+    cum_scores: torch.Tensor,
+    transition: torch.Tensor,
+    duration_bias: torch.Tensor,
+    lengths: torch.Tensor,
+    K: int,
+    semiring: str = "log",
+    proj_start: Optional[torch.Tensor] = None,
+    proj_end: Optional[torch.Tensor] = None,
+    use_triton: bool = True,
+    use_compile: bool = False,
+) -> torch.Tensor:
+    r"""Semi-CRF log partition (``semiring="log"``) or Viterbi score (``"max"``), shape ``(B,)``.
+
+    Drop-in for the reference's ``semi_crf_streaming_forward``
+    (``streaming/autograd.py:270-431``); see the module docstring for the
+    differences.  Edges are built on the fly from ``cum_scores`` with the
+    destination-first convention ``edge[c_dst, c_src] = seg[c_dst] + transition[c_src, c_dst]``.
+    """
+    if semiring not in SEMIRINGS:
+        raise ValueError(f"semiring must be 'log' or 'max', got {semiring!r}")
+    out_dtype = cum_scores.dtype if cum_scores.is_floating_point() else torch.float32
+    cum, tr, db, lengths, ps, pe = prepare_inputs(
+        cum_scores, transition, duration_bias, lengths, K, proj_start, proj_end
+    )
+    needs_grad = torch.is_grad_enabled() and any(
+        t is not None and t.requires_grad for t in (cum, tr, db, ps, pe)
+    )
+    if needs_grad:
+        out = SemiCRFStreamingHIP.apply(cum, tr, db, lengths, int(K), semiring, ps, pe)
+    elif semiring == "log":
+        out = ops.scan_forward(cum, tr, db, lengths, int(K), SEMIRINGS["log"], ps, pe, False)[0]
+    else:
+        out = ops.viterbi(cum, tr, db, lengths, int(K), ps, pe, False)[0]
+    return out if out.dtype == out_dtype else out.to(out_dtype)
+
+
+def launch_streaming_hip_kernel(
+    cum_scores, transition, duration_bias, lengths, K, semiring="log", checkpoint_interval=None,
+    proj_start=None, proj_end=None,
+):
+    """Launcher with the reference's forward-launcher contract.
+
+    Returns ``(partition (B,), ring_checkpoints (B, ceil(T/S), K, C), S)`` like
+    ``semi_crf_streaming_forward_pytorch`` (``pytorch_reference.py:116-273``) and
+    ``launch_streaming_triton_kernel`` (``triton_forward.py:554-714``, which pads
+    one extra checkpoint).  Checkpoints hold raw alpha (natural log units) with
+    ``NEG_INF`` in slots before position 0 or after a sequence's end.
+    """
+    if semiring not in SEMIRINGS:
+        raise ValueError(f"semiring must be 'log' or 'max', got {semiring!r}")
+    cum, tr, db, lengths, ps, pe = prepare_inputs(
+        cum_scores, transition, duration_bias, lengths, K, proj_start, proj_end
+    )
+    T = cum.shape[1] - 1
+    S = _compute_checkpoint_interval(T, K) if checkpoint_interval is None else max(int(checkpoint_interval), K)
+    n_ckpt = (T + S - 1) // S
+    part, _, ah, al, _ = ops.scan_forward(cum, tr, db, lengths, int(K), SEMIRINGS[semiring], ps, pe, True)
+    ck = ops.ring_checkpoints(ah, al, lengths, int(K), S, n_ckpt)
+    return part, ck, S
+
+
+def launch_streaming_hip_backward(
+    cum_scores, transition, duration_bias, lengths, log_Z, ring_checkpoints, checkpoint_interval,
+    grad_output, proj_start=None, proj_end=None, semiring="log",
+):
+    """Launcher with the reference's backward-launcher contract
+    (``triton_backward.py:556-790``): gradients already weighted by ``grad_output``.
+
+    The normalised alpha table is recomputed from the inputs (the same values the
+    checkpoints were built from), so ``log_Z``/``ring_checkpoints`` are accepted
+    for signature compatibility only.
+    """
+    del log_Z, ring_checkpoints, checkpoint_interval
+    K = duration_bias.shape[0]
+    cum, tr, db, lengths, ps, pe = prepare_inputs(
+        cum_scores, transition, duration_bias, lengths, K, proj_start, proj_end
+    )
+    sr = SEMIRINGS[semiring]
+    _, z2, ah, al, _ = ops.scan_forward(cum, tr, db, lengths, int(K), sr, ps, pe, True)
+    g = grad_output.detach().to(device=cum.device, dtype=torch.float32).contiguous()
+    g_cum, g_tr, g_db, g_ps, g_pe, _ = ops.scan_backward(cum, tr, db, lengths, int(K), sr, ps, pe, ah, al, z2, g)
+    return g_cum, g_tr, g_db, (g_ps if ps is not None else None), (g_pe if pe is not None else None)
+
+
+__all__ = [
+    "SemiCRFStreamingHIP",
+    "semi_crf_streaming_forward",
+    "launch_streaming_hip_kernel",
+    "launch_streaming_hip_backward",
+    "_compute_checkpoint_interval",
+    "prepare_inputs",
+    "NEG_INF",
+]

@@ -1,0 +1,185 @@
+"""PyTorch custom ops over the C ABI of libtsm_hip.so (namespace ``tsm_amd``).
+
+Each op allocates its outputs and a scratch workspace through the PyTorch
+caching allocator on the input's device, then enqueues the HIP kernels on the
+current stream of that device (no host synchronisation).  The ops have fake
+(meta) implementations, so shapes propagate under tracing.
+
+The ops take already-validated, contiguous fp32 inputs on one HIP device; the
+user-facing checks live in :mod:`torch_semimarkov_amd.streaming.autograd`.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Optional
+
+import torch
+from torch import Tensor
+
+from .. import _native as N
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _workspace(nbytes: int, dev: torch.device) -> Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=dev)
+
+
+def _size(query, *args) -> int:
+    out = ctypes.c_size_t(0)
+    N.check(query(*args, ctypes.byref(out)), query.__name__)
+    return int(out.value)
+
+
+# --------------------------------------------------------------------------- forward
+@torch.library.custom_op("tsm_amd::scan_forward", mutates_args=())
+def scan_forward(
+    cum: Tensor, transition: Tensor, duration_bias: Tensor, lengths: Tensor, K: int, semiring: int,
+    proj_start: Optional[Tensor], proj_end: Optional[Tensor], store: bool,
+) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """Partition (B,), log2 partition (B,) fp64, alpha_hat, alpha_level, recomputed-chunk counts."""
+    lib = N.lib()
+    B, Tp1, C = cum.shape
+    T = Tp1 - 1
+    dev = cum.device
+    part = torch.empty(B, device=dev, dtype=torch.float32)
+    z2 = torch.empty(B, device=dev, dtype=torch.float64)
+    rec = torch.empty(B, device=dev, dtype=torch.int32)
+    if store:
+        ah = torch.empty(B, Tp1, C, device=dev, dtype=torch.float32)
+        al = torch.empty(B, Tp1, device=dev, dtype=torch.float64)
+    else:
+        ah = torch.empty(0, device=dev, dtype=torch.float32)
+        al = torch.empty(0, device=dev, dtype=torch.float64)
+    nbytes = _size(lib.tsm_forward_workspace, B, T, C, K, semiring, proj_start is not None, proj_end is not None)
+    ws = _workspace(nbytes, dev)
+    with torch.cuda.device(dev):
+        rc = lib.tsm_forward(
+            N.ptr(cum), N.ptr(transition), N.ptr(duration_bias), N.ptr(lengths),
+            N.ptr(proj_start), N.ptr(proj_end), B, T, C, K, semiring,
+            N.ptr(part), N.ptr(z2), N.ptr(ah) if store else None, N.ptr(al) if store else None,
+            N.ptr(rec), N.ptr(ws), ws.numel(), _stream(dev),
+        )
+    N.check(rc, "tsm_forward")
+    return part, z2, ah, al, rec
+
+
+@scan_forward.register_fake
+def _(cum, transition, duration_bias, lengths, K, semiring, proj_start, proj_end, store):
+    B, Tp1, C = cum.shape
+    part = cum.new_empty(B)
+    z2 = cum.new_empty(B, dtype=torch.float64)
+    rec = cum.new_empty(B, dtype=torch.int32)
+    if store:
+        return part, z2, cum.new_empty(B, Tp1, C), cum.new_empty(B, Tp1, dtype=torch.float64), rec
+    return part, z2, cum.new_empty(0), cum.new_empty(0, dtype=torch.float64), rec
+
+
+# --------------------------------------------------------------------------- backward
+@torch.library.custom_op("tsm_amd::scan_backward", mutates_args=())
+def scan_backward(
+    cum: Tensor, transition: Tensor, duration_bias: Tensor, lengths: Tensor, K: int, semiring: int,
+    proj_start: Optional[Tensor], proj_end: Optional[Tensor], alpha_hat: Tensor, alpha_level: Tensor,
+    log2_partition: Tensor, grad_output: Tensor,
+) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """grad_cum (B,T+1,C), grad_transition (C,C), grad_duration_bias (K,C), grad_proj_start,
+    grad_proj_end ((B,T,C) or empty), recomputed-chunk counts (B,)."""
+    lib = N.lib()
+    B, Tp1, C = cum.shape
+    T = Tp1 - 1
+    dev = cum.device
+    g_cum = torch.empty(B, Tp1, C, device=dev, dtype=torch.float32)
+    g_tr = torch.empty(C, C, device=dev, dtype=torch.float32)
+    g_db = torch.empty(K, C, device=dev, dtype=torch.float32)
+    g_ps = torch.empty(B, T, C, device=dev, dtype=torch.float32) if proj_start is not None else None
+    g_pe = torch.empty(B, T, C, device=dev, dtype=torch.float32) if proj_end is not None else None
+    rec = torch.empty(B, device=dev, dtype=torch.int32)
+    nbytes = _size(lib.tsm_backward_workspace, B, T, C, K, proj_start is not None, proj_end is not None)
+    ws = _workspace(nbytes, dev)
+    with torch.cuda.device(dev):
+        rc = lib.tsm_backward(
+            N.ptr(cum), N.ptr(transition), N.ptr(duration_bias), N.ptr(lengths),
+            N.ptr(proj_start), N.ptr(proj_end), B, T, C, K, semiring,
+            N.ptr(alpha_hat), N.ptr(alpha_level), N.ptr(log2_partition), N.ptr(grad_output),
+            N.ptr(g_cum), N.ptr(g_tr), N.ptr(g_db), N.ptr(g_ps), N.ptr(g_pe), N.ptr(rec),
+            N.ptr(ws), ws.numel(), _stream(dev),
+        )
+    N.check(rc, "tsm_backward")
+    empty = torch.empty(0, device=dev, dtype=torch.float32)
+    return g_cum, g_tr, g_db, g_ps if g_ps is not None else empty, g_pe if g_pe is not None else empty.clone(), rec
+
+
+@scan_backward.register_fake
+def _(cum, transition, duration_bias, lengths, K, semiring, proj_start, proj_end, alpha_hat, alpha_level,
+      log2_partition, grad_output):
+    B, Tp1, C = cum.shape
+    g_ps = cum.new_empty(B, Tp1 - 1, C) if proj_start is not None else cum.new_empty(0)
+    g_pe = cum.new_empty(B, Tp1 - 1, C) if proj_end is not None else cum.new_empty(0)
+    return (cum.new_empty(B, Tp1, C), cum.new_empty(C, C), cum.new_empty(K, C), g_ps, g_pe,
+            cum.new_empty(B, dtype=torch.int32))
+
+
+# --------------------------------------------------------------------------- exact Viterbi
+@torch.library.custom_op("tsm_amd::viterbi", mutates_args=())
+def viterbi(
+    cum: Tensor, transition: Tensor, duration_bias: Tensor, lengths: Tensor, K: int,
+    proj_start: Optional[Tensor], proj_end: Optional[Tensor], traceback: bool,
+) -> tuple[Tensor, Tensor, Tensor]:
+    """Score (B,) fp32; with ``traceback`` also seg_count (B,) int32 and segments (B,T,4) int32
+    (start, end, label, previous label; last segment first)."""
+    lib = N.lib()
+    B, Tp1, C = cum.shape
+    T = Tp1 - 1
+    dev = cum.device
+    score = torch.empty(B, device=dev, dtype=torch.float32)
+    if traceback:
+        cnt = torch.empty(B, device=dev, dtype=torch.int32)
+        segs = torch.empty(B, T, 4, device=dev, dtype=torch.int32)
+    else:
+        cnt = torch.empty(0, device=dev, dtype=torch.int32)
+        segs = torch.empty(0, device=dev, dtype=torch.int32)
+    nbytes = _size(lib.tsm_viterbi_workspace, B, T, C, K, int(traceback))
+    ws = _workspace(nbytes, dev)
+    with torch.cuda.device(dev):
+        rc = lib.tsm_viterbi(
+            N.ptr(cum), N.ptr(transition), N.ptr(duration_bias), N.ptr(lengths),
+            N.ptr(proj_start), N.ptr(proj_end), B, T, C, K, N.ptr(score), int(traceback),
+            N.ptr(cnt) if traceback else None, N.ptr(segs) if traceback else None,
+            N.ptr(ws), ws.numel(), _stream(dev),
+        )
+    N.check(rc, "tsm_viterbi")
+    return score, cnt, segs
+
+
+@viterbi.register_fake
+def _(cum, transition, duration_bias, lengths, K, proj_start, proj_end, traceback):
+    B, Tp1, C = cum.shape
+    if traceback:
+        return (cum.new_empty(B), cum.new_empty(B, dtype=torch.int32),
+                cum.new_empty(B, Tp1 - 1, 4, dtype=torch.int32))
+    return cum.new_empty(B), cum.new_empty(0, dtype=torch.int32), cum.new_empty(0, dtype=torch.int32)
+
+
+# --------------------------------------------------------------------------- checkpoints
+@torch.library.custom_op("tsm_amd::ring_checkpoints", mutates_args=())
+def ring_checkpoints(alpha_hat: Tensor, alpha_level: Tensor, lengths: Tensor, K: int, interval: int,
+                     n_ckpt: int) -> Tensor:
+    """Reference-layout ring checkpoints (B, n_ckpt, K, C), raw alpha, natural log units."""
+    lib = N.lib()
+    B, Tp1, C = alpha_hat.shape
+    dev = alpha_hat.device
+    out = torch.empty(B, n_ckpt, K, C, device=dev, dtype=torch.float32)
+    with torch.cuda.device(dev):
+        rc = lib.tsm_ring_checkpoints(N.ptr(alpha_hat), N.ptr(alpha_level), N.ptr(lengths), B, Tp1 - 1, C, K,
+                                      interval, n_ckpt, N.ptr(out), _stream(dev))
+    N.check(rc, "tsm_ring_checkpoints")
+    return out
+
+
+@ring_checkpoints.register_fake
+def _(alpha_hat, alpha_level, lengths, K, interval, n_ckpt):
+    B, Tp1, C = alpha_hat.shape
+    return alpha_hat.new_empty(B, n_ckpt, K, C)
