@@ -157,6 +157,9 @@ CASES = [
     (2, 30, 5, 1, [30, 12], False, "log"),
     (2, 45, 7, 4, [45, 30], False, "max"),
     (4, 25, 30, 6, [25, 24, 3, 0], False, "log"),
+    (2, 40, 9, 12, [40, 33], True, "log"),      # 32-lane label groups
+    (2, 36, 5, 16, [36, 20], False, "max"),
+    (1, 30, 4, 70, None, False, "log"),         # 4-lane groups
 ]
 
 
@@ -171,10 +174,12 @@ def test_random_problems_vs_fp64_oracle(B, T, K, C, lengths, proj, sr):
     assert_grads(grads, g64)
 
 
-def test_chunked_scan_vs_fp64_oracle():
-    """T long enough for several speculative chunks (warm-up + verification)."""
+@pytest.mark.parametrize("lengths", [[2600, 1900], [2600, 1560]])
+def test_chunked_scan_vs_fp64_oracle(lengths):
+    """T long enough for several speculative chunks (warm-up + verification); the
+    second case has lengths that are exact multiples of the chunk length (520)."""
     B, T, K, C = 2, 2600, 8, 4
-    cum, tr, db, L, _, _ = rand_problem(B, T, K, C, 77, lengths=[2600, 1900])
+    cum, tr, db, L, _, _ = rand_problem(B, T, K, C, 77, lengths=lengths)
     from torch_semimarkov_amd import _native as N
 
     assert N.plan_info(B, T, C, K)["P"] > 1

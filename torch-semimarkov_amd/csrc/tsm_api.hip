@@ -85,19 +85,30 @@ int make_plan(int64_t B, int64_t T, int64_t C, int64_t K, int has_ps, int has_pe
   p.has_pe = has_pe;
   p.J = pow2_lanes(p.C);
   p.NT = (int)cdiv((int64_t)p.C * p.J, 64) * 64;
-  // ring length: >= Kmax+2; RS % 32 == J % 32 spreads label groups over LDS banks
-  int rs = p.Kmax + 2;
+  // durations per lane and padded duration range
+  p.R = (p.Kmax + p.J - 1) / p.J;
+  p.KP = p.J * p.R;
+  // ring slots: >= Kmax+2 and > KP; RS % 32 == J % 32 spreads label groups over LDS banks
+  int rs = std::max(p.Kmax + 2, p.KP + 1);
   while (rs % 32 != p.J % 32) ++rs;
   p.RS = rs;
+  // ring row: >= RS + KP, and RL % 64 == J % 64 so the 64/J label groups of a
+  // wave start on different LDS banks
+  int rl = p.RS + p.KP;
+  while (rl % 64 != p.J % 64) ++rl;
+  p.RL = rl;
   const int has_proj = (has_ps || has_pe) ? 1 : 0;
-  size_t lds = tsm::scan_lds_layout(p.C, p.Kmax, p.RS, has_proj, 0).total;
+  (void)has_proj;
+  size_t lds = tsm::scan_lds_layout(p.C, p.KP, p.RS, p.RL, 0).total;
   p.global_rings = 0;
   if (lds > (size_t)di.max_lds) {
     p.global_rings = 1;
-    lds = tsm::scan_lds_layout(p.C, p.Kmax, p.RS, has_proj, 1).total;
+    lds = tsm::scan_lds_layout(p.C, p.KP, p.RS, p.RL, 1).total;
     if (lds > (size_t)di.max_lds)
       return fail(TSM_ERR_UNSUPPORTED, "C=%d needs %zu bytes of LDS (> %d)", p.C, lds, di.max_lds);
   }
+  // register-resident duration terms when a lane has at most 32 of them
+  p.RMAX = (!p.global_rings && p.R <= 32) ? 32 : 0;
   p.scan_lds = lds;
   // chunking: about one work item per CU; chunks long enough that the warm-up
   // (W steps) costs at most ~25%.
@@ -154,7 +165,7 @@ struct Carver {
 
 struct ScanWs {
   float *st_spec, *st_end, *fin, *gring;
-  double *lv_spec, *lv_end, *offs, *fin_lvl, *z2;
+  double *lv_spec, *lv_end, *offs, *vstat, *fin_lvl, *z2;
   int* status;
 };
 
@@ -166,11 +177,12 @@ ScanWs carve_scan(Carver& cv, const Plan& p) {
   w.lv_spec = cv.take<double>(items * p.Kmax);
   w.lv_end = cv.take<double>(items * p.Kmax);
   w.offs = cv.take<double>(items);
+  w.vstat = cv.take<double>(2 * items);
   w.status = cv.take<int>(items);
   w.fin = cv.take<float>((size_t)p.B * p.C);
   w.fin_lvl = cv.take<double>(p.B);
   w.z2 = cv.take<double>(p.B);
-  w.gring = p.global_rings ? cv.take<float>(items * tsm::scan_gring_floats(p.C, p.Kmax, p.RS)) : nullptr;
+  w.gring = p.global_rings ? cv.take<float>(items * tsm::scan_gring_floats(p.C, p.KP, p.RL)) : nullptr;
   return w;
 }
 
@@ -189,6 +201,9 @@ tsm::ScanParams scan_params(const Plan& pl, const ScanWs& w, const float* cum, c
   p.K = pl.K;
   p.Kmax = pl.Kmax;
   p.RS = pl.RS;
+  p.R = pl.R;
+  p.KP = pl.KP;
+  p.RL = pl.RL;
   p.P = pl.P;
   p.Lc = pl.Lc;
   p.W = pl.W;
@@ -198,6 +213,7 @@ tsm::ScanParams scan_params(const Plan& pl, const ScanWs& w, const float* cum, c
   p.lv_spec = w.lv_spec;
   p.lv_end = w.lv_end;
   p.offs = w.offs;
+  p.vstat = w.vstat;
   p.status = w.status;
   p.fin = w.fin;
   p.fin_lvl = w.fin_lvl;
@@ -255,7 +271,7 @@ int tsm_plan_info(int64_t B, int64_t T, int64_t C, int64_t K, int has_ps, int ha
   if (!out) return fail(TSM_ERR_INVALID, "out is NULL");
   const DeviceInfo di = device_info();
   const int64_t vals[] = {p.J, p.NT, p.RS, p.P, p.Lc, p.W, p.global_rings, (int64_t)p.scan_lds, p.NB, p.TB,
-                          p.CB, p.NCB, p.JM, p.NTM, (int64_t)p.marg_lds, p.Kmax, di.n_cu};
+                          p.CB, p.NCB, p.JM, p.NTM, (int64_t)p.marg_lds, p.Kmax, di.n_cu, p.R, p.KP, p.RMAX};
   const int m = (int)(sizeof(vals) / sizeof(vals[0]));
   for (int i = 0; i < n && i < m; ++i) out[i] = vals[i];
   return TSM_OK;

@@ -27,20 +27,60 @@ __device__ __forceinline__ float fmax2(float a, float b) { return __builtin_fmax
 
 // ----------------------------------------------------------------------------
 // Reductions inside a group of G consecutive lanes (G a power of two, G <= 64).
-// Groups never straddle a wavefront because 64 % G == 0.
+// Groups never straddle a wavefront because 64 % G == 0.  Every lane receives
+// the group result.  Inside a 16-lane row the partner values come from DPP
+// (quad_perm xor1 / xor2, row_half_mirror, row_mirror: after the quad steps all
+// lanes of a quad agree, so mirroring pairs whole quads / half rows); across
+// rows v_permlane16_swap / v_permlane32_swap exchange rows, and for a
+// symmetric op, op(pair.first, pair.second) equals op(x[lane], x[lane^16]) (or
+// ^32) on every lane.  No LDS traffic and no waits on the LDS pipeline.
 // ----------------------------------------------------------------------------
-template <int G>
-__device__ __forceinline__ float group_max(float v) {
-#pragma unroll
-  for (int m = 1; m < G; m <<= 1) v = fmax2(v, __shfl_xor(v, m, 64));
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(dpp_i<CTRL>(__float_as_int(v)));
+}
+
+constexpr int kDppXor1 = 0xB1;         // quad_perm(1,0,3,2)
+constexpr int kDppXor2 = 0x4E;         // quad_perm(2,3,0,1)
+constexpr int kDppHalfMirror = 0x141;  // row_half_mirror
+constexpr int kDppMirror = 0x140;      // row_mirror
+
+struct OpMax {
+  __device__ __forceinline__ float operator()(float a, float b) const { return fmax2(a, b); }
+};
+struct OpSum {
+  __device__ __forceinline__ float operator()(float a, float b) const { return a + b; }
+};
+
+template <int G, typename Op>
+__device__ __forceinline__ float group_reduce(float v, Op op) {
+  if constexpr (G >= 2) v = op(v, dpp_f<kDppXor1>(v));
+  if constexpr (G >= 4) v = op(v, dpp_f<kDppXor2>(v));
+  if constexpr (G >= 8) v = op(v, dpp_f<kDppHalfMirror>(v));
+  if constexpr (G >= 16) v = op(v, dpp_f<kDppMirror>(v));
+  if constexpr (G >= 32) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_int(v), __float_as_int(v), false, false);
+    v = op(__int_as_float(r[0]), __int_as_float(r[1]));
+  }
+  if constexpr (G >= 64) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false);
+    v = op(__int_as_float(r[0]), __int_as_float(r[1]));
+  }
   return v;
 }
 
 template <int G>
+__device__ __forceinline__ float group_max(float v) {
+  return group_reduce<G>(v, OpMax{});
+}
+
+template <int G>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-  for (int m = 1; m < G; m <<= 1) v += __shfl_xor(v, m, 64);
-  return v;
+  return group_reduce<G>(v, OpSum{});
 }
 
 // Log-sum-exp (base 2) of per-lane partials (m, s), where each lane holds
@@ -59,16 +99,26 @@ struct ValIdx {
   int i;
 };
 
+__device__ __forceinline__ ValIdx better_first(ValIdx a, float ov, int oi) {
+  if (ov > a.v || (ov == a.v && oi < a.i)) return ValIdx{ov, oi};
+  return a;
+}
+
 template <int G>
 __device__ __forceinline__ ValIdx group_argmax_first(ValIdx a) {
-#pragma unroll
-  for (int m = 1; m < G; m <<= 1) {
-    float ov = __shfl_xor(a.v, m, 64);
-    int oi = __shfl_xor(a.i, m, 64);
-    if (ov > a.v || (ov == a.v && oi < a.i)) {
-      a.v = ov;
-      a.i = oi;
-    }
+  if constexpr (G >= 2) a = better_first(a, dpp_f<kDppXor1>(a.v), dpp_i<kDppXor1>(a.i));
+  if constexpr (G >= 4) a = better_first(a, dpp_f<kDppXor2>(a.v), dpp_i<kDppXor2>(a.i));
+  if constexpr (G >= 8) a = better_first(a, dpp_f<kDppHalfMirror>(a.v), dpp_i<kDppHalfMirror>(a.i));
+  if constexpr (G >= 16) a = better_first(a, dpp_f<kDppMirror>(a.v), dpp_i<kDppMirror>(a.i));
+  if constexpr (G >= 32) {
+    const auto rv = __builtin_amdgcn_permlane16_swap(__float_as_int(a.v), __float_as_int(a.v), false, false);
+    const auto ri = __builtin_amdgcn_permlane16_swap(a.i, a.i, false, false);
+    a = better_first(ValIdx{__int_as_float(rv[0]), (int)ri[0]}, __int_as_float(rv[1]), (int)ri[1]);
+  }
+  if constexpr (G >= 64) {
+    const auto rv = __builtin_amdgcn_permlane32_swap(__float_as_int(a.v), __float_as_int(a.v), false, false);
+    const auto ri = __builtin_amdgcn_permlane32_swap(a.i, a.i, false, false);
+    a = better_first(ValIdx{__int_as_float(rv[0]), (int)ri[0]}, __int_as_float(rv[1]), (int)ri[1]);
   }
   return a;
 }

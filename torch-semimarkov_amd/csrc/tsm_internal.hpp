@@ -20,6 +20,7 @@ struct ScanParams {
   const float* ps;         // (B, T, C) proj_start or null
   const float* pe;         // (B, T, C) proj_end or null
   int B, T, C, K, Kmax, RS;
+  int R, KP, RL;           // durations per lane, padded durations, ring row length
   int P, Lc, W;            // chunks per sequence, chunk length, warm-up
   float tol;               // verification tolerance, log2 units
   // per-position output (normalised log2 values and fp64 levels), may be null
@@ -31,6 +32,7 @@ struct ScanParams {
   float* st_end;           // (B*P, Kmax, C)
   double* lv_end;          // (B*P, Kmax)
   double* offs;            // (B*P) frame offsets (log2 units)
+  double* vstat;           // (B*P, 2) max / min of exact - speculative boundary state
   int* status;             // (B*P) 0 exact, 1 speculative+verified, 2 recomputed
   int32_t* recomputed;     // (B) number of recomputed chunks, or null
   // forward only: final row at position len, partition

@@ -9,10 +9,14 @@
 namespace tsm {
 
 // Per-class lane group size J (power of two <= 64): thread tid works for label
-// c = tid / J on durations k = 1 + (tid % J) + J*r.  NT = round_up(C*J, 64).
+// c = tid / J on durations k = 1 + (tid % J) + J*r, r < R = ceil(Kmax/J).
+// NT = round_up(C*J, 64).  KP = J*R >= Kmax is the padded duration range.
 struct Plan {
   int B, T, C, K, Kmax;
-  int J, NT, RS;     // lanes per class, threads per block, ring length
+  int J, NT, RS;     // lanes per class, threads per block, ring slots (>= Kmax+2, >= KP+1)
+  int R, KP, RL;     // durations per lane, padded durations, ring row length (>= RS + KP,
+                     // RL % 64 == J % 64 so the label groups of a wave hit distinct banks)
+  int RMAX;          // register terms per lane in the scans (32) or 0 for the generic loop
   int P, Lc, W;      // scan chunks per sequence, chunk length, warm-up steps
   int global_rings;  // 1: rings live in the workspace (LDS too small)
   size_t scan_lds;   // dynamic LDS bytes of the scan kernels
@@ -26,47 +30,45 @@ struct Plan {
 __host__ __device__ inline size_t align16(size_t x) { return (x + 15) & ~size_t(15); }
 
 // ---- scan kernel LDS layout (bytes offsets) --------------------------------
+// Rings hold, per label, RL = RS + KP floats: slot s (0 <= s < RS) plus a mirror
+// copy of slots s < KP at s + RS, so the KP durations of a step are read at
+// consecutive indices without wrap-around.
 struct ScanLds {
-  size_t lring;  // double[RS]
-  size_t urng;   // float[C*RS]   (ring of normalised values)   -- LDS only if !global
-  size_t crng;   // float[C*RS]   (ring of cumulative scores)
-  size_t prng;   // float[C*RS]   (ring of projection scores)   -- only if a projection
-  size_t dbt;    // float[C*(Kmax+1)]  duration bias, log2 units, [c][k]
-  size_t trt;    // float[C*C]    transition, log2 units, mix layout [class][inner]
-  size_t row;    // float[2*C]    normalised row for the label mix (double buffered)
-  size_t dlt;    // float[2*(Kmax+1)] level differences per duration (double buffered)
-  size_t wred;   // float[2*32]   per-wave maxima (double buffered)
-  size_t red;    // double[64]    block reductions (verification)
+  size_t lring;  // double[RS]      per-position levels (log2 units)
+  size_t red;    // double[64]      block reductions (verification)
+  size_t urng;   // float[C*RL]     state ring (normalised values + folded projection)
+  size_t crng;   // float[C*RL]     ring of cumulative scores
+  size_t dbt;    // float[C*(KP+1)] duration bias, log2 units, [c][k] (generic loop only)
+  size_t trt;    // float[C*C]      transition, log2 units, mix layout [class][inner]
+  size_t row;    // float[C]        row for the label mix
+  size_t dlt;    // float[KP+1]     level difference per duration (-1e30 when invalid)
+  size_t wred;   // float[64]       per-wave maxima
   size_t total;
 };
 
-__host__ __device__ inline ScanLds scan_lds_layout(int C, int Kmax, int RS, int has_proj, int global_rings) {
+__host__ __device__ inline ScanLds scan_lds_layout(int C, int KP, int RS, int RL, int global_rings) {
   ScanLds L;
   size_t o = 0;
   L.lring = o; o = align16(o + sizeof(double) * RS);
   L.red = o; o = align16(o + sizeof(double) * 64);
-  const size_t ring = sizeof(float) * (size_t)C * RS;
-  const size_t dbsz = sizeof(float) * (size_t)C * (Kmax + 1);
   if (!global_rings) {
-    L.urng = o; o = align16(o + ring);
-    L.crng = o; o = align16(o + ring);
-    L.prng = o; o = align16(o + (has_proj ? ring : 0));
-    L.dbt = o; o = align16(o + dbsz);
+    L.urng = o; o = align16(o + sizeof(float) * (size_t)C * RL);
+    L.crng = o; o = align16(o + sizeof(float) * (size_t)C * RL);
+    L.dbt = o; o = align16(o + sizeof(float) * (size_t)C * (KP + 1));
   } else {
-    L.urng = L.crng = L.prng = L.dbt = 0;
+    L.urng = L.crng = L.dbt = 0;
   }
   L.trt = o; o = align16(o + sizeof(float) * (size_t)C * C);
-  L.row = o; o = align16(o + sizeof(float) * 2 * C);
-  L.dlt = o; o = align16(o + sizeof(float) * 2 * (Kmax + 1));
+  L.row = o; o = align16(o + sizeof(float) * C);
+  L.dlt = o; o = align16(o + sizeof(float) * (KP + 1));
   L.wred = o; o = align16(o + sizeof(float) * 64);
   L.total = o;
   return L;
 }
 
-// Per work item global ring footprint (floats) when the rings do not fit LDS:
-// urng, crng, prng (C*RS each) + dbt (C*(Kmax+1)).
-__host__ __device__ inline size_t scan_gring_floats(int C, int Kmax, int RS) {
-  return 3 * (size_t)C * RS + (size_t)C * (Kmax + 1);
+// Per work item ring footprint (floats) in the workspace when LDS is too small.
+__host__ __device__ inline size_t scan_gring_floats(int C, int KP, int RL) {
+  return 2 * (size_t)C * RL + (size_t)C * (KP + 1);
 }
 
 // ---- marginal kernel LDS layout (one block of CB destination labels) -------

@@ -32,12 +32,13 @@
 namespace tsm {
 namespace {
 
+constexpr float kInvalid = -1e30f;  // level difference of a duration that does not exist
+
 struct Smem {
   double* lring;
   double* red;
   float* urng;
   float* crng;
-  float* prng;
   float* dbt;
   float* trt;
   float* row;
@@ -45,24 +46,20 @@ struct Smem {
   float* wred;
 };
 
-__device__ inline Smem carve_scan_smem(char* base, const ScanParams& p, int item, bool has_proj,
-                                       bool global_rings) {
-  const ScanLds L = scan_lds_layout(p.C, p.Kmax, p.RS, has_proj, global_rings);
+__device__ inline Smem carve_scan_smem(char* base, const ScanParams& p, int item, bool global_rings) {
+  const ScanLds L = scan_lds_layout(p.C, p.KP, p.RS, p.RL, global_rings);
   Smem s;
   s.lring = reinterpret_cast<double*>(base + L.lring);
   s.red = reinterpret_cast<double*>(base + L.red);
   if (!global_rings) {
     s.urng = reinterpret_cast<float*>(base + L.urng);
     s.crng = reinterpret_cast<float*>(base + L.crng);
-    s.prng = reinterpret_cast<float*>(base + L.prng);
     s.dbt = reinterpret_cast<float*>(base + L.dbt);
   } else {
-    float* g = p.gring + (size_t)item * scan_gring_floats(p.C, p.Kmax, p.RS);
-    const size_t ring = (size_t)p.C * p.RS;
+    float* g = p.gring + (size_t)item * scan_gring_floats(p.C, p.KP, p.RL);
     s.urng = g;
-    s.crng = g + ring;
-    s.prng = g + 2 * ring;
-    s.dbt = g + 3 * ring;
+    s.crng = g + (size_t)p.C * p.RL;
+    s.dbt = g + 2 * (size_t)p.C * p.RL;
   }
   s.trt = reinterpret_cast<float*>(base + L.trt);
   s.row = reinterpret_cast<float*>(base + L.row);
@@ -71,14 +68,15 @@ __device__ inline Smem carve_scan_smem(char* base, const ScanParams& p, int item
   return s;
 }
 
-// Duration bias (log2) transposed to [c][k], k = 1..Kmax (index min(k, K-1)),
-// and the transition (log2) in the layout the label mix reads.
+// Duration bias (log2) transposed to [c][k], k = 0..KP (row min(k, K-1); 0 for
+// k = 0 and k > Kmax), the transition (log2) in the layout the label mix reads,
+// and zeroed rings (every slot a padded duration may read holds a finite value).
 __device__ inline void load_constants(const ScanParams& p, const Smem& s, bool forward) {
-  const int C = p.C, Kmax = p.Kmax, K = p.K;
-  for (int idx = threadIdx.x; idx < C * (Kmax + 1); idx += blockDim.x) {
-    const int c = idx / (Kmax + 1), k = idx % (Kmax + 1);
+  const int C = p.C, Kmax = p.Kmax, K = p.K, KP = p.KP;
+  for (int idx = threadIdx.x; idx < C * (KP + 1); idx += blockDim.x) {
+    const int c = idx / (KP + 1), k = idx % (KP + 1);
     const int di = k < K - 1 ? k : K - 1;
-    s.dbt[idx] = (k == 0) ? 0.0f : p.db[(size_t)di * C + c] * kLog2e;
+    s.dbt[idx] = (k == 0 || k > Kmax) ? 0.0f : p.db[(size_t)di * C + c] * kLog2e;
   }
   for (int idx = threadIdx.x; idx < C * C; idx += blockDim.x) {
     const int a = idx / C, bb = idx % C;
@@ -86,6 +84,22 @@ __device__ inline void load_constants(const ScanParams& p, const Smem& s, bool f
     // backward mix: output label a = c_src, inner bb = c_dst -> trans[c_src][c_dst]
     s.trt[idx] = (forward ? p.trans[(size_t)bb * C + a] : p.trans[(size_t)a * C + bb]) * kLog2e;
   }
+  for (int idx = threadIdx.x; idx < C * p.RL; idx += blockDim.x) {
+    s.urng[idx] = 0.0f;
+    s.crng[idx] = 0.0f;
+  }
+}
+
+// Forward rings store position pos at a = RS-1-(pos % RS) (and a+RS when a < KP),
+// so durations k = 1..KP of step t sit at A_t + k with A_t = RS-1-(t % RS).
+__device__ __forceinline__ int fwd_slot(int pos, int RS) { return RS - 1 - pos % RS; }
+// Backward rings store position pos at a = pos % RS (and a+RS when a < KP), so
+// positions t+k of step t sit at (t % RS) + k.
+__device__ __forceinline__ int bwd_slot(int pos, int RS) { return pos % RS; }
+
+__device__ __forceinline__ void ring_put(float* ring_c, int a, float v, int RS, int KP) {
+  ring_c[a] = v;
+  if (a < KP) ring_c[a + RS] = v;
 }
 
 template <bool LOGSR>
@@ -108,6 +122,68 @@ struct Acc {
     else return group_max<J>(m);
   }
 };
+
+// (+) over the lane's durations k = k_lane + J*r, r < R, of
+//   fmaf(sgn*(cum_ring - cur_cum), log2e, (db + dlt[k]) + state_ring)
+// combined across the J lanes of the label.  ul / cl / dl point at the lane's
+// first term; term r is J*r floats further.  RMAX > 0: all terms in registers
+// (two passes: max, then exponentials); RMAX == 0: batches of 8 with an online
+// rescale and the duration bias read from LDS (dr).
+template <int J, int RMAX, bool LOGSR, bool FWD>
+__device__ __forceinline__ float pull(const float* ul, const float* cl, const float* dl, const float* dr,
+                                      const float (&dbr)[RMAX > 0 ? RMAX : 1], float cur_cum, int R) {
+  if constexpr (RMAX > 0) {
+    // all loads first (kept in flight together), then the arithmetic
+    float uv[RMAX], cv[RMAX], dv[RMAX];
+#pragma unroll
+    for (int r = 0; r < RMAX; ++r) {
+      if (r < R) {
+        uv[r] = ul[J * r];
+        cv[r] = cl[J * r];
+        dv[r] = dl[J * r];
+      }
+    }
+    float xs[RMAX];
+#pragma unroll
+    for (int r = 0; r < RMAX; ++r) {
+      if (r < R) {
+        const float content = FWD ? (cur_cum - cv[r]) : (cv[r] - cur_cum);
+        xs[r] = fmaf(content, kLog2e, (dbr[r] + dv[r]) + uv[r]);
+      }
+    }
+    float m = kMinusInf;
+#pragma unroll
+    for (int r = 0; r < RMAX; ++r)
+      if (r < R) m = fmax2(m, xs[r]);
+    if constexpr (LOGSR) {
+      float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+      for (int r = 0; r < RMAX; r += 2) {
+        if (r < R) s0 += exp2_hw(xs[r] - m);
+        if (r + 1 < R) s1 += exp2_hw(xs[r + 1] - m);
+      }
+      return group_lse2<J>(m, s0 + s1);
+    } else {
+      return group_max<J>(m);
+    }
+  } else {
+    Acc<LOGSR> acc;
+    for (int r0 = 0; r0 < R; r0 += 8) {
+      float xs[8];
+      const int n = min(8, R - r0);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        if (u < n) {
+          const int o = J * (r0 + u);
+          const float content = FWD ? (cur_cum - cl[o]) : (cl[o] - cur_cum);
+          xs[u] = fmaf(content, kLog2e, (dr[o] + dl[o]) + ul[o]);
+        }
+      }
+      acc.template add<8>(xs, n);
+    }
+    return acc.template reduce<J>();
+  }
+}
 
 // Label mix: out = (+)_{i} (row[i] + trt[cls*C + i]) over the lane's inner
 // indices i = j, j+J, ... then combined across the J lanes.
@@ -164,17 +240,19 @@ __device__ inline int bwd_last_chunk(const ScanParams& p, int len) { return len 
 // mode 0: exact from position 0; mode 1: speculative from t_lo - W;
 // mode 2: exact from the state at t_lo given in (init_st, init_lv).
 // Owned positions: [0, t_hi] for chunk 0, (t_lo, t_hi] otherwise.
+// State ring entry at position s: u-hat[s] (+ proj_start[s]), i.e. everything
+// a segment starting at s contributes that does not depend on its length.
 // ============================================================================
-template <int J, bool LOGSR, bool GR>
+template <int J, int RMAX, bool LOGSR, bool GR>
 __device__ void forward_chunk(const ScanParams& p, char* smem_base, int b, int j, int mode,
                               const float* init_st, const double* init_lv) {
-  const int C = p.C, Kmax = p.Kmax, RS = p.RS, T = p.T;
+  const int C = p.C, Kmax = p.Kmax, RS = p.RS, T = p.T, KP = p.KP, RL = p.RL, R = p.R;
   const int len = seq_len(p, b);
   const int t_lo = j * p.Lc;
   const int t_hi = min(t_lo + p.Lc, len);
   const int item = b * p.P + j;
   const bool has_ps = p.ps != nullptr, has_pe = p.pe != nullptr;
-  Smem s = carve_scan_smem(smem_base, p, item, has_ps, GR);
+  Smem s = carve_scan_smem(smem_base, p, item, GR);
   const int tid = threadIdx.x, NT = blockDim.x;
   const int c_raw = tid / J, lj = tid % J;
   const bool cval = c_raw < C;
@@ -184,9 +262,19 @@ __device__ void forward_chunk(const ScanParams& p, char* smem_base, int b, int j
   const float* ps_b = has_ps ? p.ps + (size_t)b * T * C : nullptr;
   const float* pe_b = has_pe ? p.pe + (size_t)b * T * C : nullptr;
   const bool store = p.val != nullptr;
+  const int k_lane = 1 + lj;
 
   load_constants(p, s, true);
+  __syncthreads();
+  float dbr[RMAX > 0 ? RMAX : 1];
+  if constexpr (RMAX > 0) {
+#pragma unroll
+    for (int r = 0; r < RMAX; ++r) dbr[r] = (r < R) ? s.dbt[c * (KP + 1) + k_lane + J * r] : 0.0f;
+  }
+  __syncthreads();
   const int t_start = mode == 0 ? 0 : (mode == 1 ? t_lo - p.W : t_lo);
+  float* uc = s.urng + c * RL;
+  float* cc_ring = s.crng + c * RL;
   // ---- initial ring ----
   if (mode == 0) {
     // alpha-hat[0] = 0 for all labels, level 0; u[0] = mix of a zero row.
@@ -195,9 +283,9 @@ __device__ void forward_chunk(const ScanParams& p, char* smem_base, int b, int j
     __syncthreads();
     const float u0 = label_mix<J, LOGSR>(s.row, s.trt, c, lj, C, 0.0f);
     if (cval && lj == 0) {
-      s.urng[c * RS + 0] = u0;
-      s.crng[c * RS + 0] = cum_b[c];
-      if (has_ps && T > 0) s.prng[c * RS + 0] = ps_b[c] * kLog2e;
+      const float ps0 = (has_ps && T > 0) ? ps_b[c] * kLog2e : 0.0f;
+      ring_put(uc, fwd_slot(0, RS), u0 + ps0, RS, KP);
+      ring_put(cc_ring, fwd_slot(0, RS), cum_b[c], RS, KP);
       if (store && j == 0) p.val[((size_t)b * (T + 1)) * C + c] = 0.0f;
       if (len == 0) p.fin[(size_t)b * C + c] = 0.0f;
     }
@@ -205,64 +293,50 @@ __device__ void forward_chunk(const ScanParams& p, char* smem_base, int b, int j
       if (store && j == 0) p.lvl[(size_t)b * (T + 1)] = 0.0;
       if (len == 0) p.fin_lvl[b] = 0.0;
     }
-    for (int k = tid; k <= Kmax; k += NT) s.dlt[k] = 0.0f;
+    for (int k = tid; k <= KP; k += NT) s.dlt[k] = (k == 1) ? 0.0f : kInvalid;
   } else {
     // positions t_start - i, i in [0, Kmax)
+    __syncthreads();
     for (int idx = tid; idx < Kmax * C; idx += NT) {
-      const int i = idx / C, cc = idx % C;
+      const int i = idx / C, c2 = idx % C;
       const int pos = t_start - i;
-      const int slot = pos % RS;
-      s.urng[cc * RS + slot] = (mode == 1) ? 0.0f : init_st[(size_t)i * C + cc];
-      s.crng[cc * RS + slot] = cum_b[(size_t)pos * C + cc];
-      if (has_ps) s.prng[cc * RS + slot] = ps_b[(size_t)pos * C + cc] * kLog2e;
+      const float v = (mode == 1) ? (has_ps ? ps_b[(size_t)pos * C + c2] * kLog2e : 0.0f)
+                                  : init_st[(size_t)i * C + c2];
+      ring_put(s.urng + c2 * RL, fwd_slot(pos, RS), v, RS, KP);
+      ring_put(s.crng + c2 * RL, fwd_slot(pos, RS), cum_b[(size_t)pos * C + c2], RS, KP);
     }
     for (int i = tid; i < Kmax; i += NT) s.lring[(t_start - i) % RS] = (mode == 1) ? 0.0 : init_lv[i];
     const double l0 = (mode == 1) ? 0.0 : init_lv[0];
-    for (int k = tid; k <= Kmax; k += NT)
-      s.dlt[k] = (k <= 1 || mode == 1) ? 0.0f : (float)(init_lv[k - 1] - l0);
+    for (int k = tid; k <= KP; k += NT)
+      s.dlt[k] = (k < 1 || k > Kmax) ? kInvalid : ((k == 1 || mode == 1) ? 0.0f : (float)(init_lv[k - 1] - l0));
   }
   double lvl_prev = (mode == 2) ? init_lv[0] : 0.0;
-  float cur_cum = (t_start + 1 <= T) ? cum_b[(size_t)(t_start + 1) * C + c] : 0.0f;
-  float cur_pe = (has_pe && t_start < T) ? pe_b[(size_t)t_start * C + c] * kLog2e : 0.0f;
+  // Per-step global loads are unconditional (clamped rows; absent projections read
+  // cum and are scaled by 0) so the compiler waits on each prefetch precisely
+  // instead of draining the whole memory pipeline at branch joins.
+  const float* ps_src = has_ps ? ps_b : cum_b;
+  const float* pe_src = has_pe ? pe_b : cum_b;
+  const float ps_scale = has_ps ? kLog2e : 0.0f;
+  const float pe_scale = has_pe ? kLog2e : 0.0f;
+  float cur_cum = cum_b[(size_t)min(t_start + 1, T) * C + c];
+  float cur_pe = pe_src[(size_t)min(t_start, T - 1) * C + c] * pe_scale;
   __syncthreads();
 
   const int rec_spec = (mode == 1) ? t_lo : -1;
   for (int t = t_start + 1; t <= t_hi; ++t) {
     // prefetch next-step operands
-    const float nxt_cum = (t + 1 <= T) ? cum_b[(size_t)(t + 1) * C + c] : 0.0f;
-    const float nxt_pe = (has_pe && t < T) ? pe_b[(size_t)t * C + c] * kLog2e : 0.0f;
-    const float cur_ps = (has_ps && t < T) ? ps_b[(size_t)t * C + c] * kLog2e : 0.0f;
-    const int kcap = (mode == 0) ? min(Kmax, t) : Kmax;
-    const int base = t % RS;
-    const float* ur = s.urng + c * RS;
-    const float* cr = s.crng + c * RS;
-    const float* pr = s.prng + c * RS;
-    const float* dr = s.dbt + c * (Kmax + 1);
+    const float nxt_cum = cum_b[(size_t)min(t + 1, T) * C + c];
+    const float nxt_pe = pe_src[(size_t)min(t, T - 1) * C + c] * pe_scale;
+    const float cur_ps = ps_src[(size_t)min(t, T - 1) * C + c] * ps_scale;
+    const int A = fwd_slot(t, RS);
 
-    // ---- pull over durations ----
-    Acc<LOGSR> acc;
-    for (int k0 = 1 + lj; k0 <= kcap; k0 += 8 * J) {
-      float xs[8];
-      int n = 0;
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int k = k0 + u * J;
-        if (k <= kcap) {
-          const int slot = wrap_slot(base - k, RS);
-          float rest = dr[k] + s.dlt[k] + ur[slot];
-          if (has_ps) rest += pr[slot];
-          xs[u] = fmaf(cur_cum - cr[slot], kLog2e, rest);
-          n = u + 1;
-        }
-      }
-      acc.template add<8>(xs, n);
-    }
-    float a2 = acc.template reduce<J>();
-    if (has_pe) a2 += cur_pe;
+    // ---- pull over durations: alpha'[t,c] = (+)_k seg(t-k,k,c) + u[t-k,c] ----
+    float a2 = pull<J, RMAX, LOGSR, true>(uc + A + k_lane, cc_ring + A + k_lane, s.dlt + k_lane,
+                                          s.dbt + c * (KP + 1) + k_lane, dbr, cur_cum, R);
+    a2 += cur_pe;
 
     // ---- normaliser: max over labels ----
-    float wm = a2;
-    for (int m = J; m < 64; m <<= 1) wm = fmax2(wm, __shfl_xor(wm, m, 64));
+    const float wm = group_max<64>(a2);
     if ((tid & 63) == 0) s.wred[wid] = wm;
     if (cval && lj == 0) s.row[c] = a2;
     __syncthreads();  // A
@@ -279,31 +353,32 @@ __device__ void forward_chunk(const ScanParams& p, char* smem_base, int b, int j
       if (store && owned) p.lvl[(size_t)b * (T + 1) + t] = lvl_t;
       if (t == len) p.fin_lvl[b] = lvl_t;
     }
-    // level differences for the next step: dlt[k] = lvl[t+1-k] - lvl[t]
-    for (int k = tid + 1; k <= Kmax; k += NT)
-      s.dlt[k] = (k == 1) ? 0.0f : (float)(s.lring[wrap_slot(base + 1 - k, RS)] - lvl_t);
+    // level differences for step t+1: dlt[k] = lvl[t+1-k] - lvl[t]
+    const int kcap_next = (mode == 0) ? min(Kmax, t + 1) : Kmax;
+    for (int k = tid + 1; k <= KP; k += NT)
+      s.dlt[k] = (k > kcap_next) ? kInvalid
+                                 : ((k == 1) ? 0.0f : (float)(s.lring[wrap_slot(t % RS + 1 - k, RS)] - lvl_t));
     // ---- label mix: u[t,c] = (+)_{c'} alpha-hat[t,c'] + trans[c',c] ----
     const float u2 = label_mix<J, LOGSR>(s.row, s.trt, c, lj, C, mx);
     if (cval && lj == 0) {
-      s.urng[c * RS + base] = u2;
-      s.crng[c * RS + base] = cur_cum;
-      if (has_ps) s.prng[c * RS + base] = cur_ps;
+      ring_put(uc, A, u2 + cur_ps, RS, KP);
+      ring_put(cc_ring, A, cur_cum, RS, KP);
     }
-    if (tid == 0) s.lring[base] = lvl_t;
+    if (tid == 0) s.lring[t % RS] = lvl_t;
     lvl_prev = lvl_t;
     cur_cum = nxt_cum;
     cur_pe = nxt_pe;
     __syncthreads();  // C
-    // ---- boundary states for verification ----
+    // ---- boundary states for verification: ring positions t-i, i < Kmax ----
     const bool rec_end = (t == t_hi) && (t_hi < len);
     if (t == rec_spec || rec_end) {
       float* st = (t == rec_spec ? p.st_spec : p.st_end) + (size_t)item * Kmax * C;
       double* lv = (t == rec_spec ? p.lv_spec : p.lv_end) + (size_t)item * Kmax;
       for (int idx = tid; idx < Kmax * C; idx += NT) {
-        const int i = idx / C, cc = idx % C;
-        st[idx] = s.urng[cc * RS + wrap_slot(base - i, RS)];
+        const int i = idx / C, c2 = idx % C;
+        st[idx] = s.urng[c2 * RL + A + i];
       }
-      for (int i = tid; i < Kmax; i += NT) lv[i] = s.lring[wrap_slot(base - i, RS)];
+      for (int i = tid; i < Kmax; i += NT) lv[i] = s.lring[wrap_slot(t % RS - i, RS)];
     }
   }
 }
@@ -313,18 +388,20 @@ __device__ void forward_chunk(const ScanParams& p, char* smem_base, int b, int j
 // mode 0: exact from position len; mode 1: speculative from t_hi + W;
 // mode 2: exact from the state at t_hi given in (init_st, init_lv).
 // Owned positions: [t_lo, t_hi) plus len for the last chunk.
+// State ring entry at position e: beta-hat[e] (+ proj_end[e-1]), i.e. everything
+// a segment ending at e contributes that does not depend on its length.
 // ============================================================================
-template <int J, bool LOGSR, bool GR>
+template <int J, int RMAX, bool LOGSR, bool GR>
 __device__ void backward_chunk(const ScanParams& p, char* smem_base, int b, int j, int mode,
                                const float* init_st, const double* init_lv) {
-  const int C = p.C, Kmax = p.Kmax, RS = p.RS, T = p.T;
+  const int C = p.C, Kmax = p.Kmax, RS = p.RS, T = p.T, KP = p.KP, RL = p.RL, R = p.R;
   const int len = seq_len(p, b);
   const int t_lo = j * p.Lc;
   const int jl = bwd_last_chunk(p, len);
   const int t_hi = (j == jl) ? len : (j + 1) * p.Lc;
   const int item = b * p.P + j;
   const bool has_ps = p.ps != nullptr, has_pe = p.pe != nullptr;
-  Smem s = carve_scan_smem(smem_base, p, item, has_pe, GR);
+  Smem s = carve_scan_smem(smem_base, p, item, GR);
   const int tid = threadIdx.x, NT = blockDim.x;
   const int c_raw = tid / J, lj = tid % J;
   const bool cval = c_raw < C;
@@ -334,86 +411,71 @@ __device__ void backward_chunk(const ScanParams& p, char* smem_base, int b, int 
   const float* ps_b = has_ps ? p.ps + (size_t)b * T * C : nullptr;
   const float* pe_b = has_pe ? p.pe + (size_t)b * T * C : nullptr;
   const bool store = p.val != nullptr;
+  const int k_lane = 1 + lj;
 
   load_constants(p, s, false);
+  __syncthreads();
+  float dbr[RMAX > 0 ? RMAX : 1];
+  if constexpr (RMAX > 0) {
+#pragma unroll
+    for (int r = 0; r < RMAX; ++r) dbr[r] = (r < R) ? s.dbt[c * (KP + 1) + k_lane + J * r] : 0.0f;
+  }
+  __syncthreads();
   const int t_start = mode == 0 ? len : (mode == 1 ? t_hi + p.W : t_hi);
+  float* uc = s.urng + c * RL;
+  float* cc_ring = s.crng + c * RL;
   if (mode == 0) {
     if (cval && lj == 0) {
-      s.urng[c * RS + len % RS] = 0.0f;
-      s.crng[c * RS + len % RS] = cum_b[(size_t)len * C + c];
+      const float pe0 = (has_pe && len >= 1) ? pe_b[(size_t)(len - 1) * C + c] * kLog2e : 0.0f;
+      ring_put(uc, bwd_slot(len, RS), pe0, RS, KP);
+      ring_put(cc_ring, bwd_slot(len, RS), cum_b[(size_t)len * C + c], RS, KP);
       if (store) p.val[((size_t)b * (T + 1) + len) * C + c] = 0.0f;
     }
     if (tid == 0) {
       s.lring[len % RS] = 0.0;
       if (store) p.lvl[(size_t)b * (T + 1) + len] = 0.0;
     }
-    for (int k = tid; k <= Kmax; k += NT) s.dlt[k] = 0.0f;
+    for (int k = tid; k <= KP; k += NT) s.dlt[k] = (k == 1) ? 0.0f : kInvalid;
   } else {
+    __syncthreads();
     for (int idx = tid; idx < Kmax * C; idx += NT) {
-      const int i = idx / C, cc = idx % C;
+      const int i = idx / C, c2 = idx % C;
       const int pos = t_start + i;
-      const int slot = pos % RS;
-      s.urng[cc * RS + slot] = (mode == 1) ? 0.0f : init_st[(size_t)i * C + cc];
-      s.crng[cc * RS + slot] = cum_b[(size_t)pos * C + cc];
+      const float v = (mode == 1) ? (has_pe ? pe_b[(size_t)(pos - 1) * C + c2] * kLog2e : 0.0f)
+                                  : init_st[(size_t)i * C + c2];
+      ring_put(s.urng + c2 * RL, bwd_slot(pos, RS), v, RS, KP);
+      ring_put(s.crng + c2 * RL, bwd_slot(pos, RS), cum_b[(size_t)pos * C + c2], RS, KP);
     }
     for (int i = tid; i < Kmax; i += NT) s.lring[(t_start + i) % RS] = (mode == 1) ? 0.0 : init_lv[i];
     const double l0 = (mode == 1) ? 0.0 : init_lv[0];
     // dlt[k] = lvl[t_start - 1 + k] - lvl[t_start]
-    for (int k = tid; k <= Kmax; k += NT)
-      s.dlt[k] = (k <= 1 || mode == 1) ? 0.0f : (float)(init_lv[k - 1] - l0);
-  }
-  // proj_end ring holds positions [t, t+Kmax-1] during step t (segment ends t+k-1)
-  if (has_pe) {
-    for (int idx = tid; idx < Kmax * C; idx += NT) {
-      const int i = idx / C, cc = idx % C;
-      const int pos = t_start - 1 + i;
-      if (pos >= 0 && pos < T && pos < len) s.prng[cc * RS + pos % RS] = pe_b[(size_t)pos * C + cc] * kLog2e;
-    }
+    for (int k = tid; k <= KP; k += NT)
+      s.dlt[k] = (k < 1 || k > Kmax) ? kInvalid : ((k == 1 || mode == 1) ? 0.0f : (float)(init_lv[k - 1] - l0));
   }
   double lvl_next = (mode == 2) ? init_lv[0] : 0.0;
-  float cur_cum = (t_start >= 1) ? cum_b[(size_t)(t_start - 1) * C + c] : 0.0f;
+  // unconditional per-step loads (see forward_chunk)
+  const float* ps_src = has_ps ? ps_b : cum_b;
+  const float* pe_src = has_pe ? pe_b : cum_b;
+  const float ps_scale = has_ps ? kLog2e : 0.0f;
+  const float pe_scale = has_pe ? kLog2e : 0.0f;
+  float cur_cum = cum_b[(size_t)max(t_start - 1, 0) * C + c];
   __syncthreads();
 
   const int rec_spec = (mode == 1) ? t_hi : -1;
   const int rec_end = (j >= 1) ? t_lo : -1;
   for (int t = t_start - 1; t >= t_lo; --t) {
-    const float nxt_cum = (t >= 1) ? cum_b[(size_t)(t - 1) * C + c] : 0.0f;
-    const float nxt_pe = (has_pe && t >= 1) ? pe_b[(size_t)(t - 1) * C + c] * kLog2e : 0.0f;
-    const float cur_ps = has_ps ? ps_b[(size_t)t * C + c] * kLog2e : 0.0f;
-    const int kcap = (mode == 0) ? min(Kmax, len - t) : Kmax;
-    const int base = t % RS;
-    const float* ur = s.urng + c * RS;
-    const float* cr = s.crng + c * RS;
-    const float* pr = s.prng + c * RS;
-    const float* dr = s.dbt + c * (Kmax + 1);
+    const float nxt_cum = cum_b[(size_t)max(t - 1, 0) * C + c];
+    // proj_end of the segment ending at t-1 (folded into ring position t); none for t = 0
+    const float pe_prev = pe_src[(size_t)max(t - 1, 0) * C + c] * (t >= 1 ? pe_scale : 0.0f);
+    const float cur_ps = ps_src[(size_t)t * C + c] * ps_scale;
+    const int A = bwd_slot(t, RS);
 
     // ---- pull: w[t,c] = (+)_k seg(t,k,c) + beta[t+k,c] ----
-    Acc<LOGSR> acc;
-    for (int k0 = 1 + lj; k0 <= kcap; k0 += 8 * J) {
-      float xs[8];
-      int n = 0;
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int k = k0 + u * J;
-        if (k <= kcap) {
-          int slot = base + k;
-          if (slot >= RS) slot -= RS;
-          float rest = dr[k] + s.dlt[k] + ur[slot];
-          if (has_pe) {
-            const int ps_slot = slot == 0 ? RS - 1 : slot - 1;
-            rest += pr[ps_slot];
-          }
-          xs[u] = fmaf(cr[slot] - cur_cum, kLog2e, rest);
-          n = u + 1;
-        }
-      }
-      acc.template add<8>(xs, n);
-    }
-    float w2 = acc.template reduce<J>();
-    if (has_ps) w2 += cur_ps;
+    float w2 = pull<J, RMAX, LOGSR, false>(uc + A + k_lane, cc_ring + A + k_lane, s.dlt + k_lane,
+                                           s.dbt + c * (KP + 1) + k_lane, dbr, cur_cum, R);
+    w2 += cur_ps;
 
-    float wm = w2;
-    for (int m = J; m < 64; m <<= 1) wm = fmax2(wm, __shfl_xor(wm, m, 64));
+    const float wm = group_max<64>(w2);
     if ((tid & 63) == 0) s.wred[wid] = wm;
     if (cval && lj == 0) s.row[c] = w2;
     __syncthreads();  // A
@@ -425,19 +487,19 @@ __device__ void backward_chunk(const ScanParams& p, char* smem_base, int b, int 
     const bool owned = t < t_hi || (j == jl);
     if (cval && lj == 0) {
       if (store && owned) p.val[((size_t)b * (T + 1) + t) * C + c] = b2;
-      s.urng[c * RS + base] = b2;
-      s.crng[c * RS + base] = cur_cum;
-      if (has_pe && t >= 1) s.prng[c * RS + wrap_slot(base - 1, RS)] = nxt_pe;
+      ring_put(uc, A, b2 + pe_prev, RS, KP);
+      ring_put(cc_ring, A, cur_cum, RS, KP);
     }
     if (tid == 0) {
       if (store && owned) p.lvl[(size_t)b * (T + 1) + t] = lvl_t;
-      s.lring[base] = lvl_t;
+      s.lring[A] = lvl_t;
     }
     // dlt for step t-1: lvl[t-1+k] - lvl[t]
-    for (int k = tid + 1; k <= Kmax; k += NT) {
-      int slot = base - 1 + k;
+    const int kcap_next = (mode == 0) ? min(Kmax, len - t + 1) : Kmax;
+    for (int k = tid + 1; k <= KP; k += NT) {
+      int slot = A - 1 + k;
       if (slot >= RS) slot -= RS;
-      s.dlt[k] = (k == 1) ? 0.0f : (float)(s.lring[slot] - lvl_t);
+      s.dlt[k] = (k > kcap_next) ? kInvalid : ((k == 1) ? 0.0f : (float)(s.lring[slot] - lvl_t));
     }
     lvl_next = lvl_t;
     cur_cum = nxt_cum;
@@ -446,13 +508,11 @@ __device__ void backward_chunk(const ScanParams& p, char* smem_base, int b, int 
       float* st = (t == rec_spec ? p.st_spec : p.st_end) + (size_t)item * Kmax * C;
       double* lv = (t == rec_spec ? p.lv_spec : p.lv_end) + (size_t)item * Kmax;
       for (int idx = tid; idx < Kmax * C; idx += NT) {
-        const int i = idx / C, cc = idx % C;
-        int slot = base + i;
-        if (slot >= RS) slot -= RS;
-        st[idx] = s.urng[cc * RS + slot];
+        const int i = idx / C, c2 = idx % C;
+        st[idx] = s.urng[c2 * RL + A + i];
       }
       for (int i = tid; i < Kmax; i += NT) {
-        int slot = base + i;
+        int slot = A + i;
         if (slot >= RS) slot -= RS;
         lv[i] = s.lring[slot];
       }
@@ -466,7 +526,7 @@ __device__ inline bool bwd_spec(const ScanParams& p, int j, int len) {
   return j < jl && (j + 1) * p.Lc + p.W + p.Kmax - 1 <= len;
 }
 
-template <int J, bool LOGSR, bool GR>
+template <int J, int RMAX, bool LOGSR, bool GR>
 __global__ void __launch_bounds__(512) scan_fwd_kernel(ScanParams p) {
   extern __shared__ __align__(16) char smem[];
   const int b = blockIdx.x / p.P, j = blockIdx.x % p.P;
@@ -478,10 +538,10 @@ __global__ void __launch_bounds__(512) scan_fwd_kernel(ScanParams p) {
   }
   const int mode = fwd_spec(p, j) ? 1 : 0;
   if (threadIdx.x == 0) p.status[item] = mode;
-  forward_chunk<J, LOGSR, GR>(p, smem, b, j, mode, nullptr, nullptr);
+  forward_chunk<J, RMAX, LOGSR, GR>(p, smem, b, j, mode, nullptr, nullptr);
 }
 
-template <int J, bool LOGSR, bool GR>
+template <int J, int RMAX, bool LOGSR, bool GR>
 __global__ void __launch_bounds__(512) scan_bwd_kernel(ScanParams p) {
   extern __shared__ __align__(16) char smem[];
   const int b = blockIdx.x / p.P, j = blockIdx.x % p.P;
@@ -493,45 +553,88 @@ __global__ void __launch_bounds__(512) scan_bwd_kernel(ScanParams p) {
   }
   const int mode = bwd_spec(p, j, len) ? 1 : 0;
   if (threadIdx.x == 0) p.status[item] = mode;
-  backward_chunk<J, LOGSR, GR>(p, smem, b, j, mode, nullptr, nullptr);
+  backward_chunk<J, RMAX, LOGSR, GR>(p, smem, b, j, mode, nullptr, nullptr);
+}
+
+// Spread of (exact - speculative) over the boundary state of every speculative
+// chunk, all boundaries in parallel: vstat[item] = (max, min) of
+//   D[i,c] = (lv_exact[i] - lv_spec[i]) + (st_exact[i,c] - st_spec[i,c])   (fp64)
+// where "exact" is the neighbouring chunk's end state (forward: chunk j-1,
+// backward: chunk j+1).  Entries unreachable in both (< -1e8 in log2 units) are
+// skipped: they add exactly nothing to any later sum.
+__global__ void __launch_bounds__(256) verify_kernel(ScanParams p, int forward) {
+  __shared__ double red[64];
+  const int b = blockIdx.x / p.P, j = blockIdx.x % p.P;
+  const int len = seq_len(p, b);
+  const int item = b * p.P + j;
+  const bool spec = forward ? fwd_spec(p, j) && j * p.Lc < len : bwd_spec(p, j, len);
+  if (!spec) return;
+  const int Kmax = p.Kmax, C = p.C;
+  const size_t e = forward ? (size_t)(item - 1) : (size_t)(item + 1), sp = (size_t)item;
+  double hi = -1e300, lo = 1e300;
+  for (int idx = threadIdx.x; idx < Kmax * C; idx += blockDim.x) {
+    const int i = idx / C;
+    const float a = p.st_end[e * Kmax * C + idx], bb = p.st_spec[sp * Kmax * C + idx];
+    if (a < -1e8f && bb < -1e8f) continue;
+    const double d = (p.lv_end[e * Kmax + i] - p.lv_spec[sp * Kmax + i]) + ((double)a - (double)bb);
+    hi = fmax(hi, d);
+    lo = fmin(lo, d);
+  }
+  double dmax, dmin;
+  block_minmax(hi, lo, red, dmax, dmin);
+  if (threadIdx.x == 0) {
+    p.vstat[2 * sp] = dmax;
+    p.vstat[2 * sp + 1] = dmin;
+  }
 }
 
 // Sequential verification / repair of a sequence's chunks (one block per sequence).
-template <int J, bool LOGSR, bool GR>
+template <int J, int RMAX, bool LOGSR, bool GR>
 __global__ void __launch_bounds__(512) fwd_fixup_kernel(ScanParams p) {
   extern __shared__ __align__(16) char smem[];
   const int b = blockIdx.x;
   const int len = seq_len(p, b);
-  const ScanLds L = scan_lds_layout(p.C, p.Kmax, p.RS, p.ps != nullptr, GR);
+  const ScanLds L = scan_lds_layout(p.C, p.KP, p.RS, p.RL, GR);
   double* red = reinterpret_cast<double*>(smem + L.red);
   const int Kmax = p.Kmax, C = p.C;
   const int nch = len == 0 ? 1 : (len + p.Lc - 1) / p.Lc;
   double F = 0.0;
   int n_re = 0;
   if (threadIdx.x == 0) p.offs[(size_t)b * p.P] = 0.0;
+  bool prev_recomputed = false;
   for (int j = 1; j < nch; ++j) {
     const int item = b * p.P + j;
     if (!fwd_spec(p, j)) {
       F = 0.0;  // chunk ran exactly from position 0
+      prev_recomputed = false;
     } else {
       const size_t e = (size_t)(item - 1), sp = (size_t)item;
-      double hi = -1e300, lo = 1e300;
-      for (int idx = threadIdx.x; idx < Kmax * C; idx += blockDim.x) {
-        const int i = idx / C;
-        const float a = p.st_end[e * Kmax * C + idx], bb = p.st_spec[sp * Kmax * C + idx];
-        if (a < -1e8f && bb < -1e8f) continue;
-        const double d = (p.lv_end[e * Kmax + i] - p.lv_spec[sp * Kmax + i]) + ((double)a - (double)bb);
-        hi = fmax(hi, d);
-        lo = fmin(lo, d);
-      }
       double dmax, dmin;
-      block_minmax(hi, lo, red, dmax, dmin);
+      if (!prev_recomputed) {
+        // measured in parallel by verify_kernel against chunk j-1's original end state
+        dmax = p.vstat[2 * sp];
+        dmin = p.vstat[2 * sp + 1];
+      } else {
+        // chunk j-1 was recomputed here: its end state changed, measure again
+        double hi = -1e300, lo = 1e300;
+        for (int idx = threadIdx.x; idx < Kmax * C; idx += blockDim.x) {
+          const int i = idx / C;
+          const float a = p.st_end[e * Kmax * C + idx], bb = p.st_spec[sp * Kmax * C + idx];
+          if (a < -1e8f && bb < -1e8f) continue;
+          const double d = (p.lv_end[e * Kmax + i] - p.lv_spec[sp * Kmax + i]) + ((double)a - (double)bb);
+          hi = fmax(hi, d);
+          lo = fmin(lo, d);
+        }
+        block_minmax(hi, lo, red, dmax, dmin);
+      }
       if (dmax - dmin <= (double)p.tol) {
         F += 0.5 * (dmax + dmin);
+        prev_recomputed = false;
       } else {
-        forward_chunk<J, LOGSR, GR>(p, smem, b, j, 2, p.st_end + e * Kmax * C, p.lv_end + e * Kmax);
+        forward_chunk<J, RMAX, LOGSR, GR>(p, smem, b, j, 2, p.st_end + e * Kmax * C, p.lv_end + e * Kmax);
         __syncthreads();
         ++n_re;
+        prev_recomputed = true;
         if (threadIdx.x == 0) p.status[item] = 2;
       }
     }
@@ -567,41 +670,50 @@ __global__ void __launch_bounds__(512) fwd_fixup_kernel(ScanParams p) {
   }
 }
 
-template <int J, bool LOGSR, bool GR>
+template <int J, int RMAX, bool LOGSR, bool GR>
 __global__ void __launch_bounds__(512) bwd_fixup_kernel(ScanParams p) {
   extern __shared__ __align__(16) char smem[];
   const int b = blockIdx.x;
   const int len = seq_len(p, b);
-  const ScanLds L = scan_lds_layout(p.C, p.Kmax, p.RS, p.pe != nullptr, GR);
+  const ScanLds L = scan_lds_layout(p.C, p.KP, p.RS, p.RL, GR);
   double* red = reinterpret_cast<double*>(smem + L.red);
   const int Kmax = p.Kmax, C = p.C;
   const int jl = bwd_last_chunk(p, len);
   double F = 0.0;
   int n_re = 0;
   if (threadIdx.x == 0) p.offs[(size_t)b * p.P + jl] = 0.0;
+  bool prev_recomputed = false;
   for (int j = jl - 1; j >= 0; --j) {
     const int item = b * p.P + j;
     if (!bwd_spec(p, j, len)) {
-      F = 0.0;
+      F = 0.0;  // chunk ran exactly from position len
+      prev_recomputed = false;
     } else {
       const size_t e = (size_t)(item + 1), sp = (size_t)item;
-      double hi = -1e300, lo = 1e300;
-      for (int idx = threadIdx.x; idx < Kmax * C; idx += blockDim.x) {
-        const int i = idx / C;
-        const float a = p.st_end[e * Kmax * C + idx], bb = p.st_spec[sp * Kmax * C + idx];
-        if (a < -1e8f && bb < -1e8f) continue;
-        const double d = (p.lv_end[e * Kmax + i] - p.lv_spec[sp * Kmax + i]) + ((double)a - (double)bb);
-        hi = fmax(hi, d);
-        lo = fmin(lo, d);
-      }
       double dmax, dmin;
-      block_minmax(hi, lo, red, dmax, dmin);
+      if (!prev_recomputed) {
+        dmax = p.vstat[2 * sp];
+        dmin = p.vstat[2 * sp + 1];
+      } else {
+        double hi = -1e300, lo = 1e300;
+        for (int idx = threadIdx.x; idx < Kmax * C; idx += blockDim.x) {
+          const int i = idx / C;
+          const float a = p.st_end[e * Kmax * C + idx], bb = p.st_spec[sp * Kmax * C + idx];
+          if (a < -1e8f && bb < -1e8f) continue;
+          const double d = (p.lv_end[e * Kmax + i] - p.lv_spec[sp * Kmax + i]) + ((double)a - (double)bb);
+          hi = fmax(hi, d);
+          lo = fmin(lo, d);
+        }
+        block_minmax(hi, lo, red, dmax, dmin);
+      }
       if (dmax - dmin <= (double)p.tol) {
         F += 0.5 * (dmax + dmin);
+        prev_recomputed = false;
       } else {
-        backward_chunk<J, LOGSR, GR>(p, smem, b, j, 2, p.st_end + e * Kmax * C, p.lv_end + e * Kmax);
+        backward_chunk<J, RMAX, LOGSR, GR>(p, smem, b, j, 2, p.st_end + e * Kmax * C, p.lv_end + e * Kmax);
         __syncthreads();
         ++n_re;
+        prev_recomputed = true;
         if (threadIdx.x == 0) p.status[item] = 2;
       }
     }
@@ -622,26 +734,28 @@ __global__ void apply_offsets_kernel(ScanParams p, int forward) {
   }
 }
 
-template <int J, bool LOGSR, bool GR>
+template <int J, int RMAX, bool LOGSR, bool GR>
 int launch_dir(const Plan& pl, const ScanParams& p, bool forward, hipStream_t st) {
   const size_t lds = pl.scan_lds;
   if (forward) {
-    auto k1 = scan_fwd_kernel<J, LOGSR, GR>;
-    auto k2 = fwd_fixup_kernel<J, LOGSR, GR>;
+    auto k1 = scan_fwd_kernel<J, RMAX, LOGSR, GR>;
+    auto k2 = fwd_fixup_kernel<J, RMAX, LOGSR, GR>;
     hipError_t e = hipFuncSetAttribute((const void*)k1, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
     e = hipFuncSetAttribute((const void*)k2, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k1, dim3(pl.B * pl.P), dim3(pl.NT), lds, st, p);
+    if (pl.P > 1) hipLaunchKernelGGL(verify_kernel, dim3(pl.B * pl.P), dim3(256), 0, st, p, 1);
     hipLaunchKernelGGL(k2, dim3(pl.B), dim3(pl.NT), lds, st, p);
   } else {
-    auto k1 = scan_bwd_kernel<J, LOGSR, GR>;
-    auto k2 = bwd_fixup_kernel<J, LOGSR, GR>;
+    auto k1 = scan_bwd_kernel<J, RMAX, LOGSR, GR>;
+    auto k2 = bwd_fixup_kernel<J, RMAX, LOGSR, GR>;
     hipError_t e = hipFuncSetAttribute((const void*)k1, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
     e = hipFuncSetAttribute((const void*)k2, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k1, dim3(pl.B * pl.P), dim3(pl.NT), lds, st, p);
+    if (pl.P > 1) hipLaunchKernelGGL(verify_kernel, dim3(pl.B * pl.P), dim3(256), 0, st, p, 0);
     hipLaunchKernelGGL(k2, dim3(pl.B), dim3(pl.NT), lds, st, p);
   }
   if (p.lvl != nullptr) {
@@ -653,25 +767,31 @@ int launch_dir(const Plan& pl, const ScanParams& p, bool forward, hipStream_t st
   return hipGetLastError();
 }
 
-template <bool LOGSR, bool GR>
+template <int RMAX, bool LOGSR, bool GR>
 int launch_j(const Plan& pl, const ScanParams& p, bool fwd, hipStream_t st) {
   switch (pl.J) {
-    case 1: return launch_dir<1, LOGSR, GR>(pl, p, fwd, st);
-    case 2: return launch_dir<2, LOGSR, GR>(pl, p, fwd, st);
-    case 4: return launch_dir<4, LOGSR, GR>(pl, p, fwd, st);
-    case 8: return launch_dir<8, LOGSR, GR>(pl, p, fwd, st);
-    case 16: return launch_dir<16, LOGSR, GR>(pl, p, fwd, st);
-    case 32: return launch_dir<32, LOGSR, GR>(pl, p, fwd, st);
-    case 64: return launch_dir<64, LOGSR, GR>(pl, p, fwd, st);
+    case 1: return launch_dir<1, RMAX, LOGSR, GR>(pl, p, fwd, st);
+    case 2: return launch_dir<2, RMAX, LOGSR, GR>(pl, p, fwd, st);
+    case 4: return launch_dir<4, RMAX, LOGSR, GR>(pl, p, fwd, st);
+    case 8: return launch_dir<8, RMAX, LOGSR, GR>(pl, p, fwd, st);
+    case 16: return launch_dir<16, RMAX, LOGSR, GR>(pl, p, fwd, st);
+    case 32: return launch_dir<32, RMAX, LOGSR, GR>(pl, p, fwd, st);
+    case 64: return launch_dir<64, RMAX, LOGSR, GR>(pl, p, fwd, st);
     default: return (int)hipErrorInvalidValue;
   }
 }
 
+// Instantiated variants: register-resident terms (RMAX = 32) with LDS rings, and
+// the generic loop with LDS or workspace rings.
+template <bool LOGSR>
+int launch_sr(const Plan& pl, const ScanParams& p, bool fwd, hipStream_t st) {
+  if (pl.global_rings) return launch_j<0, LOGSR, true>(pl, p, fwd, st);
+  if (pl.RMAX == 32) return launch_j<32, LOGSR, false>(pl, p, fwd, st);
+  return launch_j<0, LOGSR, false>(pl, p, fwd, st);
+}
+
 int launch_any(const Plan& pl, const ScanParams& p, int semiring, bool fwd, hipStream_t st) {
-  if (semiring == kLog) {
-    return pl.global_rings ? launch_j<true, true>(pl, p, fwd, st) : launch_j<true, false>(pl, p, fwd, st);
-  }
-  return pl.global_rings ? launch_j<false, true>(pl, p, fwd, st) : launch_j<false, false>(pl, p, fwd, st);
+  return semiring == kLog ? launch_sr<true>(pl, p, fwd, st) : launch_sr<false>(pl, p, fwd, st);
 }
 
 }  // namespace
