@@ -3,11 +3,15 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg3] [--cpu-sample T] [--no-cpu]
 
 A step is one forward + backward (log semiring) over the whole synthetic
-workload of BASELINE.json config 3 by default: B=1, T=1,000,000, C=24, K=300,
-emissions N(0,1) cumsum'd along T, transition N(0,0.1), duration_bias[k,c] =
--0.01k + N(0,0.05) for k >= 1 (row 0 = 0), seed 20261203, generated on the host
-and resident in HBM before timing.  Prints one JSON line; see DESIGN.md for the
-roofline model.
+workload "cfg3" by default: B=1, T=1,000,000, C=24, K=300, emissions N(0,1)
+cumsum'd along T, transition N(0,0.1), duration_bias[k,c] = -0.01k + N(0,0.05)
+for k >= 1 (row 0 = 0), seed 20261203, generated on the host and resident in HBM
+before timing.  Prints one JSON line.
+
+Roofline: the path is bound by FP32 VALU and transcendental issue (log-sum-exp
+over K*C^2 terms per position, ~10^4 ops per HBM byte), not by HBM or MFMA.
+A cell is one (b, t, k, c_dst, c_src) term of the direct recursion; the
+per-cell op counts below are fixed in advance and not re-tuned after measuring.
 """
 
 from __future__ import annotations
@@ -28,11 +32,17 @@ for _p in (ROOT, os.path.join(ROOT, "torch-semimarkov_amd")):
 
 import torch  # noqa: E402
 
-# FP32 VALU lane-op and transcendental peaks of one MI355X
+# FP32 VALU lane-op peak (packed-FP32 issue, 157.3/2 T/s) and transcendental
+# (v_exp_f32 / v_log_f32, quarter rate) peak of one MI355X
 V_PEAK = 78.6e12
 T_PEAK = 9.83e12
-# algorithmic ops per cell (b, t, k, c_dst, c_src) of the direct recursion
+# algorithmic ops per cell (b, t, k, c_dst, c_src) of the direct recursion:
+# (VALU lane-ops, transcendentals).  The backward (14, 3) splits into the alpha
+# recompute (5, 1), the beta recursion (4, 1) and the marginals (5, 1); this
+# build stores alpha instead of recomputing it.
 OPS = {"fwd_log": (5, 1), "bwd_log": (14, 3), "fwdbwd_log": (19, 4), "max": (3, 0)}
+KERNEL_OPS = {"scan_fwd_kernel": (5, 1), "scan_bwd_kernel": (4, 1), "marginal_kernel": (5, 1)}
+PROFILES = os.path.join(ROOT, "profiles")
 
 
 def roofline_cells_per_s(kind):
@@ -43,6 +53,34 @@ def roofline_cells_per_s(kind):
 def valu_equiv_ops_per_cell(kind):
     nv, nt = OPS[kind]
     return nv + nt * (V_PEAK / T_PEAK)
+
+
+def profiled_traffic(kernel, workload):
+    """HBM bytes per launch of `kernel` on `workload` from the committed rocprofv3
+    PMC summary (FETCH_SIZE and WRITE_SIZE scaled by a copy-kernel calibration),
+    or None when no summary covers it.  Lines read: `traffic <kernel> <workload> <bytes>`."""
+    path = os.path.join(PROFILES, "pmc_traffic.txt")
+    try:
+        with open(path) as f:
+            for ln in f:
+                parts = ln.split()
+                if len(parts) == 4 and parts[0] == "traffic" and parts[1] == kernel and parts[2] == workload:
+                    return float(parts[3])
+    except OSError:
+        pass
+    return None
+
+
+def copy_calibration(mib=256, reps=3):
+    """A plain device copy of known size, for scaling the FETCH_SIZE / WRITE_SIZE
+    counters: run it under `rocprofv3 --pmc FETCH_SIZE` (then WRITE_SIZE)."""
+    x = torch.empty(mib * 1024 * 1024 // 4, device="cuda")
+    x.normal_()
+    y = torch.empty_like(x)
+    for _ in range(reps):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes_read": x.numel() * 4, "bytes_written": y.numel() * 4, "reps": reps}))
 
 
 CONFIGS = {
@@ -119,13 +157,19 @@ def main():
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS))
-    ap.add_argument("--cpu-sample", type=int, default=2000)
+    ap.add_argument("--cpu-sample", type=int, default=4000)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a 256 MiB device copy (PMC counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
               file=sys.stderr)
         sys.exit(2)
+
+    if args.copy_calibration:
+        copy_calibration()
+        return
 
     import torch_semimarkov_amd as tsa
     from torch_semimarkov_amd import _native as N
@@ -158,21 +202,27 @@ def main():
     for _ in range(args.warmup):
         step(False)
     torch.cuda.synchronize()
+    # per-kernel HIP events, recorded by the library on the stream each kernel runs on
+    N.timing_enable(True)
     t0 = time.perf_counter()
     for _ in range(args.steps):
         part = step(True)
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
+    ktimes = N.timing_read()
+    N.timing_enable(False)
     ms_step = dt * 1e3 / args.steps
     fwd_ms = statistics.mean(a.elapsed_time(b) for a, b, _ in ev)
     bwd_ms = statistics.mean(b.elapsed_time(c) for _, b, c in ev)
 
     cells = B * T * K * C * C
     value = cells / (ms_step / 1e3)
-    # dominant op: the one with the larger share of the step
-    dom_kind, dom_ms, dom_name = (("bwd_log", bwd_ms, "backward (beta scan + fixup + marginals + finalize)")
-                                  if bwd_ms >= fwd_ms else ("fwd_log", fwd_ms, "forward (alpha scan + fixup)"))
-    achieved = cells * valu_equiv_ops_per_cell(dom_kind) / (dom_ms / 1e3) / 1e12
+    # dominant kernel: the largest total time over the timed steps
+    dom = max((k for k in ktimes if k in KERNEL_OPS), key=lambda k: ktimes[k][0])
+    dom_total, dom_launches = ktimes[dom]
+    dom_avg_ms = dom_total / dom_launches
+    nv, nt = KERNEL_OPS[dom]
+    achieved = cells * (nv + nt * V_PEAK / T_PEAK) / (dom_avg_ms / 1e3) / 1e12
     peak = V_PEAK / 1e12
     out = {
         "metric": "fwd+bwd scan cells/s (B*T*K*C^2), 1 GPU",
@@ -193,18 +243,22 @@ def main():
         },
         "roofline": {
             "bound": "valu",
-            "kernel": dom_name,
+            "kernel": dom,
             "achieved": achieved,
             "peak": peak,
             "unit": "TFLOP/s",
             "frac": achieved / peak,
-            "traffic": None,
-            "note": "VALU-equivalent lane-ops of the direct recursion (nominal; the kernels execute the "
-                    "exact label factorisation, ~K*C^2/(K*C+C^2) times less work)",
+            "traffic": profiled_traffic(dom, args.config),
+            "avg_launch_ms": dom_avg_ms,
+            "ops_per_cell": {"valu": nv, "transcendental": nt},
+            "note": "NOMINAL: VALU-equivalent lane-ops (transcendental weighted by V_peak/T_peak) of the "
+                    "direct recursion per cell B*T*K*C^2; the kernels execute the exact label factorisation "
+                    "(K*C + C^2 instead of K*C^2 terms per position), so frac can exceed 1",
         },
         "nominal_roofline_frac_fwdbwd": value / roofline_cells_per_s("fwdbwd_log"),
         "fwd_ms": fwd_ms,
         "bwd_ms": bwd_ms,
+        "kernel_avg_ms": {k: v[0] / v[1] for k, v in sorted(ktimes.items())},
         "plan": plan,
         "logZ": float(part.detach()[0]),
     }

@@ -128,6 +128,23 @@ int tsm_ring_checkpoints(const float* alpha_hat, const double* alpha_level, cons
                          int64_t T, int64_t C, int64_t K, int64_t checkpoint_interval, int64_t n_checkpoints,
                          float* out, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Opt-in kernel timing (benchmarks, diagnostics).  No counterpart in the
+ * reference, which has no per-kernel timer; it exists so a benchmark can time
+ * one kernel on the stream the library launches it on.
+ *   tsm_timing_enable(1)  clears the totals and brackets every later kernel
+ *                         launch with two hipEvents on its stream; (0) stops.
+ *   tsm_timing_read       waits for the recorded events and fills, for kernel
+ *                         ids 0..n-1, the total milliseconds and launch counts
+ *                         (host arrays; either may be NULL).
+ *   tsm_timing_kernel_count / tsm_timing_kernel_name  the kernel ids.
+ * The timing state is process-wide (guarded by a mutex).
+ * ------------------------------------------------------------------------- */
+int tsm_timing_enable(int enable);
+int tsm_timing_read(double* total_ms, int64_t* launches, int n);
+int tsm_timing_kernel_count(void);
+const char* tsm_timing_kernel_name(int kernel_id);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,7 +1,7 @@
 """GPU parity tests: the HIP path (through the C ABI) against the oracle and the
 reference's golden vectors.
 
-Tolerances: log Z within 1e-5 relative; gradients
+Tolerances (the path's stated parity bar): log Z within 1e-5 relative; gradients
 within 1e-5 relative + 1e-4 absolute against the fp64 oracle; Viterbi scores and
 segmentations bit-exact against the fp32 restatement of the reference.
 """
@@ -22,6 +22,7 @@ else:  # collected on CPU, never run there
     DEV = None
 
 import torch_semimarkov_amd as tsa  # noqa: E402
+from torch_semimarkov_amd import _native as N  # noqa: E402
 from torch_semimarkov_amd.streaming import launch_streaming_hip_backward, launch_streaming_hip_kernel, ops  # noqa: E402
 
 RTOL_Z = 1e-5
@@ -234,7 +235,7 @@ def test_deterministic_bitwise():
 
 
 def test_k1_full_size_config2_vs_hmm():
-    """BASELINE config 2 (B=32, T=10^4, C=8, K=1) against a probability-space HMM in fp64."""
+    """Config 2 of the benchmark set (B=32, T=10^4, C=8, K=1) against a probability-space HMM in fp64."""
     B, T, C, K = 32, 10_000, 8, 1
     g = torch.Generator().manual_seed(20261202)
     em = torch.randn(B, T, C, generator=g)
@@ -337,3 +338,23 @@ def test_launcher_checkpoints_and_backward_contract():
     assert gps is None and gpe is None
     assert_grads([gc.cpu(), gt.cpu(), gd.cpu()],
                  [torch.from_numpy(z[k]) for k in ("grad_cum", "grad_transition", "grad_duration_bias")])
+
+
+def test_kernel_timing_counts_launches():
+    z = load_golden("stream_medium")
+    cum, tr, db, L, K, sr, ps, pe = fixture_inputs(z, requires_grad=True)
+    N.timing_enable(True)
+    try:
+        part = tsa.semi_crf_streaming_forward(cum, tr, db, L, K, semiring=sr)
+        part.sum().backward()
+        torch.cuda.synchronize()
+        t = N.timing_read()
+    finally:
+        N.timing_enable(False)
+    for name in ("scan_fwd_kernel", "scan_bwd_kernel", "marginal_kernel", "finalize_rows_kernel"):
+        ms, n = t[name]
+        assert n == 1 and ms > 0.0, (name, t[name])
+    # disabled: nothing more is recorded
+    part = tsa.semi_crf_streaming_forward(cum.detach(), tr.detach(), db.detach(), L, K, semiring=sr)
+    torch.cuda.synchronize()
+    assert N.timing_read() == {}

@@ -159,3 +159,17 @@ def test_segment_dataclass():
     assert s.duration == 5
     r = tsa.ViterbiResult(scores=torch.zeros(1), segments=[[s]])
     assert r.segments[0][0].label == 2
+
+
+def test_kernel_timing_interface_without_gpu():
+    lib = N.lib()
+    n = lib.tsm_timing_kernel_count()
+    names = [lib.tsm_timing_kernel_name(i).decode() for i in range(n)]
+    assert "scan_fwd_kernel" in names and "marginal_kernel" in names and "viterbi_kernel" in names
+    assert len(set(names)) == n
+    assert lib.tsm_timing_kernel_name(n) is None and lib.tsm_timing_kernel_name(-1) is None
+    # enabling and reading with nothing launched needs no device
+    N.timing_enable(True)
+    assert N.timing_read() == {}
+    N.timing_enable(False)
+    assert lib.tsm_timing_read(None, None, -1) == 1

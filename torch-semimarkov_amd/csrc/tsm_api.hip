@@ -479,4 +479,21 @@ int tsm_ring_checkpoints(const float* alpha_hat, const double* alpha_level, cons
   return TSM_OK;
 }
 
+int tsm_timing_enable(int enable) {
+  const int e = tsm::timing_enable(enable);
+  if (e != hipSuccess) return hip_fail(e, "tsm_timing_enable");
+  return TSM_OK;
+}
+
+int tsm_timing_read(double* total_ms, int64_t* launches, int n) {
+  if (n < 0) return fail(TSM_ERR_INVALID, "n < 0");
+  const int e = tsm::timing_read(total_ms, launches, n);
+  if (e != hipSuccess) return hip_fail(e, "tsm_timing_read");
+  return TSM_OK;
+}
+
+int tsm_timing_kernel_count(void) { return tsm::kNumKernels; }
+
+const char* tsm_timing_kernel_name(int kernel_id) { return tsm::timing_name(kernel_id); }
+
 }  // extern "C"

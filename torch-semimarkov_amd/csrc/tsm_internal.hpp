@@ -106,4 +106,40 @@ int launch_viterbi(const Plan& pl, const ViterbiParams& v, int with_traceback, h
 int launch_checkpoints(const float* aval, const double* alvl, const int64_t* lengths, int B, int T,
                        int C, int K, int S, int n_ckpt, float* out, hipStream_t s);
 
+// Opt-in per-kernel timing.  Kernel ids index the totals of timing_read().
+enum KernelId : int {
+  kKScanFwd = 0,
+  kKScanBwd,
+  kKVerify,
+  kKFwdFixup,
+  kKBwdFixup,
+  kKApplyOffsets,
+  kKMarginal,
+  kKFinalizeRows,
+  kKFinalizeShared,
+  kKCheckpoints,
+  kKViterbi,
+  kKBacktrace,
+  kNumKernels
+};
+
+// Brackets the launches made during its lifetime with events on stream `s`
+// (a no-op unless timing is enabled).
+class TimedLaunch {
+ public:
+  TimedLaunch(int id, hipStream_t s);
+  ~TimedLaunch();
+  TimedLaunch(const TimedLaunch&) = delete;
+  TimedLaunch& operator=(const TimedLaunch&) = delete;
+
+ private:
+  int id_;
+  hipStream_t s_;
+  hipEvent_t a_, b_;
+};
+
+int timing_enable(int on);
+int timing_read(double* total_ms, int64_t* launches, int n);
+const char* timing_name(int id);
+
 }  // namespace tsm

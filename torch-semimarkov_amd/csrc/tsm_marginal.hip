@@ -319,7 +319,10 @@ int launch_marg_j(const Plan& pl, const MargParams& q, hipStream_t st) {
   auto k = marginal_kernel<J>;
   hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)pl.marg_lds);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k, dim3(pl.B * pl.NB * pl.NCB), dim3(pl.NTM), pl.marg_lds, st, q);
+  {
+    TimedLaunch tl(kKMarginal, st);
+    hipLaunchKernelGGL(k, dim3(pl.B * pl.NB * pl.NCB), dim3(pl.NTM), pl.marg_lds, st, q);
+  }
   return hipGetLastError();
 }
 
@@ -341,9 +344,15 @@ int launch_marginals(const Plan& pl, const MargParams& q, hipStream_t s) {
 int launch_finalize(const Plan& pl, const FinalParams& f, hipStream_t s) {
   int gx = (int)(((size_t)(pl.T + 1) * pl.C + 255) / 256);
   if (gx > 4096) gx = 4096;
-  hipLaunchKernelGGL(finalize_rows_kernel, dim3(gx, pl.B), dim3(256), 0, s, f);
+  {
+    TimedLaunch tl(kKFinalizeRows, s);
+    hipLaunchKernelGGL(finalize_rows_kernel, dim3(gx, pl.B), dim3(256), 0, s, f);
+  }
   const int n = pl.C * pl.C + pl.K * pl.C;
-  hipLaunchKernelGGL(finalize_shared_kernel, dim3((n + 255) / 256), dim3(256), 0, s, f);
+  {
+    TimedLaunch tl(kKFinalizeShared, s);
+    hipLaunchKernelGGL(finalize_shared_kernel, dim3((n + 255) / 256), dim3(256), 0, s, f);
+  }
   return hipGetLastError();
 }
 
@@ -353,7 +362,10 @@ int launch_checkpoints(const float* aval, const double* alvl, const int64_t* len
   int g = (int)((total + 255) / 256);
   if (g > 8192) g = 8192;
   if (g < 1) g = 1;
-  hipLaunchKernelGGL(checkpoints_kernel, dim3(g), dim3(256), 0, s, aval, alvl, lengths, B, T, C, K, S, n_ckpt, out);
+  {
+    TimedLaunch tl(kKCheckpoints, s);
+    hipLaunchKernelGGL(checkpoints_kernel, dim3(g), dim3(256), 0, s, aval, alvl, lengths, B, T, C, K, S, n_ckpt, out);
+  }
   return hipGetLastError();
 }
 

@@ -744,9 +744,18 @@ int launch_dir(const Plan& pl, const ScanParams& p, bool forward, hipStream_t st
     if (e != hipSuccess) return e;
     e = hipFuncSetAttribute((const void*)k2, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k1, dim3(pl.B * pl.P), dim3(pl.NT), lds, st, p);
-    if (pl.P > 1) hipLaunchKernelGGL(verify_kernel, dim3(pl.B * pl.P), dim3(256), 0, st, p, 1);
-    hipLaunchKernelGGL(k2, dim3(pl.B), dim3(pl.NT), lds, st, p);
+    {
+      TimedLaunch tl(kKScanFwd, st);
+      hipLaunchKernelGGL(k1, dim3(pl.B * pl.P), dim3(pl.NT), lds, st, p);
+    }
+    if (pl.P > 1) {
+      TimedLaunch tl(kKVerify, st);
+      hipLaunchKernelGGL(verify_kernel, dim3(pl.B * pl.P), dim3(256), 0, st, p, 1);
+    }
+    {
+      TimedLaunch tl(kKFwdFixup, st);
+      hipLaunchKernelGGL(k2, dim3(pl.B), dim3(pl.NT), lds, st, p);
+    }
   } else {
     auto k1 = scan_bwd_kernel<J, RMAX, LOGSR, GR>;
     auto k2 = bwd_fixup_kernel<J, RMAX, LOGSR, GR>;
@@ -754,14 +763,24 @@ int launch_dir(const Plan& pl, const ScanParams& p, bool forward, hipStream_t st
     if (e != hipSuccess) return e;
     e = hipFuncSetAttribute((const void*)k2, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k1, dim3(pl.B * pl.P), dim3(pl.NT), lds, st, p);
-    if (pl.P > 1) hipLaunchKernelGGL(verify_kernel, dim3(pl.B * pl.P), dim3(256), 0, st, p, 0);
-    hipLaunchKernelGGL(k2, dim3(pl.B), dim3(pl.NT), lds, st, p);
+    {
+      TimedLaunch tl(kKScanBwd, st);
+      hipLaunchKernelGGL(k1, dim3(pl.B * pl.P), dim3(pl.NT), lds, st, p);
+    }
+    if (pl.P > 1) {
+      TimedLaunch tl(kKVerify, st);
+      hipLaunchKernelGGL(verify_kernel, dim3(pl.B * pl.P), dim3(256), 0, st, p, 0);
+    }
+    {
+      TimedLaunch tl(kKBwdFixup, st);
+      hipLaunchKernelGGL(k2, dim3(pl.B), dim3(pl.NT), lds, st, p);
+    }
   }
   if (p.lvl != nullptr) {
     const int per = 256;
     int gx = (pl.T + 1 + per - 1) / per;
     if (gx > 1024) gx = 1024;
+    TimedLaunch tl(kKApplyOffsets, st);
     hipLaunchKernelGGL(apply_offsets_kernel, dim3(gx, pl.B), dim3(per), 0, st, p, forward ? 1 : 0);
   }
   return hipGetLastError();

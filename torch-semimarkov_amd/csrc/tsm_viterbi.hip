@@ -205,8 +205,14 @@ int launch_vit_j(const Plan& pl, const ViterbiParams& v, int with_tb, hipStream_
   auto k = viterbi_kernel<J, CMAX>;
   hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)L.total);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k, dim3(pl.B), dim3(pl.NT), L.total, st, v);
-  if (with_tb) hipLaunchKernelGGL(backtrace_kernel, dim3((pl.B + 63) / 64), dim3(64), 0, st, v);
+  {
+    TimedLaunch tl(kKViterbi, st);
+    hipLaunchKernelGGL(k, dim3(pl.B), dim3(pl.NT), L.total, st, v);
+  }
+  if (with_tb) {
+    TimedLaunch tl(kKBacktrace, st);
+    hipLaunchKernelGGL(backtrace_kernel, dim3((pl.B + 63) / 64), dim3(64), 0, st, v);
+  }
   return hipGetLastError();
 }
 

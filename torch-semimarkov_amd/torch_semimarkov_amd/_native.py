@@ -44,6 +44,10 @@ _SIGNATURES = {
     "tsm_viterbi": (
         [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _i32, _p, _p, _p, _sz, _p], _i32),
     "tsm_ring_checkpoints": ([_p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p], _i32),
+    "tsm_timing_enable": ([_i32], _i32),
+    "tsm_timing_read": ([ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i64), _i32], _i32),
+    "tsm_timing_kernel_count": ([], _i32),
+    "tsm_timing_kernel_name": ([_i32], ctypes.c_char_p),
 }
 
 EXPORTED = tuple(_SIGNATURES)
@@ -89,3 +93,19 @@ def plan_info(B, T, C, K, has_ps=False, has_pe=False) -> dict:
 def ptr(t) -> int | None:
     """Device address of a tensor (None for a missing optional tensor)."""
     return None if t is None else t.data_ptr()
+
+
+def timing_enable(on: bool = True) -> None:
+    """Start (clearing the totals) or stop per-kernel event timing in the library."""
+    check(lib().tsm_timing_enable(int(on)), "tsm_timing_enable")
+
+
+def timing_read() -> dict:
+    """{kernel name: (total ms, launches)} of the kernels timed since timing_enable(True).
+    Waits for the recorded events."""
+    L = lib()
+    n = L.tsm_timing_kernel_count()
+    ms = (ctypes.c_double * n)()
+    cnt = (_i64 * n)()
+    check(L.tsm_timing_read(ms, cnt, n), "tsm_timing_read")
+    return {L.tsm_timing_kernel_name(i).decode(): (float(ms[i]), int(cnt[i])) for i in range(n) if cnt[i] > 0}
