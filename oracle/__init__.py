@@ -19,10 +19,6 @@ brute
     Independent checks that pin ``streaming_ref``: exhaustive enumeration of
     all segmentations for tiny problems (log Z, Viterbi, exact marginals via
     autograd) and a textbook HMM forward/backward for the K=1 special case.
-native
-    ctypes wrapper around ``oracle/tsm_oracle.c`` -- an fp64 (and fp32) C
-    restatement used where the PyTorch restatement is too slow (full-size
-    configurations).  Pinned against ``streaming_ref`` in the tests.
 
 Pinning status of each function is recorded in each module's docstring.
 """

@@ -163,6 +163,29 @@ CASES = [
     (1, 30, 4, 70, None, False, "log"),         # 4-lane groups
 ]
 
+# Plans outside the register / LDS-ring fast path: more than 32 durations per
+# lane (batched online log-sum-exp, duration bias from LDS) and rings too large
+# for LDS (global-memory rings, the C=128 configuration's path).
+SLOW_PATH_CASES = [
+    (2, 600, 2200, 2, [600, 433], False, "log", dict(RMAX=0, global_rings=0)),
+    (2, 700, 560, 20, [700, 615], False, "log", dict(RMAX=0, global_rings=1)),
+    (1, 200, 64, 128, None, False, "log", dict(RMAX=0, global_rings=1)),
+    (2, 120, 40, 128, [120, 77], True, "max", dict(RMAX=0, global_rings=1)),
+]
+
+
+@pytest.mark.parametrize("B,T,K,C,lengths,proj,sr,plan", SLOW_PATH_CASES)
+def test_generic_scan_paths_vs_fp64_oracle(B, T, K, C, lengths, proj, sr, plan):
+    got = N.plan_info(B, T, C, K, proj, proj)
+    for key, v in plan.items():
+        assert got[key] == v, (key, got)
+    cum, tr, db, L, ps, pe = rand_problem(B, T, K, C, 3000 + T + K + C, lengths, proj)
+    g = torch.linspace(0.5, 2.0, B)
+    p64, g64 = oracle_fp64(cum, tr, db, L, K, sr, ps, pe, g)
+    part, grads = run_hip(cum, tr, db, L, K, sr, ps, pe, g)
+    np.testing.assert_allclose(part.double().numpy(), p64.numpy(), rtol=RTOL_Z, atol=1e-6)
+    assert_grads(grads, g64)
+
 
 @pytest.mark.parametrize("B,T,K,C,lengths,proj,sr", CASES)
 def test_random_problems_vs_fp64_oracle(B, T, K, C, lengths, proj, sr):

@@ -28,8 +28,13 @@ from .constants import NEG_INF
 
 HAS_HIP = os.path.exists(_native.library_path())
 
-# Name of the reference's GPU autograd function, for code written against it.
+# Names of the reference's GPU autograd function and launchers
+# (streaming/__init__.py:136-177), for code written against them.  HAS_TRITON
+# answers the reference's question "is the GPU backend usable", here the HIP one.
 SemiCRFStreamingTriton = SemiCRFStreamingHIP
+launch_streaming_triton_kernel = launch_streaming_hip_kernel
+launch_streaming_triton_backward = launch_streaming_hip_backward
+HAS_TRITON = HAS_HIP
 
 
 def compute_edge_block_streaming(
@@ -67,7 +72,10 @@ __all__ = [
     "compute_edge_block_streaming",
     "launch_streaming_hip_kernel",
     "launch_streaming_hip_backward",
+    "launch_streaming_triton_kernel",
+    "launch_streaming_triton_backward",
     "_compute_checkpoint_interval",
     "NEG_INF",
     "HAS_HIP",
+    "HAS_TRITON",
 ]
