@@ -90,6 +90,17 @@ def run_hip(cum, tr, db, L, K, semiring="log", ps=None, pe=None, g=None):
     return part.detach().cpu(), [x.cpu() for x in grads]
 
 
+@pytest.fixture(params=["fast", "generic"])
+def scan_path(request, monkeypatch):
+    """Run a test on the register-resident log-semiring scan (where the plan
+    allows it) and again with TSM_SCAN_PATH=generic on the generic kernels."""
+    if request.param == "generic":
+        monkeypatch.setenv("TSM_SCAN_PATH", "generic")
+    else:
+        monkeypatch.delenv("TSM_SCAN_PATH", raising=False)
+    return request.param
+
+
 def assert_grads(got, want, tol=GRAD_TOL):
     for a, b in zip(got, want):
         np.testing.assert_allclose(a.double().numpy(), b.double().numpy(), **tol)
@@ -97,7 +108,7 @@ def assert_grads(got, want, tol=GRAD_TOL):
 
 # --------------------------------------------------------------------------- golden vectors
 @pytest.mark.parametrize("name", STREAM_FIXTURES)
-def test_forward_backward_match_reference_golden(name):
+def test_forward_backward_match_reference_golden(name, scan_path):
     z = load_golden(name)
     cum, tr, db, L, K, sr, ps, pe = fixture_inputs(z, requires_grad=True)
     part = tsa.semi_crf_streaming_forward(cum, tr, db, L, K, semiring=sr, proj_start=ps, proj_end=pe)
@@ -175,7 +186,8 @@ SLOW_PATH_CASES = [
 
 
 @pytest.mark.parametrize("B,T,K,C,lengths,proj,sr,plan", SLOW_PATH_CASES)
-def test_generic_scan_paths_vs_fp64_oracle(B, T, K, C, lengths, proj, sr, plan):
+def test_generic_scan_paths_vs_fp64_oracle(B, T, K, C, lengths, proj, sr, plan, monkeypatch):
+    monkeypatch.setenv("TSM_SCAN_PATH", "generic")
     got = N.plan_info(B, T, C, K, proj, proj)
     for key, v in plan.items():
         assert got[key] == v, (key, got)
@@ -188,7 +200,7 @@ def test_generic_scan_paths_vs_fp64_oracle(B, T, K, C, lengths, proj, sr, plan):
 
 
 @pytest.mark.parametrize("B,T,K,C,lengths,proj,sr", CASES)
-def test_random_problems_vs_fp64_oracle(B, T, K, C, lengths, proj, sr):
+def test_random_problems_vs_fp64_oracle(B, T, K, C, lengths, proj, sr, scan_path):
     cum, tr, db, L, ps, pe = rand_problem(B, T, K, C, 1000 + T + K + C, lengths, proj)
     g = torch.linspace(0.5, 2.0, B)
     p64, g64 = oracle_fp64(cum, tr, db, L, K, sr, ps, pe, g)
@@ -199,7 +211,7 @@ def test_random_problems_vs_fp64_oracle(B, T, K, C, lengths, proj, sr):
 
 
 @pytest.mark.parametrize("lengths", [[2600, 1900], [2600, 1560]])
-def test_chunked_scan_vs_fp64_oracle(lengths):
+def test_chunked_scan_vs_fp64_oracle(lengths, scan_path):
     """T long enough for several speculative chunks (warm-up + verification); the
     second case has lengths that are exact multiples of the chunk length (520)."""
     B, T, K, C = 2, 2600, 8, 4
@@ -213,7 +225,7 @@ def test_chunked_scan_vs_fp64_oracle(lengths):
     assert_grads(grads, g64)
 
 
-def test_verifier_recomputes_non_mixing_chunks():
+def test_verifier_recomputes_non_mixing_chunks(scan_path):
     """Sticky transitions keep early evidence alive across chunk boundaries, so
     the warmed-up states disagree with the exact ones and chunks are recomputed
     from the previous chunk's exact state; results still match the oracle."""
@@ -236,7 +248,7 @@ def test_verifier_recomputes_non_mixing_chunks():
     assert_grads(grads, g64)
 
 
-def test_grad_output_weighting_and_isolation():
+def test_grad_output_weighting_and_isolation(scan_path):
     """tests/test_streaming_triton.py:901-1087: shared grads are sum_b g_b * grad_b, per-sequence
     grads are scaled, a zero weight isolates a sequence."""
     cum, tr, db, L, _, _ = rand_problem(2, 30, 5, 4, 9, [30, 22])
@@ -248,7 +260,7 @@ def test_grad_output_weighting_and_isolation():
         torch.testing.assert_close(gh[i], 0.5 * ga[i] + 2.0 * gb[i], rtol=1e-5, atol=1e-6)
 
 
-def test_deterministic_bitwise():
+def test_deterministic_bitwise(scan_path):
     cum, tr, db, L, ps, pe = rand_problem(3, 300, 10, 6, 3, [300, 250, 10], proj=True)
     a = run_hip(cum, tr, db, L, 10, ps=ps, pe=pe)
     b = run_hip(cum, tr, db, L, 10, ps=ps, pe=pe)
@@ -257,7 +269,7 @@ def test_deterministic_bitwise():
         assert torch.equal(x, y)
 
 
-def test_k1_full_size_config2_vs_hmm():
+def test_k1_full_size_config2_vs_hmm(scan_path):
     """Config 2 of the benchmark set (B=32, T=10^4, C=8, K=1) against a probability-space HMM in fp64."""
     B, T, C, K = 32, 10_000, 8, 1
     g = torch.Generator().manual_seed(20261202)
@@ -381,3 +393,4 @@ def test_kernel_timing_counts_launches():
     part = tsa.semi_crf_streaming_forward(cum.detach(), tr.detach(), db.detach(), L, K, semiring=sr)
     torch.cuda.synchronize()
     assert N.timing_read() == {}
+

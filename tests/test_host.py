@@ -173,3 +173,11 @@ def test_kernel_timing_interface_without_gpu():
     assert N.timing_read() == {}
     N.timing_enable(False)
     assert lib.tsm_timing_read(None, None, -1) == 1
+
+
+def test_fast_path_is_planned_for_the_benchmark_shapes():
+    """The log-semiring scans of the benchmark configurations run on the
+    register-resident kernels (the generic kernels remain for the max
+    semiring, very large label sets and tests)."""
+    for B, T, C, K in ((1, 1_000_000, 24, 300), (4, 1000, 24, 100), (32, 10_000, 8, 1), (64, 8192, 32, 64)):
+        assert N.plan_info(B, T, C, K)["fast"] == 1, (B, T, C, K)

@@ -52,7 +52,9 @@ def build(arch: str = "gfx950", jobs: int = 4, verbose: bool = False) -> str:
     cc = hipcc()
     os.makedirs(BUILD_DIR, exist_ok=True)
     os.makedirs(OUT_DIR, exist_ok=True)
-    srcs = sorted(f for f in os.listdir(CSRC) if f.endswith(".hip"))
+    # largest translation units first so the parallel build ends together
+    srcs = sorted((f for f in os.listdir(CSRC) if f.endswith(".hip")),
+                  key=lambda f: (-os.path.getsize(os.path.join(CSRC, f)), f))
     objs = []
     cmds = []
     for f in srcs:
@@ -72,7 +74,7 @@ def build(arch: str = "gfx950", jobs: int = 4, verbose: bool = False) -> str:
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--arch", default="gfx950")
-    ap.add_argument("--jobs", type=int, default=4)
+    ap.add_argument("--jobs", type=int, default=min(8, os.cpu_count() or 4))
     ap.add_argument("-v", "--verbose", action="store_true")
     a = ap.parse_args()
     print(build(a.arch, a.jobs, a.verbose))

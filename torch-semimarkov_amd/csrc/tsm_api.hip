@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include <math.h>
+#include <stdlib.h>
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
@@ -66,6 +67,55 @@ int pow2_lanes(int C) {
 }
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// (lanes per label, durations per lane) pairs compiled for the fast scan
+// (tsm_fast_j*.hip).
+bool fast_instantiated(int J, int R) {
+  if (R < 1) return false;
+  switch (J) {
+    case 8:
+    case 32: return R <= 16 || R == 20 || R == 24 || R == 28 || R == 32;
+    case 16: return R <= 32;
+    case 64: return R <= 8;
+    default: return false;
+  }
+}
+
+// Register-resident log-semiring scan: pick the lane-group size J whose padded
+// duration range and wave count give the least work per step; leave p.fast = 0
+// when no instance fits.  TSM_SCAN_PATH=generic in the environment disables
+// the fast path (used by the tests to exercise the generic kernels).
+void plan_fast(Plan& p, const DeviceInfo& di) {
+  p.fast = 0;
+  const char* env = getenv("TSM_SCAN_PATH");
+  if (env != nullptr && strcmp(env, "generic") == 0) return;
+  double best = 1e300;
+  for (int J : {8, 16, 32, 64}) {
+    if (p.C > 4 * J) continue;  // the label mix handles at most 4 labels per lane
+    int R = (p.Kmax + J - 1) / J;
+    while (R <= 32 && !fast_instantiated(J, R)) ++R;
+    if (R > 32) continue;
+    const int NT = (int)cdiv((int64_t)p.C * J, 64) * 64;
+    if (NT > (R > 16 ? 512 : 1024)) continue;  // the kernels' launch bounds
+    const int KP = J * R;
+    const int RS = std::max(p.Kmax + 2, KP + 1);
+    int RL = RS + KP;
+    while (RL % 32 != J % 32) ++RL;  // label rows of a half-wave start on distinct banks
+    const size_t lds = tsm::fast_lds_layout(p.C, RL, RS).total;
+    if (lds > (size_t)di.max_lds) continue;
+    const double cost = (double)((NT / 64 + 3) / 4) * (R + 12);  // waves per SIMD x work per wave
+    if (cost < best) {
+      best = cost;
+      p.fast = 1;
+      p.FJ = J;
+      p.FR = R;
+      p.FNT = NT;
+      p.FRS = RS;
+      p.FRL = RL;
+      p.fast_lds = lds;
+    }
+  }
+}
 
 // Thread mapping, rings, chunking and marginal blocking for a problem shape.
 int make_plan(int64_t B, int64_t T, int64_t C, int64_t K, int has_ps, int has_pe, Plan* out) {
@@ -145,6 +195,7 @@ int make_plan(int64_t B, int64_t T, int64_t C, int64_t K, int has_ps, int has_pe
   }
   p.NB = (int)NB;
   p.TB = (int)TB;
+  plan_fast(p, di);
   *out = p;
   return TSM_OK;
 }
@@ -271,7 +322,8 @@ int tsm_plan_info(int64_t B, int64_t T, int64_t C, int64_t K, int has_ps, int ha
   if (!out) return fail(TSM_ERR_INVALID, "out is NULL");
   const DeviceInfo di = device_info();
   const int64_t vals[] = {p.J, p.NT, p.RS, p.P, p.Lc, p.W, p.global_rings, (int64_t)p.scan_lds, p.NB, p.TB,
-                          p.CB, p.NCB, p.JM, p.NTM, (int64_t)p.marg_lds, p.Kmax, di.n_cu, p.R, p.KP, p.RMAX};
+                          p.CB, p.NCB, p.JM, p.NTM, (int64_t)p.marg_lds, p.Kmax, di.n_cu, p.R, p.KP, p.RMAX,
+                          p.fast, p.FJ, p.FR, p.FNT, (int64_t)p.fast_lds};
   const int m = (int)(sizeof(vals) / sizeof(vals[0]));
   for (int i = 0; i < n && i < m; ++i) out[i] = vals[i];
   return TSM_OK;

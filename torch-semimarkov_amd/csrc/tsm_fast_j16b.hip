@@ -1,0 +1,33 @@
+// Register-resident scan instances: 16-lane label groups, 17-32 durations per lane.
+// (Split across files so the instances compile in parallel.)
+#include "tsm_fastscan.hpp"
+
+namespace tsm {
+
+int launch_fast_j16_hi(const Plan& pl, const ScanParams& p, bool fwd, hipStream_t st) {
+  switch (pl.FR) {
+    case 17: return fastscan::launch_fast_jr<16, 17>(pl, p, fwd, st);
+    case 18: return fastscan::launch_fast_jr<16, 18>(pl, p, fwd, st);
+    case 19: return fastscan::launch_fast_jr<16, 19>(pl, p, fwd, st);
+    case 20: return fastscan::launch_fast_jr<16, 20>(pl, p, fwd, st);
+    case 21: return fastscan::launch_fast_jr<16, 21>(pl, p, fwd, st);
+    case 22: return fastscan::launch_fast_jr<16, 22>(pl, p, fwd, st);
+    case 23: return fastscan::launch_fast_jr<16, 23>(pl, p, fwd, st);
+    case 24: return fastscan::launch_fast_jr<16, 24>(pl, p, fwd, st);
+    case 25: return fastscan::launch_fast_jr<16, 25>(pl, p, fwd, st);
+    case 26: return fastscan::launch_fast_jr<16, 26>(pl, p, fwd, st);
+    case 27: return fastscan::launch_fast_jr<16, 27>(pl, p, fwd, st);
+    case 28: return fastscan::launch_fast_jr<16, 28>(pl, p, fwd, st);
+    case 29: return fastscan::launch_fast_jr<16, 29>(pl, p, fwd, st);
+    case 30: return fastscan::launch_fast_jr<16, 30>(pl, p, fwd, st);
+    case 31: return fastscan::launch_fast_jr<16, 31>(pl, p, fwd, st);
+    case 32: return fastscan::launch_fast_jr<16, 32>(pl, p, fwd, st);
+    default: return (int)hipErrorInvalidValue;
+  }
+}
+
+int launch_fast_j16(const Plan& pl, const ScanParams& p, bool fwd, hipStream_t st) {
+  return pl.FR <= 16 ? launch_fast_j16_lo(pl, p, fwd, st) : launch_fast_j16_hi(pl, p, fwd, st);
+}
+
+}  // namespace tsm

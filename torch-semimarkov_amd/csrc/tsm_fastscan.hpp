@@ -1,0 +1,406 @@
+// Register-resident log-semiring scan (forward alpha / backward beta) for gfx950.
+//
+// Same recursion, chunking and verification as the generic scan, with a data
+// layout that makes one duration term cost one 8-byte LDS read, four VALU
+// operations and one exponential:
+//
+//   * a group of J lanes serves one label c; lane j owns durations
+//     k = 1 + j + J*r, r < R, with R a compile-time constant (padded
+//     durations are masked through the duration bias register);
+//   * the ring of label c holds, per position s, one fp64 value
+//       x[s] = lvl[s] + v[s] - sgn*cum[s,c]*log2(e)
+//     (v = normalised state plus the projection a segment starting / ending at
+//     s contributes, lvl = the position's fp64 level), so the term of duration
+//     k at step t is x[s] + db[k] + sgn*cum[t,c]*log2(e) with s = t -/+ k;
+//   * a lane sums its terms in one pass relative to its first term y0,
+//     exp2((float)((x + db) - y0)) -- the large parts cancel in fp64 and only
+//     the small exponent is rounded to fp32 (exact fallback to a two-pass
+//     maximum when the sum overflows) -- then the J lanes combine;
+//   * the ring of label c is read and written only by c's lane group, which
+//     lives in one wavefront, so the only cross-wave exchange per step is the
+//     row of all labels' results: one LDS barrier per step.
+//
+// sgn = +1 forward (content cum[t]-cum[t-k]), -1 backward (cum[t+k]-cum[t]).
+#pragma once
+
+#include <float.h>
+
+#include "tsm_scan_common.hpp"
+
+namespace tsm {
+namespace fastscan {
+
+using namespace scan_detail;
+
+constexpr double kInvD = -1e30;  // ring value of a position that does not exist
+constexpr int kCJ = 4;           // labels per lane in the label mix (plans keep C <= 4*J)
+constexpr double kLog2eD = 1.4426950408889634;
+
+// Wait for this wave's LDS operations, then barrier.  Global loads in flight
+// (next-step prefetches) stay in flight.
+__device__ __forceinline__ void lds_barrier() { __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// Compiler-only ordering point between a wave's LDS writes and its later reads
+// of the same words by other lanes (LDS executes a wave's operations in order).
+__device__ __forceinline__ void wave_lds_order() { __asm__ volatile("" ::: "memory"); }
+
+template <bool FWD>
+__device__ __forceinline__ int slot_of(int pos, int RS) {
+  return FWD ? RS - 1 - pos % RS : pos % RS;
+}
+
+__device__ __forceinline__ void ring_put(double* ring_c, int a, double x, int RS, int KP) {
+  ring_c[a] = x;
+  if (a < KP) ring_c[a + RS] = x;
+}
+
+template <int J, int R, bool FWD>
+struct Chunk {
+  // ---------------------------------------------------------------------------
+  // One chunk of one sequence.
+  //   FWD: mode 0 exact from position 0; 1 speculative from t_lo - W; 2 exact
+  //        from (init_st, init_lv) at t_lo.  Steps t = t_start+1 .. t_hi.
+  //   BWD: mode 0 exact from position len; 1 speculative from t_hi + W; 2 exact
+  //        from the state at t_hi.  Steps t = t_start-1 .. t_lo.
+  // ---------------------------------------------------------------------------
+  __device__ static void run(const ScanParams& p, char* smem, int b, int j, int mode, const float* init_st,
+                             const double* init_lv) {
+    constexpr int KP = J * R;
+    const int C = p.C, Kmax = p.Kmax, K = p.K, RS = p.RS, RL = p.RL, T = p.T;
+    const int len = seq_len(p, b);
+    const int item = b * p.P + j;
+    const FastLds L = fast_lds_layout(C, RL, RS);
+    double* ring = reinterpret_cast<double*>(smem + L.ring);
+    double* lring = reinterpret_cast<double*>(smem + L.lring);
+    float* row = reinterpret_cast<float*>(smem + L.row);
+    const int tid = threadIdx.x, NT = blockDim.x;
+    const int g = tid / J, lj = tid % J;
+    const bool cval = g < C;
+    const int c = cval ? g : C - 1;  // padding groups shadow the last label and never write
+    const float* cum_b = p.cum + (size_t)b * (T + 1) * C;
+    const bool has_ps = p.ps != nullptr, has_pe = p.pe != nullptr;
+    const float* ps_b = has_ps ? p.ps + (size_t)b * T * C : nullptr;
+    const float* pe_b = has_pe ? p.pe + (size_t)b * T * C : nullptr;
+    const bool store = p.val != nullptr;
+    const double sgn = FWD ? 1.0 : -1.0;
+    // fp64 cumulative score of position pos (own label) in log2 units, times sgn
+    auto cumx = [&](int pos) { return sgn * (double)cum_b[(size_t)pos * C + c] * kLog2eD; };
+
+    int t_lo, t_hi, t_start, jl = 0;
+    if (FWD) {
+      t_lo = j * p.Lc;
+      t_hi = min(t_lo + p.Lc, len);
+      t_start = mode == 0 ? 0 : (mode == 1 ? t_lo - p.W : t_lo);
+    } else {
+      jl = bwd_last_chunk(p, len);
+      t_lo = j * p.Lc;
+      t_hi = (j == jl) ? len : (j + 1) * p.Lc;
+      t_start = mode == 0 ? len : (mode == 1 ? t_hi + p.W : t_hi);
+    }
+
+    // ---- per-lane constants ----
+    double dbr[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int k = 1 + lj + J * r;
+      const int di = k < K - 1 ? k : K - 1;
+      dbr[r] = (k <= Kmax) ? (double)(p.db[(size_t)di * C + c] * kLog2e) : kInvD;
+    }
+    float trr[kCJ];
+#pragma unroll
+    for (int i = 0; i < kCJ; ++i) {
+      const int ci = lj + J * i;
+      // forward mix: own label c is the destination, ci the source; backward: c is the source
+      trr[i] = (ci < C) ? (FWD ? p.trans[(size_t)ci * C + c] : p.trans[(size_t)c * C + ci]) * kLog2e : 0.0f;
+    }
+
+    // ---- empty rings ----
+    for (int idx = tid; idx < C * RL; idx += NT) ring[idx] = kInvD;
+    for (int i = tid; i < RS; i += NT) lring[i] = 0.0;
+    __syncthreads();
+
+    double* rc = ring + (size_t)c * RL;
+    double lvl_prev;
+    // ---- initial state ----
+    if (mode == 0) {
+      const int pos = t_start;  // FWD: 0, BWD: len
+      lvl_prev = 0.0;
+      float v0;
+      if (FWD) {
+        // alpha-hat[0] = 0 for every label; u[0,c] = (+)_{c'} trans[c',c]
+        float m = kMinusInf;
+#pragma unroll
+        for (int i = 0; i < kCJ; ++i)
+          if (lj + J * i < C) m = fmax2(m, trr[i]);
+        float sm = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kCJ; ++i)
+          if (lj + J * i < C) sm += exp2_hw(trr[i] - m);
+        const float u0 = group_lse2<J>(m, sm);
+        v0 = u0 + ((has_ps && T > 0) ? ps_b[c] * kLog2e : 0.0f);
+        if (g == 0) {
+#pragma unroll
+          for (int i = 0; i < kCJ; ++i) {
+            const int ci = lj + J * i;
+            if (ci < C) {
+              if (store && j == 0) p.val[((size_t)b * (T + 1)) * C + ci] = 0.0f;
+              if (len == 0) p.fin[(size_t)b * C + ci] = 0.0f;
+            }
+          }
+        }
+        if (tid == 0) {
+          if (store && j == 0) p.lvl[(size_t)b * (T + 1)] = 0.0;
+          if (len == 0) p.fin_lvl[b] = 0.0;
+        }
+      } else {
+        v0 = (has_pe && len >= 1) ? pe_b[(size_t)(len - 1) * C + c] * kLog2e : 0.0f;
+        if (cval && lj == 0 && store) p.val[((size_t)b * (T + 1) + len) * C + c] = 0.0f;
+        if (tid == 0 && store) p.lvl[(size_t)b * (T + 1) + len] = 0.0;
+      }
+      if (cval && lj == 0) ring_put(rc, slot_of<FWD>(pos, RS), (double)v0 - cumx(pos), RS, KP);
+      if (tid == 0) lring[pos % RS] = 0.0;
+    } else {
+      lvl_prev = (mode == 1) ? 0.0 : init_lv[0];
+      // positions t_start -/+ i, i < Kmax
+      if (cval) {
+        for (int i = lj; i < Kmax; i += J) {
+          const int pos = FWD ? t_start - i : t_start + i;
+          float v;
+          if (mode == 1) {
+            if (FWD) v = has_ps ? ps_b[(size_t)pos * C + c] * kLog2e : 0.0f;
+            else v = has_pe ? pe_b[(size_t)(pos - 1) * C + c] * kLog2e : 0.0f;
+          } else {
+            v = init_st[(size_t)i * C + c];
+          }
+          const double lv = (mode == 1) ? 0.0 : init_lv[i];
+          ring_put(rc, slot_of<FWD>(pos, RS), lv + (double)v - cumx(pos), RS, KP);
+        }
+      }
+      for (int i = tid; i < Kmax; i += NT) {
+        const int pos = FWD ? t_start - i : t_start + i;
+        lring[pos % RS] = (mode == 1) ? 0.0 : init_lv[i];
+      }
+    }
+    __syncthreads();
+
+    // ---- per-step operands, prefetched one step ahead ----
+    const int dir = FWD ? 1 : -1;
+    const int t_first = t_start + dir;
+    const int t_end = FWD ? t_hi + 1 : t_lo - 1;  // exclusive
+    auto clampT = [&](int t) { return t < 0 ? 0 : (t > T ? T : t); };
+    auto clampT1 = [&](int t) { return t < 0 ? 0 : (t > T - 1 ? T - 1 : t); };
+    // projection operands: forward adds proj_end[t-1] to the pull and proj_start[t]
+    // to the ring entry; backward adds proj_start[t] to the pull and proj_end[t-1]
+    // to the ring entry.  Absent projections read cum and are scaled by 0.
+    const float* pa_src = FWD ? (has_pe ? pe_b : cum_b) : (has_ps ? ps_b : cum_b);
+    const float* pb_src = FWD ? (has_ps ? ps_b : cum_b) : (has_pe ? pe_b : cum_b);
+    const float pa_scale = (FWD ? has_pe : has_ps) ? kLog2e : 0.0f;
+    const float pb_scale = (FWD ? has_ps : has_pe) ? kLog2e : 0.0f;
+    auto pa_row = [&](int t) { return FWD ? clampT1(t - 1) : clampT1(t); };
+    auto pb_row = [&](int t) { return FWD ? clampT1(t) : clampT1(t - 1); };
+    float cum_n = cum_b[(size_t)clampT(t_first) * C + c];
+    float pa_n = pa_src[(size_t)pa_row(t_first) * C + c];
+    float pb_n = pb_src[(size_t)pb_row(t_first) * C + c];
+
+    const int rec_spec = (mode == 1) ? (FWD ? t_lo : t_hi) : -1;
+    const int rec_end = FWD ? ((t_hi < len) ? t_hi : -1) : ((j >= 1) ? t_lo : -1);
+
+    for (int t = t_first; t != t_end; t += dir) {
+      const double cx_t = sgn * (double)cum_n * kLog2eD;
+      const float pa_t = pa_n * ((FWD ? t >= 1 : true) ? pa_scale : 0.0f);
+      const float pb_t = pb_n * ((FWD ? true : t >= 1) ? pb_scale : 0.0f);
+      {
+        const int tn = t + dir;
+        cum_n = cum_b[(size_t)clampT(tn) * C + c];
+        pa_n = pa_src[(size_t)pa_row(tn) * C + c];
+        pb_n = pb_src[(size_t)pb_row(tn) * C + c];
+      }
+      const int A = slot_of<FWD>(t, RS);
+
+      // ---- pull over the lane's durations ----
+      const double* rb = rc + A + 1 + lj;
+      double e[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) e[r] = rb[J * r];
+      double y0 = e[0] + dbr[0];
+      float s = 1.0f;
+#pragma unroll
+      for (int r = 1; r < R; ++r) s += exp2_hw((float)((e[r] + dbr[r]) - y0));
+      if (__ballot(!(s <= FLT_MAX))) {
+        // a later term exceeds the first by more than the fp32 exponent range
+        double m = y0;
+#pragma unroll
+        for (int r = 1; r < R; ++r) m = fmax(m, e[r] + dbr[r]);
+        s = 0.0f;
+#pragma unroll
+        for (int r = 0; r < R; ++r) s += exp2_hw((float)((e[r] + dbr[r]) - m));
+        y0 = m;
+      }
+      // the lane's terms relative to the previous position's level, combined over the group
+      const float a2 = group_lse2<J>((float)((y0 + cx_t) - lvl_prev), s) + pa_t;
+      const int par = t & 1;
+      if (cval && lj == 0) row[par * C + c] = a2;
+      lds_barrier();
+
+      // ---- all labels: normaliser and label mix ----
+      float rv[kCJ];
+      float ml = kMinusInf;
+#pragma unroll
+      for (int i = 0; i < kCJ; ++i) {
+        const int ci = lj + J * i;
+        rv[i] = (ci < C) ? row[par * C + ci] : kMinusInf;
+        ml = fmax2(ml, rv[i]);
+      }
+      const float mx = group_max<J>(ml);
+      const double lvl_t = lvl_prev + (double)mx;
+      float mq = kMinusInf;
+#pragma unroll
+      for (int i = 0; i < kCJ; ++i)
+        if (lj + J * i < C) mq = fmax2(mq, (rv[i] - mx) + trr[i]);
+      float sq = 0.0f;
+#pragma unroll
+      for (int i = 0; i < kCJ; ++i)
+        if (lj + J * i < C) sq += exp2_hw(((rv[i] - mx) + trr[i]) - mq);
+      const float mixv = group_lse2<J>(mq, sq);
+
+      const bool owned = FWD ? (j == 0 || t > t_lo) : (t < t_hi || j == jl);
+      if (FWD) {
+        if (g == 0) {
+#pragma unroll
+          for (int i = 0; i < kCJ; ++i) {
+            const int ci = lj + J * i;
+            if (ci < C) {
+              const float ah = rv[i] - mx;
+              if (store && owned) p.val[((size_t)b * (T + 1) + t) * C + ci] = ah;
+              if (t == len) p.fin[(size_t)b * C + ci] = ah;
+            }
+          }
+        }
+        if (tid == 0) {
+          if (store && owned) p.lvl[(size_t)b * (T + 1) + t] = lvl_t;
+          if (t == len) p.fin_lvl[b] = lvl_t;
+        }
+      } else {
+        if (cval && lj == 0 && store && owned) p.val[((size_t)b * (T + 1) + t) * C + c] = mixv;
+        if (tid == 0 && store && owned) p.lvl[(size_t)b * (T + 1) + t] = lvl_t;
+      }
+      // ---- ring entry for position t ----
+      if (cval && lj == 0) ring_put(rc, A, (lvl_t + (double)(mixv + pb_t)) - cx_t, RS, KP);
+      if (tid == 0) lring[t % RS] = lvl_t;
+      lvl_prev = lvl_t;
+      wave_lds_order();
+
+      // ---- boundary states for verification: positions t -/+ i, i < Kmax ----
+      if (t == rec_spec || t == rec_end) {
+        float* st = (t == rec_spec ? p.st_spec : p.st_end) + (size_t)item * Kmax * C;
+        double* lv = (t == rec_spec ? p.lv_spec : p.lv_end) + (size_t)item * Kmax;
+        if (cval) {
+          for (int i = lj; i < Kmax; i += J) {
+            const int pos = FWD ? t - i : t + i;
+            const double x = rc[A + i];
+            const double lp = (i == 0) ? lvl_t : lring[pos % RS];
+            // positions outside the sequence keep the "does not exist" marker
+            st[(size_t)i * C + c] = (x < -1e29) ? -1e30f : (float)((x - lp) + cumx(pos));
+          }
+        }
+        for (int i = tid; i < Kmax; i += NT) {
+          const int pos = FWD ? t - i : t + i;
+          lv[i] = (i == 0) ? lvl_t : lring[pos % RS];
+        }
+      }
+    }
+  }
+};
+
+// Parallel pass (phase 0: one block per chunk) and sequential verification /
+// repair (phase 1: one block per sequence) of one direction.
+template <int J, int R, bool FWD>
+__global__ void __launch_bounds__(R > 16 ? 512 : 1024) fast_scan_kernel(ScanParams p, int phase) {
+  extern __shared__ __align__(16) char smem[];
+  if (phase == 0) {
+    const int b = blockIdx.x / p.P, j = blockIdx.x % p.P;
+    const int len = seq_len(p, b);
+    const int item = b * p.P + j;
+    if (FWD ? (j > 0 && j * p.Lc >= len) : (j > bwd_last_chunk(p, len))) {
+      if (threadIdx.x == 0) p.status[item] = -1;  // empty chunk
+      return;
+    }
+    const int mode = (FWD ? fwd_spec(p, j) : bwd_spec(p, j, len)) ? 1 : 0;
+    if (threadIdx.x == 0) p.status[item] = mode;
+    Chunk<J, R, FWD>::run(p, smem, b, j, mode, nullptr, nullptr);
+    return;
+  }
+  const int b = blockIdx.x;
+  const int len = seq_len(p, b);
+  const FastLds L = fast_lds_layout(p.C, p.RL, p.RS);
+  double* red = reinterpret_cast<double*>(smem + L.red);
+  const int Kmax = p.Kmax, C = p.C;
+  double F = 0.0;
+  int n_re = 0;
+  bool prev_recomputed = false;
+  const int jl = bwd_last_chunk(p, len);
+  const int nch = len == 0 ? 1 : (len + p.Lc - 1) / p.Lc;
+  if (threadIdx.x == 0) p.offs[(size_t)b * p.P + (FWD ? 0 : jl)] = 0.0;
+  for (int j = FWD ? 1 : jl - 1; FWD ? j < nch : j >= 0; j += FWD ? 1 : -1) {
+    const int item = b * p.P + j;
+    if (!(FWD ? fwd_spec(p, j) : bwd_spec(p, j, len))) {
+      F = 0.0;  // the chunk ran exactly from the sequence end
+      prev_recomputed = false;
+    } else {
+      const size_t e = FWD ? (size_t)(item - 1) : (size_t)(item + 1), sp = (size_t)item;
+      double dmax, dmin;
+      if (!prev_recomputed) {
+        // measured in parallel by verify_kernel against the neighbour's original end state
+        dmax = p.vstat[2 * sp];
+        dmin = p.vstat[2 * sp + 1];
+      } else {
+        // the neighbour was recomputed here: its end state changed, measure again
+        double hi, lo;
+        boundary_spread_part(p, e, sp, hi, lo);
+        block_minmax(hi, lo, red, dmax, dmin);
+      }
+      if (dmax - dmin <= (double)p.tol) {
+        F += 0.5 * (dmax + dmin);
+        prev_recomputed = false;
+      } else {
+        Chunk<J, R, FWD>::run(p, smem, b, j, 2, p.st_end + e * Kmax * C, p.lv_end + e * Kmax);
+        __syncthreads();
+        ++n_re;
+        prev_recomputed = true;
+        if (threadIdx.x == 0) p.status[item] = 2;
+      }
+    }
+    if (threadIdx.x == 0) p.offs[(size_t)item] = F;
+  }
+  __syncthreads();
+  if (FWD) {
+    finish_partition<true>(p, b, len, F, n_re);
+  } else if (threadIdx.x == 0 && p.recomputed != nullptr) {
+    p.recomputed[b] = n_re;
+  }
+}
+
+// Launch of one direction: parallel pass, verification, sequential repair, level offsets.
+template <int J, int R>
+int launch_fast_jr(const Plan& pl, const ScanParams& p, bool fwd, hipStream_t st) {
+  auto k = fwd ? fast_scan_kernel<J, R, true> : fast_scan_kernel<J, R, false>;
+  const size_t lds = pl.fast_lds;
+  hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (e != hipSuccess) return e;
+  {
+    TimedLaunch tl(fwd ? kKScanFwd : kKScanBwd, st);
+    hipLaunchKernelGGL(k, dim3(pl.B * pl.P), dim3(pl.FNT), lds, st, p, 0);
+  }
+  e = (hipError_t)launch_verify(pl, p, fwd, st);
+  if (e != hipSuccess) return e;
+  {
+    TimedLaunch tl(fwd ? kKFwdFixup : kKBwdFixup, st);
+    hipLaunchKernelGGL(k, dim3(pl.B), dim3(pl.FNT), lds, st, p, 1);
+  }
+  e = (hipError_t)launch_apply_offsets(pl, p, fwd, st);
+  if (e != hipSuccess) return e;
+  return hipGetLastError();
+}
+
+}  // namespace fastscan
+}  // namespace tsm

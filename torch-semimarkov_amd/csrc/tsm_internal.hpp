@@ -99,6 +99,16 @@ struct ViterbiParams {
 
 // launchers (return hipError_t as int)
 int launch_scan_forward(const Plan& pl, const ScanParams& p, int semiring, hipStream_t s);
+// verification of speculative chunk boundaries / level offsets (shared by both scan paths)
+int launch_verify(const Plan& pl, const ScanParams& p, bool forward, hipStream_t s);
+int launch_apply_offsets(const Plan& pl, const ScanParams& p, bool forward, hipStream_t s);
+// register-resident log-semiring scan, one entry per lane-group size (pl.FJ)
+int launch_fast_j8(const Plan& pl, const ScanParams& p, bool forward, hipStream_t s);
+int launch_fast_j16(const Plan& pl, const ScanParams& p, bool forward, hipStream_t s);
+int launch_fast_j16_lo(const Plan& pl, const ScanParams& p, bool forward, hipStream_t s);
+int launch_fast_j16_hi(const Plan& pl, const ScanParams& p, bool forward, hipStream_t s);
+int launch_fast_j32(const Plan& pl, const ScanParams& p, bool forward, hipStream_t s);
+int launch_fast_j64(const Plan& pl, const ScanParams& p, bool forward, hipStream_t s);
 int launch_scan_backward(const Plan& pl, const ScanParams& p, int semiring, hipStream_t s);
 int launch_marginals(const Plan& pl, const MargParams& q, hipStream_t s);
 int launch_finalize(const Plan& pl, const FinalParams& f, hipStream_t s);

@@ -25,9 +25,37 @@ struct Plan {
   int JM, NTM;       // marginal: lanes per label, threads per block
   size_t marg_lds;   // dynamic LDS bytes of the marginal kernel
   int has_ps, has_pe;
+  // register-resident log-semiring scan ("fast" path), used when fast == 1:
+  // FJ lanes per label, FR durations per lane (compile-time), FNT threads,
+  // FRS ring slots, FRL ring row length (float2 elements), fast_lds bytes
+  int fast, FJ, FR, FNT, FRS, FRL;
+  size_t fast_lds;
 };
 
 __host__ __device__ inline size_t align16(size_t x) { return (x + 15) & ~size_t(15); }
+
+// ---- fast scan LDS layout ---------------------------------------------------
+// One ring per label of RL fp64 entries: slot s < RS plus a mirror of slots
+// s < KP at s + RS.  Entry = level + normalised state (+ folded projection)
+// - sgn * cumulative score, all in log2 units.
+struct FastLds {
+  size_t ring;   // double[C*RL]
+  size_t lring;  // double[RS]   per-position levels
+  size_t row;    // float[2*C]   per-step row of all labels (double buffered)
+  size_t red;    // double[64]   block reductions (verification)
+  size_t total;
+};
+
+__host__ __device__ inline FastLds fast_lds_layout(int C, int RL, int RS) {
+  FastLds L;
+  size_t o = 0;
+  L.ring = o; o = align16(o + 8 * (size_t)C * RL);
+  L.lring = o; o = align16(o + sizeof(double) * RS);
+  L.row = o; o = align16(o + sizeof(float) * 2 * C);
+  L.red = o; o = align16(o + sizeof(double) * 64);
+  L.total = o;
+  return L;
+}
 
 // ---- scan kernel LDS layout (bytes offsets) --------------------------------
 // Rings hold, per label, RL = RS + KP floats: slot s (0 <= s < RS) plus a mirror

@@ -28,9 +28,12 @@
 
 #include "tsm_device.hpp"
 #include "tsm_internal.hpp"
+#include "tsm_scan_common.hpp"
 
 namespace tsm {
 namespace {
+
+using namespace scan_detail;
 
 constexpr float kInvalid = -1e30f;  // level difference of a duration that does not exist
 
@@ -202,38 +205,8 @@ __device__ __forceinline__ float label_mix(const float* row, const float* trt, i
   }
 }
 
-// Block-wide max / min of a double (all threads receive the result).
-__device__ inline void block_minmax(double vmax, double vmin, double* red, double& omax, double& omin) {
-  for (int m = 1; m < 64; m <<= 1) {
-    vmax = fmax(vmax, __shfl_xor(vmax, m, 64));
-    vmin = fmin(vmin, __shfl_xor(vmin, m, 64));
-  }
-  const int w = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) {
-    red[w] = vmax;
-    red[32 + w] = vmin;
-  }
-  __syncthreads();
-  omax = red[0];
-  omin = red[32];
-  for (int i = 1; i < nw; ++i) {
-    omax = fmax(omax, red[i]);
-    omin = fmin(omin, red[32 + i]);
-  }
-  __syncthreads();
-}
 
-__device__ inline int seq_len(const ScanParams& p, int b) {
-  int64_t L = p.lengths[b];
-  if (L < 0) L = 0;
-  if (L > p.T) L = p.T;
-  return (int)L;
-}
 
-// Backward chunks own [j*Lc, (j+1)*Lc); the last one, jl, also owns position len.
-// jl = (len-1)/Lc keeps jl < P even when len is a multiple of Lc.
-__device__ inline int bwd_last_chunk(const ScanParams& p, int len) { return len > 0 ? (len - 1) / p.Lc : 0; }
 
 // ============================================================================
 // forward chunk
@@ -520,11 +493,6 @@ __device__ void backward_chunk(const ScanParams& p, char* smem_base, int b, int 
   }
 }
 
-__device__ inline bool fwd_spec(const ScanParams& p, int j) { return j >= 1 && j * p.Lc - p.W >= p.Kmax - 1; }
-__device__ inline bool bwd_spec(const ScanParams& p, int j, int len) {
-  const int jl = bwd_last_chunk(p, len);
-  return j < jl && (j + 1) * p.Lc + p.W + p.Kmax - 1 <= len;
-}
 
 template <int J, int RMAX, bool LOGSR, bool GR>
 __global__ void __launch_bounds__(512) scan_fwd_kernel(ScanParams p) {
@@ -569,17 +537,9 @@ __global__ void __launch_bounds__(256) verify_kernel(ScanParams p, int forward) 
   const int item = b * p.P + j;
   const bool spec = forward ? fwd_spec(p, j) && j * p.Lc < len : bwd_spec(p, j, len);
   if (!spec) return;
-  const int Kmax = p.Kmax, C = p.C;
   const size_t e = forward ? (size_t)(item - 1) : (size_t)(item + 1), sp = (size_t)item;
-  double hi = -1e300, lo = 1e300;
-  for (int idx = threadIdx.x; idx < Kmax * C; idx += blockDim.x) {
-    const int i = idx / C;
-    const float a = p.st_end[e * Kmax * C + idx], bb = p.st_spec[sp * Kmax * C + idx];
-    if (a < -1e8f && bb < -1e8f) continue;
-    const double d = (p.lv_end[e * Kmax + i] - p.lv_spec[sp * Kmax + i]) + ((double)a - (double)bb);
-    hi = fmax(hi, d);
-    lo = fmin(lo, d);
-  }
+  double hi, lo;
+  boundary_spread_part(p, e, sp, hi, lo);
   double dmax, dmin;
   block_minmax(hi, lo, red, dmax, dmin);
   if (threadIdx.x == 0) {
@@ -616,15 +576,8 @@ __global__ void __launch_bounds__(512) fwd_fixup_kernel(ScanParams p) {
         dmin = p.vstat[2 * sp + 1];
       } else {
         // chunk j-1 was recomputed here: its end state changed, measure again
-        double hi = -1e300, lo = 1e300;
-        for (int idx = threadIdx.x; idx < Kmax * C; idx += blockDim.x) {
-          const int i = idx / C;
-          const float a = p.st_end[e * Kmax * C + idx], bb = p.st_spec[sp * Kmax * C + idx];
-          if (a < -1e8f && bb < -1e8f) continue;
-          const double d = (p.lv_end[e * Kmax + i] - p.lv_spec[sp * Kmax + i]) + ((double)a - (double)bb);
-          hi = fmax(hi, d);
-          lo = fmin(lo, d);
-        }
+        double hi, lo;
+        boundary_spread_part(p, e, sp, hi, lo);
         block_minmax(hi, lo, red, dmax, dmin);
       }
       if (dmax - dmin <= (double)p.tol) {
@@ -641,33 +594,7 @@ __global__ void __launch_bounds__(512) fwd_fixup_kernel(ScanParams p) {
     if (threadIdx.x == 0) p.offs[(size_t)item] = F;
   }
   __syncthreads();
-  // partition from the final row
-  if (threadIdx.x < 64) {
-    float m = kMinusInf;
-    for (int cc = threadIdx.x; cc < C; cc += 64) m = fmax2(m, p.fin[(size_t)b * C + cc]);
-    for (int k = 1; k < 64; k <<= 1) m = fmax2(m, __shfl_xor(m, k, 64));
-    float r;
-    if constexpr (LOGSR) {
-      float sm = 0.0f;
-      for (int cc = threadIdx.x; cc < C; cc += 64) sm += exp2_hw(p.fin[(size_t)b * C + cc] - m);
-      for (int k = 1; k < 64; k <<= 1) sm += __shfl_xor(sm, k, 64);
-      r = m + log2_hw(sm);
-    } else {
-      r = m;
-    }
-    if (threadIdx.x == 0) {
-      if (p.recomputed != nullptr) p.recomputed[b] = n_re;
-      if (len == 0) {
-        // reference: the final alpha is never written -> reduction over NEG_INF
-        p.z2[b] = (double)kNegInf * 1.4426950408889634;
-        p.zout[b] = kNegInf;
-      } else {
-        const double z2 = p.fin_lvl[b] + F + (double)r;
-        p.z2[b] = z2;
-        p.zout[b] = (float)(z2 * kLn2);
-      }
-    }
-  }
+  finish_partition<LOGSR>(p, b, len, F, n_re);
 }
 
 template <int J, int RMAX, bool LOGSR, bool GR>
@@ -695,15 +622,8 @@ __global__ void __launch_bounds__(512) bwd_fixup_kernel(ScanParams p) {
         dmax = p.vstat[2 * sp];
         dmin = p.vstat[2 * sp + 1];
       } else {
-        double hi = -1e300, lo = 1e300;
-        for (int idx = threadIdx.x; idx < Kmax * C; idx += blockDim.x) {
-          const int i = idx / C;
-          const float a = p.st_end[e * Kmax * C + idx], bb = p.st_spec[sp * Kmax * C + idx];
-          if (a < -1e8f && bb < -1e8f) continue;
-          const double d = (p.lv_end[e * Kmax + i] - p.lv_spec[sp * Kmax + i]) + ((double)a - (double)bb);
-          hi = fmax(hi, d);
-          lo = fmin(lo, d);
-        }
+        double hi, lo;
+        boundary_spread_part(p, e, sp, hi, lo);
         block_minmax(hi, lo, red, dmax, dmin);
       }
       if (dmax - dmin <= (double)p.tol) {
@@ -748,10 +668,7 @@ int launch_dir(const Plan& pl, const ScanParams& p, bool forward, hipStream_t st
       TimedLaunch tl(kKScanFwd, st);
       hipLaunchKernelGGL(k1, dim3(pl.B * pl.P), dim3(pl.NT), lds, st, p);
     }
-    if (pl.P > 1) {
-      TimedLaunch tl(kKVerify, st);
-      hipLaunchKernelGGL(verify_kernel, dim3(pl.B * pl.P), dim3(256), 0, st, p, 1);
-    }
+    launch_verify(pl, p, true, st);
     {
       TimedLaunch tl(kKFwdFixup, st);
       hipLaunchKernelGGL(k2, dim3(pl.B), dim3(pl.NT), lds, st, p);
@@ -767,22 +684,13 @@ int launch_dir(const Plan& pl, const ScanParams& p, bool forward, hipStream_t st
       TimedLaunch tl(kKScanBwd, st);
       hipLaunchKernelGGL(k1, dim3(pl.B * pl.P), dim3(pl.NT), lds, st, p);
     }
-    if (pl.P > 1) {
-      TimedLaunch tl(kKVerify, st);
-      hipLaunchKernelGGL(verify_kernel, dim3(pl.B * pl.P), dim3(256), 0, st, p, 0);
-    }
+    launch_verify(pl, p, false, st);
     {
       TimedLaunch tl(kKBwdFixup, st);
       hipLaunchKernelGGL(k2, dim3(pl.B), dim3(pl.NT), lds, st, p);
     }
   }
-  if (p.lvl != nullptr) {
-    const int per = 256;
-    int gx = (pl.T + 1 + per - 1) / per;
-    if (gx > 1024) gx = 1024;
-    TimedLaunch tl(kKApplyOffsets, st);
-    hipLaunchKernelGGL(apply_offsets_kernel, dim3(gx, pl.B), dim3(per), 0, st, p, forward ? 1 : 0);
-  }
+  launch_apply_offsets(pl, p, forward, st);
   return hipGetLastError();
 }
 
@@ -805,15 +713,55 @@ int launch_j(const Plan& pl, const ScanParams& p, bool fwd, hipStream_t st) {
 template <bool LOGSR>
 int launch_sr(const Plan& pl, const ScanParams& p, bool fwd, hipStream_t st) {
   if (pl.global_rings) return launch_j<0, LOGSR, true>(pl, p, fwd, st);
-  if (pl.RMAX == 32) return launch_j<32, LOGSR, false>(pl, p, fwd, st);
+  // the log semiring's register-resident scan lives in tsm_fastscan.hpp; here
+  // only the max semiring keeps a register variant
+  if constexpr (!LOGSR) {
+    if (pl.RMAX == 32) return launch_j<32, LOGSR, false>(pl, p, fwd, st);
+  }
   return launch_j<0, LOGSR, false>(pl, p, fwd, st);
 }
 
+int launch_fast(const Plan& pl, const ScanParams& p, bool fwd, hipStream_t st) {
+  // the fast path's ring geometry replaces the generic one
+  ScanParams q = p;
+  q.RS = pl.FRS;
+  q.RL = pl.FRL;
+  q.R = pl.FR;
+  q.KP = pl.FJ * pl.FR;
+  switch (pl.FJ) {
+    case 8: return launch_fast_j8(pl, q, fwd, st);
+    case 16: return launch_fast_j16(pl, q, fwd, st);
+    case 32: return launch_fast_j32(pl, q, fwd, st);
+    case 64: return launch_fast_j64(pl, q, fwd, st);
+    default: return (int)hipErrorInvalidValue;
+  }
+}
+
 int launch_any(const Plan& pl, const ScanParams& p, int semiring, bool fwd, hipStream_t st) {
+  if (semiring == kLog && pl.fast) return launch_fast(pl, p, fwd, st);
   return semiring == kLog ? launch_sr<true>(pl, p, fwd, st) : launch_sr<false>(pl, p, fwd, st);
 }
 
 }  // namespace
+
+int launch_verify(const Plan& pl, const ScanParams& p, bool forward, hipStream_t st) {
+  if (pl.P > 1) {
+    TimedLaunch tl(kKVerify, st);
+    hipLaunchKernelGGL(verify_kernel, dim3(pl.B * pl.P), dim3(256), 0, st, p, forward ? 1 : 0);
+  }
+  return hipGetLastError();
+}
+
+int launch_apply_offsets(const Plan& pl, const ScanParams& p, bool forward, hipStream_t st) {
+  if (p.lvl != nullptr) {
+    const int per = 256;
+    int gx = (pl.T + 1 + per - 1) / per;
+    if (gx > 1024) gx = 1024;
+    TimedLaunch tl(kKApplyOffsets, st);
+    hipLaunchKernelGGL(apply_offsets_kernel, dim3(gx, pl.B), dim3(per), 0, st, p, forward ? 1 : 0);
+  }
+  return hipGetLastError();
+}
 
 int launch_scan_forward(const Plan& pl, const ScanParams& p, int semiring, hipStream_t s) {
   return launch_any(pl, p, semiring, true, s);
