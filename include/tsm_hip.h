@@ -49,9 +49,10 @@ const char* tsm_last_error(void);
  * Launch plan for a problem shape, for diagnostics and tests.  Fills up to
  * `n` int64 host values: J, NT, RS, P, Lc, W, global_rings, scan_lds, NB, TB,
  * CB, NCB, JM, NTM, marg_lds, Kmax, n_cu, R, KP, RMAX, fast, FJ, FR, FNT,
- * fast_lds (fast = 1: log-semiring scans use the register-resident kernels
- * with FJ lanes per label and FR durations per lane; the environment variable
- * TSM_SCAN_PATH=generic turns them off).
+ * fast_lds, mfast, MR (fast = 1: log-semiring scans use the register-resident
+ * kernels with FJ lanes per label and FR durations per lane; mfast = 1: the
+ * marginals use the register-resident kernel with MR durations per lane; the
+ * environment variable TSM_SCAN_PATH=generic turns both off).
  */
 int tsm_plan_info(int64_t B, int64_t T, int64_t C, int64_t K, int has_proj_start, int has_proj_end,
                   int64_t* out, int n);

@@ -196,6 +196,43 @@ int make_plan(int64_t B, int64_t T, int64_t C, int64_t K, int has_ps, int has_pe
   p.NB = (int)NB;
   p.TB = (int)TB;
   plan_fast(p, di);
+  p.mfast = 0;
+  const char* env = getenv("TSM_SCAN_PATH");
+  const bool generic_only = env != nullptr && strcmp(env, "generic") == 0;
+  if (!generic_only && p.C <= 64 && (p.Kmax + 15) / 16 <= 32) {
+    // register-resident marginals: 16 lanes per label, one wavefront of 4 labels
+    // per workgroup, rings hold the KP positions of a step plus the 16 staged ahead
+    const int J = 16, MR = (p.Kmax + 15) / 16, KP = J * MR;
+    const int CBm = 64 / J;
+    const int RSm = std::max(p.Kmax + 2, KP + J);
+    int RLm = RSm + KP;
+    while (RLm % 32 != J % 32) ++RLm;
+    const size_t lds = tsm::margfast_lds_layout(CBm, RLm, J, p.C).total;
+    if (lds <= (size_t)di.max_lds) {
+      p.mfast = 1;
+      p.MR = MR;
+      p.MRS = RSm;
+      p.MRL = RLm;
+      p.CB = CBm;
+      p.NCB = (int)cdiv(p.C, CBm);
+      p.JM = J;
+      p.NTM = 64;
+      p.marg_lds = lds;
+      // about two rounds of workgroups over the CUs (as many per CU as LDS allows),
+      // blocks at least 4*KP positions long (staging overhead <= 25%)
+      const int64_t per_cu = std::max<int64_t>(1, std::min<int64_t>(8, (int64_t)di.max_lds / (int64_t)lds));
+      int64_t nbm = cdiv(2 * (int64_t)di.n_cu * per_cu, (int64_t)p.B * p.NCB);
+      nbm = std::min<int64_t>(nbm, std::max<int64_t>(1, T / (4 * (int64_t)KP)));
+      nbm = std::max<int64_t>(nbm, 1);
+      int64_t tbm = cdiv(T, nbm);
+      if (tbm < p.Kmax) {
+        tbm = p.Kmax;
+        nbm = cdiv(T, tbm);
+      }
+      p.NB = (int)nbm;
+      p.TB = (int)tbm;
+    }
+  }
   *out = p;
   return TSM_OK;
 }
@@ -323,7 +360,7 @@ int tsm_plan_info(int64_t B, int64_t T, int64_t C, int64_t K, int has_ps, int ha
   const DeviceInfo di = device_info();
   const int64_t vals[] = {p.J, p.NT, p.RS, p.P, p.Lc, p.W, p.global_rings, (int64_t)p.scan_lds, p.NB, p.TB,
                           p.CB, p.NCB, p.JM, p.NTM, (int64_t)p.marg_lds, p.Kmax, di.n_cu, p.R, p.KP, p.RMAX,
-                          p.fast, p.FJ, p.FR, p.FNT, (int64_t)p.fast_lds};
+                          p.fast, p.FJ, p.FR, p.FNT, (int64_t)p.fast_lds, p.mfast, p.MR};
   const int m = (int)(sizeof(vals) / sizeof(vals[0]));
   for (int i = 0; i < n && i < m; ++i) out[i] = vals[i];
   return TSM_OK;
@@ -426,7 +463,8 @@ int tsm_backward(const float* cum, const float* tr, const float* db, const int64
   q.C = pl.C;
   q.K = pl.K;
   q.Kmax = pl.Kmax;
-  q.RS = pl.RS;
+  q.RS = pl.mfast ? pl.MRS : pl.RS;
+  q.RL = pl.MRL;
   q.NB = pl.NB;
   q.TB = pl.TB;
   q.CB = pl.CB;

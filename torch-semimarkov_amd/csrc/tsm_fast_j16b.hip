@@ -1,6 +1,7 @@
-// Register-resident scan instances: 16-lane label groups, 17-32 durations per lane.
+// Register-resident scan and marginal instances: 16-lane label groups, 17-32 durations per lane.
 // (Split across files so the instances compile in parallel.)
 #include "tsm_fastscan.hpp"
+#include "tsm_margfast.hpp"
 
 namespace tsm {
 
@@ -28,6 +29,32 @@ int launch_fast_j16_hi(const Plan& pl, const ScanParams& p, bool fwd, hipStream_
 
 int launch_fast_j16(const Plan& pl, const ScanParams& p, bool fwd, hipStream_t st) {
   return pl.FR <= 16 ? launch_fast_j16_lo(pl, p, fwd, st) : launch_fast_j16_hi(pl, p, fwd, st);
+}
+
+int launch_margfast_j16_hi(const Plan& pl, const MargParams& q, hipStream_t st) {
+  switch (pl.MR) {
+    case 17: return margfast::launch_margfast_jr<16, 17>(pl, q, st);
+    case 18: return margfast::launch_margfast_jr<16, 18>(pl, q, st);
+    case 19: return margfast::launch_margfast_jr<16, 19>(pl, q, st);
+    case 20: return margfast::launch_margfast_jr<16, 20>(pl, q, st);
+    case 21: return margfast::launch_margfast_jr<16, 21>(pl, q, st);
+    case 22: return margfast::launch_margfast_jr<16, 22>(pl, q, st);
+    case 23: return margfast::launch_margfast_jr<16, 23>(pl, q, st);
+    case 24: return margfast::launch_margfast_jr<16, 24>(pl, q, st);
+    case 25: return margfast::launch_margfast_jr<16, 25>(pl, q, st);
+    case 26: return margfast::launch_margfast_jr<16, 26>(pl, q, st);
+    case 27: return margfast::launch_margfast_jr<16, 27>(pl, q, st);
+    case 28: return margfast::launch_margfast_jr<16, 28>(pl, q, st);
+    case 29: return margfast::launch_margfast_jr<16, 29>(pl, q, st);
+    case 30: return margfast::launch_margfast_jr<16, 30>(pl, q, st);
+    case 31: return margfast::launch_margfast_jr<16, 31>(pl, q, st);
+    case 32: return margfast::launch_margfast_jr<16, 32>(pl, q, st);
+    default: return (int)hipErrorInvalidValue;
+  }
+}
+
+int launch_margfast_j16(const Plan& pl, const MargParams& q, hipStream_t st) {
+  return pl.MR <= 16 ? launch_margfast_j16_lo(pl, q, st) : launch_margfast_j16_hi(pl, q, st);
 }
 
 }  // namespace tsm

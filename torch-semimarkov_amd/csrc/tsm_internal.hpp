@@ -52,6 +52,7 @@ struct MargParams {
   const float* ps;
   const float* pe;
   int B, T, C, K, Kmax, RS;
+  int RL;                  // ring row length of the register-resident marginal kernel
   int NB, TB, CB, NCB;
   const float* aval;       // (B, T+1, C) alpha-hat (log2)
   const double* alvl;      // (B, T+1) alpha levels (global frame)
@@ -99,6 +100,7 @@ struct ViterbiParams {
 
 // launchers (return hipError_t as int)
 int launch_scan_forward(const Plan& pl, const ScanParams& p, int semiring, hipStream_t s);
+int launch_scan_backward(const Plan& pl, const ScanParams& p, int semiring, hipStream_t s);
 // verification of speculative chunk boundaries / level offsets (shared by both scan paths)
 int launch_verify(const Plan& pl, const ScanParams& p, bool forward, hipStream_t s);
 int launch_apply_offsets(const Plan& pl, const ScanParams& p, bool forward, hipStream_t s);
@@ -109,7 +111,10 @@ int launch_fast_j16_lo(const Plan& pl, const ScanParams& p, bool forward, hipStr
 int launch_fast_j16_hi(const Plan& pl, const ScanParams& p, bool forward, hipStream_t s);
 int launch_fast_j32(const Plan& pl, const ScanParams& p, bool forward, hipStream_t s);
 int launch_fast_j64(const Plan& pl, const ScanParams& p, bool forward, hipStream_t s);
-int launch_scan_backward(const Plan& pl, const ScanParams& p, int semiring, hipStream_t s);
+// register-resident marginals (16 lanes per label, pl.MR durations per lane)
+int launch_margfast_j16(const Plan& pl, const MargParams& q, hipStream_t s);
+int launch_margfast_j16_lo(const Plan& pl, const MargParams& q, hipStream_t s);
+int launch_margfast_j16_hi(const Plan& pl, const MargParams& q, hipStream_t s);
 int launch_marginals(const Plan& pl, const MargParams& q, hipStream_t s);
 int launch_finalize(const Plan& pl, const FinalParams& f, hipStream_t s);
 int launch_viterbi(const Plan& pl, const ViterbiParams& v, int with_traceback, hipStream_t s);

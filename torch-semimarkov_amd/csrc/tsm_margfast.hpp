@@ -1,0 +1,311 @@
+// Register-resident segment marginals for gfx950 (companion of tsm_fastscan.hpp).
+//
+// Given the stored forward table (alpha-hat, fp64 levels) and backward table
+// (beta-hat, levels), every start position t is independent:
+//   P(t,k,c) = exp2( A[t,c] + x[t+k,c] + db[k,c] )
+//   A[t,c]   = lvl_a[t] + u[t,c] (+ ps[t,c]) - cum[t,c]*log2(e) - log2 Z
+//   x[e,c]   = lvl_b[e] + beta-hat[e,c] (+ pe[e-1,c]) + cum[e,c]*log2(e)
+//   u[t,c]   = log2 sum_{c'} 2^(alpha-hat[t,c'] + trans[c',c])
+// (all log2 units; the large level and cumulative-score parts cancel in fp64,
+// only the final exponent is rounded to fp32).  The gradients need
+//   S[t,c] = sum_k P            (start sums: grad_cum[t] -= S, grad_ps[t] += S)
+//   E[e,c] = sum_k P(e-k,k,c)   (end sums: grad_cum[e] += E, grad_pe[e-1] += E)
+//   D[k,c] = sum_t P            (grad duration_bias)
+//   G[c',c] = sum_t S[t,c] * 2^(alpha-hat[t,c'] + trans[c',c] - u[t,c])   (grad trans)
+//
+// One wavefront serves 4 labels of one position block: a 16-lane group (one
+// DPP row) per label, lane j owning durations k = 1 + j + 16*r (r < R, the
+// compile-time mapping of the scans).  x lives in an LDS ring per label
+// (mirrored so the KP = 16*R terms of a step are read without wrap-around),
+// staged 16 positions at a time, together with the per-step operands, from
+// loads issued one batch earlier.  E lives in registers: lane j's register r
+// holds the running end sum of position t+1+j+16r, so after each step the
+// sums slide one lane down the row (DPP row rotate; lane 0 first takes its
+// next register) and position t+1, complete, leaves from lane 0.  D and G
+// accumulate in registers (fp32, folded into fp64 every 64 steps).  Waves
+// never synchronise with each other.
+// Outputs follow the blocked layout of the generic marginal kernel (e_own /
+// halo / s_out rows, fp64 per-block partials), so the same finalize kernels
+// produce the gradients.
+#pragma once
+
+#include "tsm_device.hpp"
+#include "tsm_internal.hpp"
+
+namespace tsm {
+namespace margfast {
+
+constexpr double kInvD = -1e30;
+constexpr int kCJ = 4;  // labels per lane in the label mix (plans keep C <= 4*J)
+constexpr int kRowLoads = 16;  // alpha-hat row loads per lane per batch: J*C <= 1024
+constexpr double kLog2eD = 1.4426950408889634;
+
+__device__ __forceinline__ void wave_lds_order() { __asm__ volatile("" ::: "memory"); }
+
+__device__ __forceinline__ int mlen(const int64_t* lengths, int b, int T) {
+  int64_t L = lengths[b];
+  if (L < 0) L = 0;
+  if (L > T) L = T;
+  return (int)L;
+}
+
+constexpr int kDppRowRor15 = 0x12F;  // row_ror:15 -- lane i reads lane (i+1) mod 16 of its row
+
+template <int J, int R>
+__global__ void __launch_bounds__(64) margfast_kernel(MargParams q) {
+  static_assert(J == 16, "end sums slide along one 16-lane DPP row");
+  extern __shared__ __align__(16) char smem[];
+  constexpr int KP = J * R;
+  constexpr int CB = 64 / J;
+  const int cbk = blockIdx.x % q.NCB;
+  const int blk = (blockIdx.x / q.NCB) % q.NB;
+  const int b = blockIdx.x / (q.NCB * q.NB);
+  const int C = q.C, Kmax = q.Kmax, K = q.K, T = q.T, RS = q.RS, RL = q.RL;
+  const int lane = threadIdx.x, g = lane / J, lj = lane % J;
+  const int c_raw = cbk * CB + g;
+  const bool cval = c_raw < C;
+  const int c = cval ? c_raw : C - 1;
+  const int len = mlen(q.lengths, b, T);
+  const int t0 = blk * q.TB;
+  float* e_own_b = q.e_own + (size_t)b * (T + 1) * C;
+  double* dbp = q.db_part + ((size_t)b * q.NB + blk) * Kmax * C;
+  double* trp = q.tr_part + ((size_t)b * q.NB + blk) * C * C;
+  if (t0 >= len) {
+    // no starts here: zero this block's partials (they are summed over all
+    // blocks) and the end sum at len when the block begins there
+    if (cval) {
+      for (int k = lj; k < Kmax; k += J) dbp[(size_t)k * C + c] = 0.0;
+      for (int cs = lj; cs < C; cs += J) trp[(size_t)cs * C + c] = 0.0;
+      if (t0 == len && lj == 0) e_own_b[(size_t)len * C + c] = 0.0f;
+    }
+    return;
+  }
+  const int t1 = min(t0 + q.TB, len);
+  const bool has_ps = q.ps != nullptr, has_pe = q.pe != nullptr;
+  const float* cum_b = q.cum + (size_t)b * (T + 1) * C;
+  const float* ps_b = has_ps ? q.ps + (size_t)b * T * C : nullptr;
+  const float* pe_b = has_pe ? q.pe + (size_t)b * T * C : nullptr;
+  const float* av_b = q.aval + (size_t)b * (T + 1) * C;
+  const double* al_b = q.alvl + (size_t)b * (T + 1);
+  const float* bv_b = q.bval + (size_t)b * (T + 1) * C;
+  const double* bl_b = q.blvl + (size_t)b * (T + 1);
+  const double z2 = q.z2[b];
+
+  const MargFastLds L = margfast_lds_layout(CB, RL, J, C);
+  double* xr = reinterpret_cast<double*>(smem + L.xring) + (size_t)g * RL;
+  // per-step operands of the current batch of J positions [tb, tb+J)
+  float* arow = reinterpret_cast<float*>(smem + L.arow);  // [J][C] alpha-hat rows
+  double* alv = reinterpret_cast<double*>(smem + L.alv);  // [J]    alpha levels
+  float* cmv = reinterpret_cast<float*>(smem + L.cmv);    // [CB][J] cum of own labels
+  float* psv = reinterpret_cast<float*>(smem + L.psv);    // [CB][J] proj_start of own labels
+
+  // ---- constants ----
+  double dbr[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int k = 1 + lj + J * r;
+    const int di = k < K - 1 ? k : K - 1;
+    dbr[r] = (k <= Kmax) ? (double)(q.db[(size_t)di * C + c] * kLog2e) : kInvD;
+  }
+  float trr[kCJ];
+#pragma unroll
+  for (int i = 0; i < kCJ; ++i) {
+    const int ci = lj + J * i;
+    trr[i] = (ci < C) ? q.trans[(size_t)ci * C + c] * kLog2e : 0.0f;  // source ci -> destination c
+  }
+
+  // x of position e (own label), or "does not exist" beyond len
+  auto x_of = [&](int e, float bv, double bl, float cm, float pe) -> double {
+    return (e <= len) ? (bl + (double)(bv + pe)) + (double)cm * kLog2eD : kInvD;
+  };
+  auto clampT = [&](int e) { return e > T ? T : e; };
+
+  // ---- initial ring: x for positions t0+1 .. t0+KP ----
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int e = t0 + 1 + lj + J * r;
+    const int ec = clampT(e);
+    const float pe = (has_pe && ec >= 1) ? pe_b[(size_t)(ec - 1) * C + c] * kLog2e : 0.0f;
+    const double x = x_of(e, bv_b[(size_t)ec * C + c], bl_b[ec], cum_b[(size_t)ec * C + c], pe);
+    const int a = e % RS;
+    xr[a] = x;
+    if (a < KP) xr[a + RS] = x;
+  }
+  // Batches of J steps.  At a batch start tb the registers loaded one batch
+  // earlier are written to LDS -- x for positions tb+KP+1 .. tb+KP+J and the
+  // operands of steps tb .. tb+J-1 -- and the next batch's loads are issued.
+  int e_n = t0 + KP + 1 + lj;  // x position this lane stages at the next batch start
+  float sb_bv, sb_cm, sb_pe;
+  double sb_bl;
+  float ra[kRowLoads];
+  double ral;
+  float rcm, rps;
+  auto load_batch = [&](int tb, int e) {
+    const int ec = clampT(e);
+    sb_bv = bv_b[(size_t)ec * C + c];
+    sb_bl = bl_b[ec];
+    sb_cm = cum_b[(size_t)ec * C + c];
+    sb_pe = (has_pe && ec >= 1) ? pe_b[(size_t)(ec - 1) * C + c] * kLog2e : 0.0f;
+#pragma unroll
+    for (int i = 0; i < kRowLoads; ++i) {
+      const int idx = lane + 64 * i;
+      ra[i] = (idx < J * C) ? av_b[(size_t)clampT(tb + idx / C) * C + idx % C] : 0.0f;
+    }
+    ral = al_b[clampT(tb + (lane % J))];
+    const int tp = clampT(tb + lj);
+    rcm = cum_b[(size_t)tp * C + c];
+    rps = has_ps ? ps_b[(size_t)min(tp, T - 1) * C + c] : 0.0f;
+  };
+  load_batch(t0, e_n);
+  if (cval && lj == 0) e_own_b[(size_t)t0 * C + c] = 0.0f;
+  wave_lds_order();
+
+  float d32[R];
+  double d64[R];
+  float ea[R];  // running end sums of positions t+1+lj+16r (this block's starts)
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    d32[r] = 0.0f;
+    d64[r] = 0.0;
+    ea[r] = 0.0f;
+  }
+  float g32[kCJ];
+  double g64[kCJ];
+#pragma unroll
+  for (int i = 0; i < kCJ; ++i) {
+    g32[i] = 0.0f;
+    g64[i] = 0.0;
+  }
+  float* s_out_b = q.s_out + (size_t)b * (T + 1) * C;
+  float* halo_b = q.halo + ((size_t)b * q.NB + blk) * Kmax * C;
+  // end rows [t0, own_hi) are this block's own; rows own_hi .. own_hi+Kmax-1 go to the
+  // halo that the next block's rows add in the finalize kernel
+  const int own_hi = t0 + q.TB;
+
+  for (int t = t0; t < t1; ++t) {
+    const int ib = (t - t0) % J;  // step within the batch
+    if (ib == 0) {
+      const double x = x_of(e_n, sb_bv, sb_bl, sb_cm, sb_pe);
+      const int a = e_n % RS;
+      xr[a] = x;
+      if (a < KP) xr[a + RS] = x;
+#pragma unroll
+      for (int i = 0; i < kRowLoads; ++i)
+        if (lane + 64 * i < J * C) arow[lane + 64 * i] = ra[i];
+      if (lane < J) alv[lane] = ral;
+      cmv[g * J + lj] = rcm;
+      psv[g * J + lj] = rps;
+      e_n += J;
+      load_batch(t + J, e_n);
+      wave_lds_order();
+    }
+    // ---- this step's operands ----
+    float rv[kCJ];
+#pragma unroll
+    for (int i = 0; i < kCJ; ++i) rv[i] = arow[ib * C + min(lj + J * i, C - 1)];
+    const double al = alv[ib];
+    const float cm = cmv[g * J + ib];
+    const float ps_t = psv[g * J + ib];
+    // ---- u[t,c] and the softmax weights of the source labels ----
+    float mq = kMinusInf;
+#pragma unroll
+    for (int i = 0; i < kCJ; ++i)
+      if (lj + J * i < C) mq = fmax2(mq, rv[i] + trr[i]);
+    const float M = group_max<J>(mq);
+    float ew[kCJ];
+    float sw = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kCJ; ++i) {
+      ew[i] = (lj + J * i < C) ? exp2_hw((rv[i] + trr[i]) - M) : 0.0f;
+      sw += ew[i];
+    }
+    const float S = group_sum<J>(sw);
+    const float u2 = M + log2_hw(S);
+    const double At = ((al + (double)(u2 + ps_t * kLog2e)) - (double)cm * kLog2eD) - z2;
+
+    // ---- segment marginals over the lane's durations ----
+    const double* xb = xr + (t % RS + 1 + lj);
+    double xv[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) xv[r] = xb[J * r];
+    float sp0 = 0.0f, sp1 = 0.0f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float P = exp2_hw((float)((xv[r] + dbr[r]) + At));
+      d32[r] += P;
+      ea[r] += P;
+      if (r & 1) sp1 += P;
+      else sp0 += P;
+    }
+    const float St = group_sum<J>(sp0 + sp1);
+    // ---- transition gradient: softmax weight of each source label times S[t,c] ----
+    const float wS = St / S;
+#pragma unroll
+    for (int i = 0; i < kCJ; ++i) g32[i] = fmaf(ew[i], wS, g32[i]);
+    if (cval && lj == 0) {
+      s_out_b[(size_t)t * C + c] = St;
+      // end row t+1 is complete (all its starts t+1-k >= t0 are done)
+      const int p = t + 1;
+      if (p < own_hi) e_own_b[(size_t)p * C + c] = ea[0];
+      else halo_b[(size_t)(p - own_hi) * C + c] = ea[0];
+    }
+    // slide the end sums to positions t+2+lj+16r: lane 0 takes its next register
+    // (dropping the flushed row), then each register rotates one lane down the row
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float nxt = (r + 1 < R) ? ea[r + 1] : 0.0f;
+      ea[r] = (lj == 0) ? nxt : ea[r];
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) ea[r] = dpp_f<kDppRowRor15>(ea[r]);
+    if (((t - t0) & 63) == 63) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        d64[r] += (double)d32[r];
+        d32[r] = 0.0f;
+      }
+#pragma unroll
+      for (int i = 0; i < kCJ; ++i) {
+        g64[i] += (double)g32[i];
+        g32[i] = 0.0f;
+      }
+    }
+  }
+  // ---- pending end rows t1+1 .. t1+Kmax-1 (partial sums from this block's starts) ----
+  if (cval) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int p = t1 + 1 + lj + J * r;
+      if (p <= t1 - 1 + Kmax && p <= len) {
+        if (p < own_hi) e_own_b[(size_t)p * C + c] = ea[r];
+        else halo_b[(size_t)(p - own_hi) * C + c] = ea[r];
+      }
+    }
+  }
+  // ---- block partials ----
+  if (cval) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int k = 1 + lj + J * r;
+      if (k <= Kmax) dbp[(size_t)(k - 1) * C + c] = d64[r] + (double)d32[r];
+    }
+#pragma unroll
+    for (int i = 0; i < kCJ; ++i) {
+      const int ci = lj + J * i;
+      if (ci < C) trp[(size_t)ci * C + c] = g64[i] + (double)g32[i];
+    }
+  }
+}
+
+template <int J, int R>
+int launch_margfast_jr(const Plan& pl, const MargParams& q, hipStream_t st) {
+  auto k = margfast_kernel<J, R>;
+  hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)pl.marg_lds);
+  if (e != hipSuccess) return e;
+  TimedLaunch tl(kKMarginal, st);
+  hipLaunchKernelGGL(k, dim3(pl.B * pl.NB * pl.NCB), dim3(64), pl.marg_lds, st, q);
+  return hipGetLastError();
+}
+
+}  // namespace margfast
+}  // namespace tsm

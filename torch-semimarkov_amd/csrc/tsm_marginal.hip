@@ -329,6 +329,7 @@ int launch_marg_j(const Plan& pl, const MargParams& q, hipStream_t st) {
 }  // namespace
 
 int launch_marginals(const Plan& pl, const MargParams& q, hipStream_t s) {
+  if (pl.mfast) return launch_margfast_j16(pl, q, s);
   switch (pl.JM) {
     case 1: return launch_marg_j<1>(pl, q, s);
     case 2: return launch_marg_j<2>(pl, q, s);

@@ -30,9 +30,39 @@ struct Plan {
   // FRS ring slots, FRL ring row length (float2 elements), fast_lds bytes
   int fast, FJ, FR, FNT, FRS, FRL;
   size_t fast_lds;
+  // register-resident marginal kernel (mfast == 1): 16 lanes per label, MR
+  // durations per lane, one wavefront of 4 labels per workgroup, ring slots /
+  // row length.  NB, TB, CB, NCB and marg_lds above then describe its blocking.
+  int mfast, MR, MRS, MRL;
 };
 
+
+
 __host__ __device__ inline size_t align16(size_t x) { return (x + 15) & ~size_t(15); }
+
+// LDS layout of the register-resident marginal kernel (one wavefront of CB
+// labels): per label an fp64 x ring of RL entries, then the per-step operands
+// of one batch of J positions.
+struct MargFastLds {
+  size_t xring;  // double[CB*RL]
+  size_t arow;   // float[J*C]   alpha-hat rows
+  size_t alv;    // double[J]    alpha levels
+  size_t cmv;    // float[CB*J]  cumulative scores of the own labels
+  size_t psv;    // float[CB*J]  proj_start of the own labels
+  size_t total;
+};
+
+__host__ __device__ inline MargFastLds margfast_lds_layout(int CB, int RL, int J, int C) {
+  MargFastLds L;
+  size_t o = 0;
+  L.xring = o; o = align16(o + 8 * (size_t)CB * RL);
+  L.arow = o; o = align16(o + 4 * (size_t)J * C);
+  L.alv = o; o = align16(o + 8 * (size_t)J);
+  L.cmv = o; o = align16(o + 4 * (size_t)CB * J);
+  L.psv = o; o = align16(o + 4 * (size_t)CB * J);
+  L.total = o;
+  return L;
+}
 
 // ---- fast scan LDS layout ---------------------------------------------------
 // One ring per label of RL fp64 entries: slot s < RS plus a mirror of slots

@@ -22,7 +22,7 @@ _ERRORS = {1: ValueError, 2: NotImplementedError, 3: RuntimeError, 4: RuntimeErr
 PLAN_FIELDS = (
     "J", "NT", "RS", "P", "Lc", "W", "global_rings", "scan_lds", "NB", "TB",
     "CB", "NCB", "JM", "NTM", "marg_lds", "Kmax", "n_cu", "R", "KP", "RMAX",
-    "fast", "FJ", "FR", "FNT", "fast_lds",
+    "fast", "FJ", "FR", "FNT", "fast_lds", "mfast", "MR",
 )
 
 _p = ctypes.c_void_p
