@@ -36,6 +36,8 @@ import torch  # noqa: E402
 # (v_exp_f32 / v_log_f32, quarter rate) peak of one MI355X
 V_PEAK = 78.6e12
 T_PEAK = 9.83e12
+# lane-op peak without packed FP32 (the kernels are built with packed FP32 off)
+V_PEAK_NONPACKED = 39.3e12
 # algorithmic ops per cell (b, t, k, c_dst, c_src) of the direct recursion:
 # (VALU lane-ops, transcendentals).  The backward (14, 3) splits into the alpha
 # recompute (5, 1), the beta recursion (4, 1) and the marginals (5, 1); this
@@ -66,6 +68,24 @@ def profiled_traffic(kernel, workload):
                 parts = ln.split()
                 if len(parts) == 4 and parts[0] == "traffic" and parts[1] == kernel and parts[2] == workload:
                     return float(parts[3])
+    except OSError:
+        pass
+    return None
+
+
+def profiled_executed(kernel, workload):
+    """Executed VALU lane-op and transcendental rates of `kernel` from the committed
+    SQ-counter summary (lines `executed <kernel> <workload> <lane-ops/s> <trans/s>`)."""
+    path = os.path.join(PROFILES, f"pmc_instructions_{workload}.txt")
+    try:
+        with open(path) as f:
+            for ln in f:
+                parts = ln.split()
+                if len(parts) == 5 and parts[0] == "executed" and parts[1] == kernel and parts[2] == workload:
+                    v, t = float(parts[3]), float(parts[4])
+                    return {"valu_lane_ops_per_s": v, "valu_frac_nonpacked_peak": v / V_PEAK_NONPACKED,
+                            "transcendental_per_s": t, "transcendental_frac": t / T_PEAK,
+                            "source": os.path.relpath(path, ROOT)}
     except OSError:
         pass
     return None
@@ -249,6 +269,7 @@ def main():
             "unit": "TFLOP/s",
             "frac": achieved / peak,
             "traffic": profiled_traffic(dom, args.config),
+            "executed": profiled_executed(dom, args.config),
             "avg_launch_ms": dom_avg_ms,
             "ops_per_cell": {"valu": nv, "transcendental": nt},
             "note": "NOMINAL: VALU-equivalent lane-ops (transcendental weighted by V_peak/T_peak) of the "

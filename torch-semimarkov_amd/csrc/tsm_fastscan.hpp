@@ -312,24 +312,28 @@ struct Chunk {
   }
 };
 
-// Parallel pass (phase 0: one block per chunk) and sequential verification /
-// repair (phase 1: one block per sequence) of one direction.
+// Parallel pass of one direction: one block per chunk, exact or speculative.
 template <int J, int R, bool FWD>
-__global__ void __launch_bounds__(R > 16 ? 512 : 1024) fast_scan_kernel(ScanParams p, int phase) {
+__global__ void __launch_bounds__(R > 16 ? 512 : 1024) fast_scan_kernel(ScanParams p) {
   extern __shared__ __align__(16) char smem[];
-  if (phase == 0) {
-    const int b = blockIdx.x / p.P, j = blockIdx.x % p.P;
-    const int len = seq_len(p, b);
-    const int item = b * p.P + j;
-    if (FWD ? (j > 0 && j * p.Lc >= len) : (j > bwd_last_chunk(p, len))) {
-      if (threadIdx.x == 0) p.status[item] = -1;  // empty chunk
-      return;
-    }
-    const int mode = (FWD ? fwd_spec(p, j) : bwd_spec(p, j, len)) ? 1 : 0;
-    if (threadIdx.x == 0) p.status[item] = mode;
-    Chunk<J, R, FWD>::run(p, smem, b, j, mode, nullptr, nullptr);
+  const int b = blockIdx.x / p.P, j = blockIdx.x % p.P;
+  const int len = seq_len(p, b);
+  const int item = b * p.P + j;
+  if (FWD ? (j > 0 && j * p.Lc >= len) : (j > bwd_last_chunk(p, len))) {
+    if (threadIdx.x == 0) p.status[item] = -1;  // empty chunk
     return;
   }
+  const int mode = (FWD ? fwd_spec(p, j) : bwd_spec(p, j, len)) ? 1 : 0;
+  if (threadIdx.x == 0) p.status[item] = mode;
+  Chunk<J, R, FWD>::run(p, smem, b, j, mode, nullptr, nullptr);
+}
+
+// Sequential verification / repair of one direction: one block per sequence
+// walks its chunks, accepts a speculative chunk's frame offset when the
+// boundary spread is within tolerance, recomputes it exactly otherwise.
+template <int J, int R, bool FWD>
+__global__ void __launch_bounds__(R > 16 ? 512 : 1024) fast_fixup_kernel(ScanParams p) {
+  extern __shared__ __align__(16) char smem[];
   const int b = blockIdx.x;
   const int len = seq_len(p, b);
   const FastLds L = fast_lds_layout(p.C, p.RL, p.RS);
@@ -384,18 +388,21 @@ __global__ void __launch_bounds__(R > 16 ? 512 : 1024) fast_scan_kernel(ScanPara
 template <int J, int R>
 int launch_fast_jr(const Plan& pl, const ScanParams& p, bool fwd, hipStream_t st) {
   auto k = fwd ? fast_scan_kernel<J, R, true> : fast_scan_kernel<J, R, false>;
+  auto kf = fwd ? fast_fixup_kernel<J, R, true> : fast_fixup_kernel<J, R, false>;
   const size_t lds = pl.fast_lds;
   hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return e;
+  e = hipFuncSetAttribute((const void*)kf, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (e != hipSuccess) return e;
   {
     TimedLaunch tl(fwd ? kKScanFwd : kKScanBwd, st);
-    hipLaunchKernelGGL(k, dim3(pl.B * pl.P), dim3(pl.FNT), lds, st, p, 0);
+    hipLaunchKernelGGL(k, dim3(pl.B * pl.P), dim3(pl.FNT), lds, st, p);
   }
   e = (hipError_t)launch_verify(pl, p, fwd, st);
   if (e != hipSuccess) return e;
   {
     TimedLaunch tl(fwd ? kKFwdFixup : kKBwdFixup, st);
-    hipLaunchKernelGGL(k, dim3(pl.B), dim3(pl.FNT), lds, st, p, 1);
+    hipLaunchKernelGGL(kf, dim3(pl.B), dim3(pl.FNT), lds, st, p);
   }
   e = (hipError_t)launch_apply_offsets(pl, p, fwd, st);
   if (e != hipSuccess) return e;
