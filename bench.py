@@ -135,6 +135,94 @@ def make_inputs(name):
     return cfg, cum, tr, db, L
 
 
+def bench_head(args):
+    """cfg1: SemiMarkovCRFHead(24, 100, 512) on h ~ N(0,1) (4, 1000, 512), random labels:
+    one step = compute_loss + backward, then decode_with_traceback; latency-bound."""
+    import torch_semimarkov_amd as tsa
+
+    seed = 20261201
+    B, T, H, C, K = 4, 1000, 512, 24, 100
+    torch.manual_seed(seed)
+    head = tsa.SemiMarkovCRFHead(C, K, hidden_dim=H)
+    g = torch.Generator().manual_seed(seed)
+    h = torch.randn(B, T, H, generator=g)
+    labels = torch.randint(0, C, (B, T), generator=g)
+    dev = torch.device("cuda", 0)
+    head = head.to(dev)
+    h, labels = h.to(dev), labels.to(dev)
+    L = torch.full((B,), T, dtype=torch.long, device=dev)
+
+    def train_step():
+        head.zero_grad(set_to_none=True)
+        loss = head.compute_loss(h, L, labels)
+        loss.backward()
+        return loss
+
+    for _ in range(args.warmup):
+        train_step()
+        head.decode_with_traceback(h, L)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        train_step()
+    torch.cuda.synchronize()
+    train_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        res = head.decode_with_traceback(h, L)
+    torch.cuda.synchronize()
+    decode_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    cells = B * T * K * C * C
+    print(json.dumps({
+        "metric": "head compute_loss+backward cells/s (B*T*K*C^2), 1 GPU", "value": cells / (train_ms / 1e3),
+        "unit": "cells/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": train_ms,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (random-init head, N(0,1) hidden states, uniform labels)",
+        "config": {"workload": "cfg1: SemiMarkovCRFHead(24, 100, 512) loss + backward", "B": B, "T": T, "H": H,
+                   "C": C, "K": K, "seed": seed},
+        "decode_with_traceback_ms": decode_ms, "segments_seq0": len(res.segments[0]),
+    }))
+
+
+def bench_viterbi(args):
+    """cfg4: Viterbi with backtrace (max semiring), 64 ragged sequences."""
+    import torch_semimarkov_amd as tsa
+    from torch_semimarkov_amd.streaming import ops
+
+    seed = 20261204
+    B, T, C, K = 64, 8192, 32, 64
+    g = torch.Generator().manual_seed(seed)
+    lengths = torch.randint(4096, 8193, (B,), generator=g)
+    em = torch.randn(B, T, C, generator=g)
+    tr = 0.1 * torch.randn(C, C, generator=g)
+    db = 0.1 * torch.randn(K, C, generator=g)
+    cum = torch.zeros(B, T + 1, C)
+    cum[:, 1:] = torch.cumsum(em, dim=1)
+    dev = torch.device("cuda", 0)
+    cum, tr, db, L = cum.to(dev), tr.to(dev), db.to(dev), lengths.to(dev)
+
+    def step():
+        return ops.viterbi(cum, tr, db, L, K, None, None, True)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        out = step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    cells_sum = int(lengths.sum()) * K * C * C
+    print(json.dumps({
+        "metric": "Viterbi + backtrace cells/s (sum_b L_b*K*C^2), 1 GPU", "value": cells_sum / (ms / 1e3),
+        "unit": "cells/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "cfg4: Viterbi with traceback, ragged lengths in [4096, 8192]", "B": B,
+                   "T_max": T, "C": C, "K": K, "seed": seed},
+        "cells_B_Tmax": B * T * K * C * C, "value_B_Tmax": B * T * K * C * C / (ms / 1e3),
+    }))
+
+
 def cpu_baseline(name, cum, tr, db, K, t_sample):
     """The oracle (fp32 PyTorch-CPU restatement of the reference streaming path)
     on the first t_sample positions of the same workload, forward + backward."""
@@ -176,7 +264,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default="cfg3", choices=sorted(list(CONFIGS) + ["cfg1", "cfg4"]))
     ap.add_argument("--cpu-sample", type=int, default=4000)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -189,6 +277,12 @@ def main():
 
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.config == "cfg1":
+        bench_head(args)
+        return
+    if args.config == "cfg4":
+        bench_viterbi(args)
         return
 
     import torch_semimarkov_amd as tsa

@@ -323,6 +323,7 @@ __global__ void __launch_bounds__(R > 16 ? 512 : 1024) fast_scan_kernel(ScanPara
     if (threadIdx.x == 0) p.status[item] = -1;  // empty chunk
     return;
   }
+  if (p.retry && retry_skip(p, item)) return;
   const int mode = (FWD ? fwd_spec(p, j) : bwd_spec(p, j, len)) ? 1 : 0;
   if (threadIdx.x == 0) p.status[item] = mode;
   Chunk<J, R, FWD>::run(p, smem, b, j, mode, nullptr, nullptr);
@@ -347,7 +348,7 @@ __global__ void __launch_bounds__(R > 16 ? 512 : 1024) fast_fixup_kernel(ScanPar
   if (threadIdx.x == 0) p.offs[(size_t)b * p.P + (FWD ? 0 : jl)] = 0.0;
   for (int j = FWD ? 1 : jl - 1; FWD ? j < nch : j >= 0; j += FWD ? 1 : -1) {
     const int item = b * p.P + j;
-    if (!(FWD ? fwd_spec(p, j) : bwd_spec(p, j, len))) {
+    if (p.status[item] != 1) {
       F = 0.0;  // the chunk ran exactly from the sequence end
       prev_recomputed = false;
     } else {
@@ -400,6 +401,15 @@ int launch_fast_jr(const Plan& pl, const ScanParams& p, bool fwd, hipStream_t st
   }
   e = (hipError_t)launch_verify(pl, p, fwd, st);
   if (e != hipSuccess) return e;
+  if (pl.P > 1) {
+    // failed speculative chunks again, in parallel, with a longer warm-up
+    {
+      TimedLaunch tl(kKRetry, st);
+      hipLaunchKernelGGL(k, dim3(pl.B * pl.P), dim3(pl.FNT), lds, st, retry_params(p));
+    }
+    e = (hipError_t)launch_verify(pl, p, fwd, st);
+    if (e != hipSuccess) return e;
+  }
   {
     TimedLaunch tl(fwd ? kKFwdFixup : kKBwdFixup, st);
     hipLaunchKernelGGL(kf, dim3(pl.B), dim3(pl.FNT), lds, st, p);

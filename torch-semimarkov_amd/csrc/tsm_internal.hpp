@@ -22,6 +22,7 @@ struct ScanParams {
   int B, T, C, K, Kmax, RS;
   int R, KP, RL;           // durations per lane, padded durations, ring row length
   int P, Lc, W;            // chunks per sequence, chunk length, warm-up
+  int retry;               // 1: recompute only speculative chunks that failed verification
   float tol;               // verification tolerance, log2 units
   // per-position output (normalised log2 values and fp64 levels), may be null
   float* val;              // (B, T+1, C)
@@ -135,6 +136,7 @@ enum KernelId : int {
   kKCheckpoints,
   kKViterbi,
   kKBacktrace,
+  kKRetry,
   kNumKernels
 };
 

@@ -504,6 +504,7 @@ __global__ void __launch_bounds__(512) scan_fwd_kernel(ScanParams p) {
     if (threadIdx.x == 0) p.status[item] = -1;  // empty chunk
     return;
   }
+  if (p.retry && retry_skip(p, item)) return;
   const int mode = fwd_spec(p, j) ? 1 : 0;
   if (threadIdx.x == 0) p.status[item] = mode;
   forward_chunk<J, RMAX, LOGSR, GR>(p, smem, b, j, mode, nullptr, nullptr);
@@ -519,6 +520,7 @@ __global__ void __launch_bounds__(512) scan_bwd_kernel(ScanParams p) {
     if (threadIdx.x == 0) p.status[item] = -1;
     return;
   }
+  if (p.retry && retry_skip(p, item)) return;
   const int mode = bwd_spec(p, j, len) ? 1 : 0;
   if (threadIdx.x == 0) p.status[item] = mode;
   backward_chunk<J, RMAX, LOGSR, GR>(p, smem, b, j, mode, nullptr, nullptr);
@@ -535,7 +537,9 @@ __global__ void __launch_bounds__(256) verify_kernel(ScanParams p, int forward) 
   const int b = blockIdx.x / p.P, j = blockIdx.x % p.P;
   const int len = seq_len(p, b);
   const int item = b * p.P + j;
-  const bool spec = forward ? fwd_spec(p, j) && j * p.Lc < len : bwd_spec(p, j, len);
+  // chunks that ran speculatively (the status the scan recorded)
+  (void)len;
+  const bool spec = p.status[item] == 1;
   if (!spec) return;
   const size_t e = forward ? (size_t)(item - 1) : (size_t)(item + 1), sp = (size_t)item;
   double hi, lo;
@@ -564,7 +568,7 @@ __global__ void __launch_bounds__(512) fwd_fixup_kernel(ScanParams p) {
   bool prev_recomputed = false;
   for (int j = 1; j < nch; ++j) {
     const int item = b * p.P + j;
-    if (!fwd_spec(p, j)) {
+    if (p.status[item] != 1) {
       F = 0.0;  // chunk ran exactly from position 0
       prev_recomputed = false;
     } else {
@@ -612,7 +616,7 @@ __global__ void __launch_bounds__(512) bwd_fixup_kernel(ScanParams p) {
   bool prev_recomputed = false;
   for (int j = jl - 1; j >= 0; --j) {
     const int item = b * p.P + j;
-    if (!bwd_spec(p, j, len)) {
+    if (p.status[item] != 1) {
       F = 0.0;  // chunk ran exactly from position len
       prev_recomputed = false;
     } else {
@@ -669,6 +673,12 @@ int launch_dir(const Plan& pl, const ScanParams& p, bool forward, hipStream_t st
       hipLaunchKernelGGL(k1, dim3(pl.B * pl.P), dim3(pl.NT), lds, st, p);
     }
     launch_verify(pl, p, true, st);
+    if (pl.P > 1) {
+      const ScanParams q = retry_params(p);
+      TimedLaunch tl(kKRetry, st);
+      hipLaunchKernelGGL(k1, dim3(pl.B * pl.P), dim3(pl.NT), lds, st, q);
+    }
+    if (pl.P > 1) launch_verify(pl, p, true, st);
     {
       TimedLaunch tl(kKFwdFixup, st);
       hipLaunchKernelGGL(k2, dim3(pl.B), dim3(pl.NT), lds, st, p);
@@ -685,6 +695,12 @@ int launch_dir(const Plan& pl, const ScanParams& p, bool forward, hipStream_t st
       hipLaunchKernelGGL(k1, dim3(pl.B * pl.P), dim3(pl.NT), lds, st, p);
     }
     launch_verify(pl, p, false, st);
+    if (pl.P > 1) {
+      const ScanParams q = retry_params(p);
+      TimedLaunch tl(kKRetry, st);
+      hipLaunchKernelGGL(k1, dim3(pl.B * pl.P), dim3(pl.NT), lds, st, q);
+    }
+    if (pl.P > 1) launch_verify(pl, p, false, st);
     {
       TimedLaunch tl(kKBwdFixup, st);
       hipLaunchKernelGGL(k2, dim3(pl.B), dim3(pl.NT), lds, st, p);

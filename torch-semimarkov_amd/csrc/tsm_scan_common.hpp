@@ -30,6 +30,15 @@ __device__ inline bool bwd_spec(const ScanParams& p, int j, int len) {
   return j < jl && (j + 1) * p.Lc + p.W + p.Kmax - 1 <= len;
 }
 
+// Retry pass: whether chunk `item` ran speculatively and its boundary spread
+// (measured by the verification kernel) exceeds the tolerance.  Every thread
+// reads the chunk's status before the block may rewrite it.
+__device__ inline bool retry_skip(const ScanParams& p, int item) {
+  const bool need = p.status[item] == 1 && (p.vstat[2 * item] - p.vstat[2 * item + 1] > (double)p.tol);
+  __syncthreads();
+  return !need;
+}
+
 // Block-wide max / min of a double (all threads receive the result).
 __device__ inline void block_minmax(double vmax, double vmin, double* red, double& omax, double& omin) {
   for (int m = 1; m < 64; m <<= 1) {
@@ -99,6 +108,15 @@ __device__ inline void finish_partition(const ScanParams& p, int b, int len, dou
       p.zout[b] = (float)(z2 * kLn2);
     }
   }
+}
+
+// Parameters of the retry pass: failed speculative chunks run again with a 4x
+// longer warm-up (exactly from the sequence end when that reaches it).
+inline ScanParams retry_params(const ScanParams& p) {
+  ScanParams q = p;
+  q.retry = 1;
+  q.W = 4 * p.W;
+  return q;
 }
 
 }  // namespace scan_detail
