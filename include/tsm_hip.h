@@ -39,6 +39,10 @@ extern "C" {
 #define TSM_SEMIRING_LOG 0
 #define TSM_SEMIRING_MAX 1
 
+#define TSM_VITERBI_AUTO 0       /* factorised for large problems when it fits, else exact */
+#define TSM_VITERBI_EXACT 1      /* the reference's fp32 operation order, bit-identical scores */
+#define TSM_VITERBI_FACTORISED 2 /* K*C + C^2 terms per step, chunked over all CUs */
+
 /* Library version (major*10000 + minor*100 + patch). */
 int tsm_version(void);
 
@@ -105,11 +109,23 @@ int tsm_backward(const float* cum_scores, const float* transition, const float* 
                  void* stream);
 
 /* ---------------------------------------------------------------------------
- * Exact Viterbi: the reference's fp32 max-semiring forward, bit for bit,
- * optionally with backpointers and an on-device backtrace.
+ * Viterbi: max-semiring score, optionally with an on-device backtrace.
  * Replaces:
  *   streaming/pytorch_reference.py:116-273 (semiring="max") -> score
  *   nn.py:444-531 SemiMarkovCRFHead._traceback_single        -> segments
+ * algorithm:
+ *   TSM_VITERBI_EXACT       the reference's fp32 operation order: scores are
+ *                           bit-identical, one workgroup per sequence, K*C^2
+ *                           terms per step;
+ *   TSM_VITERBI_FACTORISED  max-plus factorisation over source labels, chunked
+ *                           with verification like the log-semiring scan:
+ *                           scores within 1e-5 relative, segmentations identical
+ *                           when no two candidates tie;
+ *   TSM_VITERBI_AUTO        factorised for problems of >= 2^28 cells
+ *                           (B*T*K*C^2) when the register-resident scan fits,
+ *                           exact otherwise.
+ * Ties: the smallest duration, then the first source label, then the first
+ * final label (nn.py:472-501).
  * Outputs:
  *   score      (B,) fp32  max over final labels of alpha[len]
  *   seg_count  (B,) int32 number of segments (with_traceback only)
@@ -119,8 +135,8 @@ int tsm_backward(const float* cum_scores, const float* transition, const float* 
 int tsm_viterbi_workspace(int64_t B, int64_t T, int64_t C, int64_t K, int with_traceback, size_t* bytes);
 int tsm_viterbi(const float* cum_scores, const float* transition, const float* duration_bias,
                 const int64_t* lengths, const float* proj_start, const float* proj_end, int64_t B, int64_t T,
-                int64_t C, int64_t K, float* score, int with_traceback, int32_t* seg_count, int32_t* segments,
-                void* workspace, size_t workspace_bytes, void* stream);
+                int64_t C, int64_t K, float* score, int with_traceback, int algorithm, int32_t* seg_count,
+                int32_t* segments, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Ring checkpoints in the reference's layout (B, n_ckpt, K, C), raw alpha in

@@ -346,7 +346,8 @@ def viterbi_traceback_single(cum_b: torch.Tensor, transition, duration_bias, K: 
     """
     C = cum_b.shape[1]
     cum = cum_b.unsqueeze(0)
-    alpha = torch.full((seq_len + 1, C), NEG_INF, dtype=torch.float32)
+    # fp32 inputs reproduce the reference's table; fp64 inputs give the exact optimum
+    alpha = torch.full((seq_len + 1, C), NEG_INF, dtype=cum_b.dtype)
     alpha[0] = 0.0
     bp_k = torch.zeros((seq_len + 1, C), dtype=torch.long)
     bp_c = torch.zeros((seq_len + 1, C), dtype=torch.long)

@@ -292,19 +292,68 @@ def test_k1_full_size_config2_vs_hmm(scan_path):
 
 
 # --------------------------------------------------------------------------- exact Viterbi
+def _path_total_fp64(cum_b, tr, db, K, n, segs):
+    """Checks that ``segs`` (start, end, label, prev) tile [0, n) with durations
+    1..K-1 and chained labels, and returns its fp64 score."""
+    pos, total, prev = 0, 0.0, None
+    for (s, e, c, cp) in segs:
+        assert s == pos and s <= e and e - s + 1 <= max(K - 1, 1)
+        if prev is not None:
+            assert cp == prev
+        total += R.segment_score(cum_b, tr, db, K, s, e, c, cp)
+        pos, prev = e + 1, c
+    assert pos == n
+    return total
+
+
 @pytest.mark.parametrize("B,T,K,C,lengths", [(3, 120, 10, 6, [120, 77, 5]), (2, 60, 1, 4, [60, 31]),
-                                             (2, 200, 64, 32, [200, 150])])
-def test_viterbi_scores_and_segments_exact(B, T, K, C, lengths):
-    cum, tr, db, L, _, _ = rand_problem(B, T, K, C, 31 + C, lengths, tscale=0.5, dscale=0.5)
-    score, cnt, segs = ops.viterbi(cum.to(DEV), tr.to(DEV), db.to(DEV), L.to(DEV), K, None, None, True)
-    want, _, _ = R.forward(cum, tr, db, L, K, "max")
-    assert torch.equal(score.cpu(), want)
+                                             (2, 3000, 12, 8, [3000, 2200]), (2, 900, 40, 24, [900, 0])])
+@pytest.mark.parametrize("tie_free", [False, True])
+def test_viterbi_factorised_vs_fp64_optimum(B, T, K, C, lengths, tie_free):
+    """The factorised (chunked, verified) Viterbi: scores within 1e-5 of the fp64
+    optimum and a valid segmentation whose fp64 score is that optimum.  Runs of
+    one label tie exactly (durations of consecutive same-label segments can be
+    permuted at equal total), so the segmentation itself is compared bit-exactly
+    on tie-free inputs, where self-transitions are penalised out of every optimum.
+    The multi-chunk case exercises speculation in the max semiring."""
+    cum, tr, db, L, _, _ = rand_problem(B, T, K, C, 57 + C, lengths, tscale=0.5, dscale=0.5)
+    if tie_free:
+        tr = tr - 30.0 * torch.eye(C)
+    score, cnt, segs = ops.viterbi(cum.to(DEV), tr.to(DEV), db.to(DEV), L.to(DEV), K, None, None, True,
+                                   N.TSM_VITERBI_FACTORISED)
+    want, _, _ = R.forward(cum.double(), tr.double(), db.double(), L, K, "max")
+    live = L > 0
+    np.testing.assert_allclose(score.cpu()[live].double().numpy(), want[live].numpy(), rtol=1e-5)
     cnt = cnt.cpu()
     segs = segs.cpu()
     for b in range(B):
-        ref_segs, best = R.viterbi_traceback_single(cum[b], tr, db, K, int(L[b]))
+        n = int(L[b])
         got = [tuple(int(v) for v in segs[b, i]) for i in range(int(cnt[b]) - 1, -1, -1)]
-        assert got == [tuple(s) for s in ref_segs]
+        if n == 0:
+            assert got == []
+            continue
+        total = _path_total_fp64(cum[b].double(), tr.double(), db.double(), K, n, got)
+        assert abs(total - float(want[b])) <= 1e-5 * abs(float(want[b])) + 1e-6, b
+        if tie_free:
+            ref_segs, _ = R.viterbi_traceback_single(cum[b].double(), tr.double(), db.double(), K, n)
+            assert got == [tuple(s) for s in ref_segs], b
+    if T >= 3000:
+        assert N.plan_info(B, T, C, K)["P"] > 1
+
+
+def test_viterbi_auto_picks_factorised_for_large_problems():
+    B, T, K, C = 2, 20000, 64, 32
+    cum, tr, db, L, _, _ = rand_problem(B, T, K, C, 91, tscale=0.5, dscale=0.5)
+    args = (cum.to(DEV), tr.to(DEV), db.to(DEV), L.to(DEV), K, None, None, True)
+    s_auto, c_auto, g_auto = ops.viterbi(*args, N.TSM_VITERBI_AUTO)
+    s_fact, c_fact, g_fact = ops.viterbi(*args, N.TSM_VITERBI_FACTORISED)
+    s_ex, c_ex, g_ex = ops.viterbi(*args, N.TSM_VITERBI_EXACT)
+    assert torch.equal(s_auto, s_fact) and torch.equal(c_auto, c_fact)
+    for b in range(B):  # rows past the count are not written
+        n = int(c_auto[b])
+        assert torch.equal(g_auto[b, :n], g_fact[b, :n])
+    # the exact algorithm accumulates raw fp32 path scores (|score| ~ 1e5 here): allow its drift
+    np.testing.assert_allclose(s_fact.cpu().numpy(), s_ex.cpu().numpy(), rtol=5e-5)
 
 
 # --------------------------------------------------------------------------- head

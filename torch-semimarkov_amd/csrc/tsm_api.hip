@@ -337,11 +337,23 @@ size_t backward_ws_bytes(const Plan& pl) {
   return cv.off + 256;
 }
 
+// Viterbi workspace: backpointers, final labels, and the scan workspace of the
+// factorised algorithm (sized for whichever algorithm a call selects).
 size_t viterbi_ws_bytes(const Plan& pl, int with_tb) {
   Carver cv(nullptr);
   if (with_tb) cv.take<int32_t>((size_t)pl.B * (pl.T + 1) * pl.C);
   cv.take<int32_t>(pl.B);
+  if (pl.fast) carve_scan(cv, pl);
   return cv.off + 256;
+}
+
+// Factorised Viterbi is used for algorithm 2, and for algorithm 0 on problems
+// of at least 2^28 cells (B*T*K*C^2) when the register-resident scan fits.
+bool viterbi_factorised(const Plan& pl, int algorithm) {
+  if (algorithm == TSM_VITERBI_EXACT || !pl.fast) return false;
+  if (algorithm == TSM_VITERBI_FACTORISED) return true;
+  const double cells = (double)pl.B * pl.T * pl.K * (double)pl.C * pl.C;
+  return cells >= (double)(1 << 28);
 }
 
 }  // namespace
@@ -518,14 +530,42 @@ int tsm_viterbi_workspace(int64_t B, int64_t T, int64_t C, int64_t K, int with_t
 
 int tsm_viterbi(const float* cum, const float* tr, const float* db, const int64_t* len, const float* ps,
                 const float* pe, int64_t B, int64_t T, int64_t C, int64_t K, float* score, int with_tb,
-                int32_t* seg_count, int32_t* segments, void* workspace, size_t ws_bytes, void* stream) {
+                int algorithm, int32_t* seg_count, int32_t* segments, void* workspace, size_t ws_bytes,
+                void* stream) {
   int rc = check_common(cum, tr, db, len, TSM_SEMIRING_MAX);
   if (rc) return rc;
   if (!score) return fail(TSM_ERR_INVALID, "score output is required");
   if (with_tb && (!seg_count || !segments)) return fail(TSM_ERR_INVALID, "traceback needs seg_count and segments");
+  if (algorithm < TSM_VITERBI_AUTO || algorithm > TSM_VITERBI_FACTORISED)
+    return fail(TSM_ERR_INVALID, "algorithm must be TSM_VITERBI_AUTO (0), _EXACT (1) or _FACTORISED (2), got %d",
+                algorithm);
   Plan pl;
   rc = make_plan(B, T, C, K, ps != nullptr, pe != nullptr, &pl);
   if (rc) return rc;
+  if (algorithm == TSM_VITERBI_FACTORISED && !pl.fast)
+    return fail(TSM_ERR_UNSUPPORTED, "the factorised Viterbi needs the register-resident scan (C <= 64, rings in LDS)");
+  if (viterbi_factorised(pl, algorithm)) {
+    const size_t need = viterbi_ws_bytes(pl, with_tb);
+    if (!workspace || ws_bytes < need)
+      return fail(TSM_ERR_WORKSPACE, "viterbi workspace too small: %zu < %zu bytes", ws_bytes, need);
+    Carver cv(workspace);
+    int32_t* bp = with_tb ? cv.take<int32_t>((size_t)pl.B * (pl.T + 1) * pl.C) : nullptr;
+    cv.take<int32_t>(pl.B);
+    ScanWs w = carve_scan(cv, pl);
+    tsm::ScanParams p = scan_params(pl, w, cum, tr, db, len, ps, pe);
+    p.val = nullptr;
+    p.lvl = nullptr;
+    p.zout = score;
+    p.bp = bp;
+    hipStream_t st = (hipStream_t)stream;
+    int e = tsm::launch_scan_viterbi(pl, p, st);
+    if (e != hipSuccess) return hip_fail(e, "tsm_viterbi (factorised scan)");
+    if (with_tb) {
+      e = tsm::launch_backtrace_fact(pl, bp, w.fin, len, seg_count, segments, st);
+      if (e != hipSuccess) return hip_fail(e, "tsm_viterbi (backtrace)");
+    }
+    return TSM_OK;
+  }
   const DeviceInfo di = device_info();
   const size_t lds = tsm::viterbi_lds_bytes(pl.C, pl.Kmax, pl.RS, ps != nullptr);
   if (lds > (size_t)di.max_lds)

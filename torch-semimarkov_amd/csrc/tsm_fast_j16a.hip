@@ -49,4 +49,26 @@ int launch_margfast_j16_lo(const Plan& pl, const MargParams& q, hipStream_t st) 
   }
 }
 
+int launch_fast_max_j16_lo(const Plan& pl, const ScanParams& p, hipStream_t st) {
+  switch (pl.FR) {
+    case 1: return fastscan::launch_fast_max_jr<16, 1>(pl, p, st);
+    case 2: return fastscan::launch_fast_max_jr<16, 2>(pl, p, st);
+    case 3: return fastscan::launch_fast_max_jr<16, 3>(pl, p, st);
+    case 4: return fastscan::launch_fast_max_jr<16, 4>(pl, p, st);
+    case 5: return fastscan::launch_fast_max_jr<16, 5>(pl, p, st);
+    case 6: return fastscan::launch_fast_max_jr<16, 6>(pl, p, st);
+    case 7: return fastscan::launch_fast_max_jr<16, 7>(pl, p, st);
+    case 8: return fastscan::launch_fast_max_jr<16, 8>(pl, p, st);
+    case 9: return fastscan::launch_fast_max_jr<16, 9>(pl, p, st);
+    case 10: return fastscan::launch_fast_max_jr<16, 10>(pl, p, st);
+    case 11: return fastscan::launch_fast_max_jr<16, 11>(pl, p, st);
+    case 12: return fastscan::launch_fast_max_jr<16, 12>(pl, p, st);
+    case 13: return fastscan::launch_fast_max_jr<16, 13>(pl, p, st);
+    case 14: return fastscan::launch_fast_max_jr<16, 14>(pl, p, st);
+    case 15: return fastscan::launch_fast_max_jr<16, 15>(pl, p, st);
+    case 16: return fastscan::launch_fast_max_jr<16, 16>(pl, p, st);
+    default: return (int)hipErrorInvalidValue;
+  }
+}
+
 }  // namespace tsm

@@ -30,4 +30,30 @@ int launch_fast_j32(const Plan& pl, const ScanParams& p, bool fwd, hipStream_t s
   }
 }
 
+int launch_fast_max_j32(const Plan& pl, const ScanParams& p, hipStream_t st) {
+  switch (pl.FR) {
+    case 1: return fastscan::launch_fast_max_jr<32, 1>(pl, p, st);
+    case 2: return fastscan::launch_fast_max_jr<32, 2>(pl, p, st);
+    case 3: return fastscan::launch_fast_max_jr<32, 3>(pl, p, st);
+    case 4: return fastscan::launch_fast_max_jr<32, 4>(pl, p, st);
+    case 5: return fastscan::launch_fast_max_jr<32, 5>(pl, p, st);
+    case 6: return fastscan::launch_fast_max_jr<32, 6>(pl, p, st);
+    case 7: return fastscan::launch_fast_max_jr<32, 7>(pl, p, st);
+    case 8: return fastscan::launch_fast_max_jr<32, 8>(pl, p, st);
+    case 9: return fastscan::launch_fast_max_jr<32, 9>(pl, p, st);
+    case 10: return fastscan::launch_fast_max_jr<32, 10>(pl, p, st);
+    case 11: return fastscan::launch_fast_max_jr<32, 11>(pl, p, st);
+    case 12: return fastscan::launch_fast_max_jr<32, 12>(pl, p, st);
+    case 13: return fastscan::launch_fast_max_jr<32, 13>(pl, p, st);
+    case 14: return fastscan::launch_fast_max_jr<32, 14>(pl, p, st);
+    case 15: return fastscan::launch_fast_max_jr<32, 15>(pl, p, st);
+    case 16: return fastscan::launch_fast_max_jr<32, 16>(pl, p, st);
+    case 20: return fastscan::launch_fast_max_jr<32, 20>(pl, p, st);
+    case 24: return fastscan::launch_fast_max_jr<32, 24>(pl, p, st);
+    case 28: return fastscan::launch_fast_max_jr<32, 28>(pl, p, st);
+    case 32: return fastscan::launch_fast_max_jr<32, 32>(pl, p, st);
+    default: return (int)hipErrorInvalidValue;
+  }
+}
+
 }  // namespace tsm

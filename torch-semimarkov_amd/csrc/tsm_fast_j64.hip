@@ -18,4 +18,18 @@ int launch_fast_j64(const Plan& pl, const ScanParams& p, bool fwd, hipStream_t s
   }
 }
 
+int launch_fast_max_j64(const Plan& pl, const ScanParams& p, hipStream_t st) {
+  switch (pl.FR) {
+    case 1: return fastscan::launch_fast_max_jr<64, 1>(pl, p, st);
+    case 2: return fastscan::launch_fast_max_jr<64, 2>(pl, p, st);
+    case 3: return fastscan::launch_fast_max_jr<64, 3>(pl, p, st);
+    case 4: return fastscan::launch_fast_max_jr<64, 4>(pl, p, st);
+    case 5: return fastscan::launch_fast_max_jr<64, 5>(pl, p, st);
+    case 6: return fastscan::launch_fast_max_jr<64, 6>(pl, p, st);
+    case 7: return fastscan::launch_fast_max_jr<64, 7>(pl, p, st);
+    case 8: return fastscan::launch_fast_max_jr<64, 8>(pl, p, st);
+    default: return (int)hipErrorInvalidValue;
+  }
+}
+
 }  // namespace tsm

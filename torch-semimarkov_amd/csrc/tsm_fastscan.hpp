@@ -54,7 +54,7 @@ __device__ __forceinline__ void ring_put(double* ring_c, int a, double x, int RS
   if (a < KP) ring_c[a + RS] = x;
 }
 
-template <int J, int R, bool FWD>
+template <int J, int R, bool FWD, bool LOGSR>
 struct Chunk {
   // ---------------------------------------------------------------------------
   // One chunk of one sequence.
@@ -129,14 +129,26 @@ struct Chunk {
       if (FWD) {
         // alpha-hat[0] = 0 for every label; u[0,c] = (+)_{c'} trans[c',c]
         float m = kMinusInf;
+        int mi = 0x7fffffff;
 #pragma unroll
         for (int i = 0; i < kCJ; ++i)
-          if (lj + J * i < C) m = fmax2(m, trr[i]);
-        float sm = 0.0f;
+          if (lj + J * i < C && trr[i] > m) {
+            m = trr[i];
+            mi = lj + J * i;
+          }
+        float u0;
+        if constexpr (LOGSR) {
+          float sm = 0.0f;
 #pragma unroll
-        for (int i = 0; i < kCJ; ++i)
-          if (lj + J * i < C) sm += exp2_hw(trr[i] - m);
-        const float u0 = group_lse2<J>(m, sm);
+          for (int i = 0; i < kCJ; ++i)
+            if (lj + J * i < C) sm += exp2_hw(trr[i] - m);
+          u0 = group_lse2<J>(m, sm);
+        } else {
+          // Viterbi: best source label of a segment starting at position 0
+          const ValIdx best = group_argmax_first<J>(ValIdx{m, mi});
+          u0 = best.v;
+          if (p.bp != nullptr && cval && lj == 0 && j == 0) p.bp[((size_t)b * (T + 1)) * C + c] = best.i;
+        }
         v0 = u0 + ((has_ps && T > 0) ? ps_b[c] * kLog2e : 0.0f);
         if (g == 0) {
 #pragma unroll
@@ -222,22 +234,41 @@ struct Chunk {
       double e[R];
 #pragma unroll
       for (int r = 0; r < R; ++r) e[r] = rb[J * r];
-      double y0 = e[0] + dbr[0];
-      float s = 1.0f;
+      float a2;
+      int kbest = 0;
+      if constexpr (LOGSR) {
+        double y0 = e[0] + dbr[0];
+        float s = 1.0f;
 #pragma unroll
-      for (int r = 1; r < R; ++r) s += exp2_hw((float)((e[r] + dbr[r]) - y0));
-      if (__ballot(!(s <= FLT_MAX))) {
-        // a later term exceeds the first by more than the fp32 exponent range
-        double m = y0;
+        for (int r = 1; r < R; ++r) s += exp2_hw((float)((e[r] + dbr[r]) - y0));
+        if (__ballot(!(s <= FLT_MAX))) {
+          // a later term exceeds the first by more than the fp32 exponent range
+          double m = y0;
 #pragma unroll
-        for (int r = 1; r < R; ++r) m = fmax(m, e[r] + dbr[r]);
-        s = 0.0f;
+          for (int r = 1; r < R; ++r) m = fmax(m, e[r] + dbr[r]);
+          s = 0.0f;
 #pragma unroll
-        for (int r = 0; r < R; ++r) s += exp2_hw((float)((e[r] + dbr[r]) - m));
-        y0 = m;
+          for (int r = 0; r < R; ++r) s += exp2_hw((float)((e[r] + dbr[r]) - m));
+          y0 = m;
+        }
+        // the lane's terms relative to the previous position's level, combined over the group
+        a2 = group_lse2<J>((float)((y0 + cx_t) - lvl_prev), s) + pa_t;
+      } else {
+        // max over durations; ties go to the smallest duration (lanes hold ascending k)
+        double ym = e[0] + dbr[0];
+        int km = 1 + lj;
+#pragma unroll
+        for (int r = 1; r < R; ++r) {
+          const double y = e[r] + dbr[r];
+          if (y > ym) {
+            ym = y;
+            km = 1 + lj + J * r;
+          }
+        }
+        const ValIdx best = group_argmax_first<J>(ValIdx{(float)((ym + cx_t) - lvl_prev), km});
+        a2 = best.v + pa_t;
+        kbest = best.i;
       }
-      // the lane's terms relative to the previous position's level, combined over the group
-      const float a2 = group_lse2<J>((float)((y0 + cx_t) - lvl_prev), s) + pa_t;
       const int par = t & 1;
       if (cval && lj == 0) row[par * C + c] = a2;
       lds_barrier();
@@ -254,14 +285,30 @@ struct Chunk {
       const float mx = group_max<J>(ml);
       const double lvl_t = lvl_prev + (double)mx;
       float mq = kMinusInf;
+      int mqi = 0x7fffffff;
 #pragma unroll
       for (int i = 0; i < kCJ; ++i)
-        if (lj + J * i < C) mq = fmax2(mq, (rv[i] - mx) + trr[i]);
-      float sq = 0.0f;
+        if (lj + J * i < C) {
+          const float q = (rv[i] - mx) + trr[i];
+          if (q > mq) {
+            mq = q;
+            mqi = lj + J * i;
+          }
+        }
+      float mixv;
+      if constexpr (LOGSR) {
+        float sq = 0.0f;
 #pragma unroll
-      for (int i = 0; i < kCJ; ++i)
-        if (lj + J * i < C) sq += exp2_hw(((rv[i] - mx) + trr[i]) - mq);
-      const float mixv = group_lse2<J>(mq, sq);
+        for (int i = 0; i < kCJ; ++i)
+          if (lj + J * i < C) sq += exp2_hw(((rv[i] - mx) + trr[i]) - mq);
+        mixv = group_lse2<J>(mq, sq);
+      } else {
+        // Viterbi: best source label for a segment starting at t (first on ties)
+        const ValIdx best = group_argmax_first<J>(ValIdx{mq, mqi});
+        mixv = best.v;
+        if (FWD && p.bp != nullptr && cval && lj == 0 && (j == 0 || t > t_lo))
+          p.bp[((size_t)b * (T + 1) + t) * C + c] = (kbest << 16) | best.i;
+      }
 
       const bool owned = FWD ? (j == 0 || t > t_lo) : (t < t_hi || j == jl);
       if (FWD) {
@@ -313,7 +360,7 @@ struct Chunk {
 };
 
 // Parallel pass of one direction: one block per chunk, exact or speculative.
-template <int J, int R, bool FWD>
+template <int J, int R, bool FWD, bool LOGSR>
 __global__ void __launch_bounds__(R > 16 ? 512 : 1024) fast_scan_kernel(ScanParams p) {
   extern __shared__ __align__(16) char smem[];
   const int b = blockIdx.x / p.P, j = blockIdx.x % p.P;
@@ -326,13 +373,13 @@ __global__ void __launch_bounds__(R > 16 ? 512 : 1024) fast_scan_kernel(ScanPara
   if (p.retry && retry_skip(p, item)) return;
   const int mode = (FWD ? fwd_spec(p, j) : bwd_spec(p, j, len)) ? 1 : 0;
   if (threadIdx.x == 0) p.status[item] = mode;
-  Chunk<J, R, FWD>::run(p, smem, b, j, mode, nullptr, nullptr);
+  Chunk<J, R, FWD, LOGSR>::run(p, smem, b, j, mode, nullptr, nullptr);
 }
 
 // Sequential verification / repair of one direction: one block per sequence
 // walks its chunks, accepts a speculative chunk's frame offset when the
 // boundary spread is within tolerance, recomputes it exactly otherwise.
-template <int J, int R, bool FWD>
+template <int J, int R, bool FWD, bool LOGSR>
 __global__ void __launch_bounds__(R > 16 ? 512 : 1024) fast_fixup_kernel(ScanParams p) {
   extern __shared__ __align__(16) char smem[];
   const int b = blockIdx.x;
@@ -368,7 +415,7 @@ __global__ void __launch_bounds__(R > 16 ? 512 : 1024) fast_fixup_kernel(ScanPar
         F += 0.5 * (dmax + dmin);
         prev_recomputed = false;
       } else {
-        Chunk<J, R, FWD>::run(p, smem, b, j, 2, p.st_end + e * Kmax * C, p.lv_end + e * Kmax);
+        Chunk<J, R, FWD, LOGSR>::run(p, smem, b, j, 2, p.st_end + e * Kmax * C, p.lv_end + e * Kmax);
         __syncthreads();
         ++n_re;
         prev_recomputed = true;
@@ -379,17 +426,18 @@ __global__ void __launch_bounds__(R > 16 ? 512 : 1024) fast_fixup_kernel(ScanPar
   }
   __syncthreads();
   if (FWD) {
-    finish_partition<true>(p, b, len, F, n_re);
+    finish_partition<LOGSR>(p, b, len, F, n_re);
   } else if (threadIdx.x == 0 && p.recomputed != nullptr) {
     p.recomputed[b] = n_re;
   }
 }
 
-// Launch of one direction: parallel pass, verification, sequential repair, level offsets.
-template <int J, int R>
-int launch_fast_jr(const Plan& pl, const ScanParams& p, bool fwd, hipStream_t st) {
-  auto k = fwd ? fast_scan_kernel<J, R, true> : fast_scan_kernel<J, R, false>;
-  auto kf = fwd ? fast_fixup_kernel<J, R, true> : fast_fixup_kernel<J, R, false>;
+// Launch of one direction: parallel pass, verification, retry, sequential repair, level offsets.
+template <int J, int R, bool FWD, bool LOGSR>
+int launch_fast_dir(const Plan& pl, const ScanParams& p, hipStream_t st) {
+  const bool fwd = FWD;
+  auto k = fast_scan_kernel<J, R, FWD, LOGSR>;
+  auto kf = fast_fixup_kernel<J, R, FWD, LOGSR>;
   const size_t lds = pl.fast_lds;
   hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return e;
@@ -417,6 +465,17 @@ int launch_fast_jr(const Plan& pl, const ScanParams& p, bool fwd, hipStream_t st
   e = (hipError_t)launch_apply_offsets(pl, p, fwd, st);
   if (e != hipSuccess) return e;
   return hipGetLastError();
+}
+
+template <int J, int R>
+int launch_fast_jr(const Plan& pl, const ScanParams& p, bool fwd, hipStream_t st) {
+  return fwd ? launch_fast_dir<J, R, true, true>(pl, p, st) : launch_fast_dir<J, R, false, true>(pl, p, st);
+}
+
+// Max-semiring forward with backpointers (factorised Viterbi).
+template <int J, int R>
+int launch_fast_max_jr(const Plan& pl, const ScanParams& p, hipStream_t st) {
+  return launch_fast_dir<J, R, true, false>(pl, p, st);
 }
 
 }  // namespace fastscan

@@ -43,6 +43,10 @@ struct ScanParams {
   float* zout;             // (B) partition in natural log units
   // rings in global memory when LDS is too small
   float* gring;            // (B*P, scan_gring_floats)
+  // max-semiring forward of the register-resident scan: per (b, t, c) the best
+  // duration k of a segment ending at t and the best source label c' of a
+  // segment starting at t, packed (k << 16 | c'); null otherwise
+  int32_t* bp;
 };
 
 struct MargParams {
@@ -112,6 +116,16 @@ int launch_fast_j16_lo(const Plan& pl, const ScanParams& p, bool forward, hipStr
 int launch_fast_j16_hi(const Plan& pl, const ScanParams& p, bool forward, hipStream_t s);
 int launch_fast_j32(const Plan& pl, const ScanParams& p, bool forward, hipStream_t s);
 int launch_fast_j64(const Plan& pl, const ScanParams& p, bool forward, hipStream_t s);
+// max-semiring forward with backpointers (factorised Viterbi), per lane-group size
+int launch_fast_max_j8(const Plan& pl, const ScanParams& p, hipStream_t s);
+int launch_fast_max_j16(const Plan& pl, const ScanParams& p, hipStream_t s);
+int launch_fast_max_j16_lo(const Plan& pl, const ScanParams& p, hipStream_t s);
+int launch_fast_max_j16_hi(const Plan& pl, const ScanParams& p, hipStream_t s);
+int launch_fast_max_j32(const Plan& pl, const ScanParams& p, hipStream_t s);
+int launch_fast_max_j64(const Plan& pl, const ScanParams& p, hipStream_t s);
+int launch_scan_viterbi(const Plan& pl, const ScanParams& p, hipStream_t s);
+int launch_backtrace_fact(const Plan& pl, const int32_t* bp, const float* fin, const int64_t* lengths,
+                          int32_t* seg_count, int32_t* segs, hipStream_t s);
 // register-resident marginals (16 lanes per label, pl.MR durations per lane)
 int launch_margfast_j16(const Plan& pl, const MargParams& q, hipStream_t s);
 int launch_margfast_j16_lo(const Plan& pl, const MargParams& q, hipStream_t s);

@@ -760,6 +760,21 @@ int launch_any(const Plan& pl, const ScanParams& p, int semiring, bool fwd, hipS
 
 }  // namespace
 
+int launch_scan_viterbi(const Plan& pl, const ScanParams& p, hipStream_t st) {
+  ScanParams q = p;
+  q.RS = pl.FRS;
+  q.RL = pl.FRL;
+  q.R = pl.FR;
+  q.KP = pl.FJ * pl.FR;
+  switch (pl.FJ) {
+    case 8: return launch_fast_max_j8(pl, q, st);
+    case 16: return launch_fast_max_j16(pl, q, st);
+    case 32: return launch_fast_max_j32(pl, q, st);
+    case 64: return launch_fast_max_j64(pl, q, st);
+    default: return (int)hipErrorInvalidValue;
+  }
+}
+
 int launch_verify(const Plan& pl, const ScanParams& p, bool forward, hipStream_t st) {
   if (pl.P > 1) {
     TimedLaunch tl(kKVerify, st);

@@ -216,7 +216,54 @@ int launch_vit_j(const Plan& pl, const ViterbiParams& v, int with_tb, hipStream_
   return hipGetLastError();
 }
 
+// Backtrace of the factorised Viterbi (one thread per sequence).  bp[t,c] holds
+// (k << 16 | c') with k the best duration of a segment of label c ending at t
+// and c' the best source label of a segment of label c starting at t, so the
+// previous label of the segment [t-k, t-1] is bp[t-k, c] & 0xffff.  The final
+// label is the first maximiser of the normalised final row fin[b, :].
+__global__ void backtrace_fact_kernel(const int32_t* bp, const float* fin, const int64_t* lengths, int B, int T,
+                                      int C, int32_t* seg_count, int32_t* segs) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= B) return;
+  int64_t L64 = lengths[b];
+  const int len = (int)(L64 < 0 ? 0 : (L64 > T ? T : L64));
+  int c = 0;
+  float best = fin[(size_t)b * C];
+  for (int cc = 1; cc < C; ++cc) {
+    const float x = fin[(size_t)b * C + cc];
+    if (x > best) {
+      best = x;
+      c = cc;
+    }
+  }
+  int t = len, n = 0;
+  int32_t* out = segs + (size_t)b * T * 4;
+  const int32_t* bpb = bp + (size_t)b * (T + 1) * C;
+  while (t > 0 && n < T) {
+    const int k = bpb[(size_t)t * C + c] >> 16;
+    if (k <= 0 || k > t) break;
+    const int s = t - k;
+    const int cp = bpb[(size_t)s * C + c] & 0xffff;
+    out[4 * n + 0] = s;
+    out[4 * n + 1] = t - 1;
+    out[4 * n + 2] = c;
+    out[4 * n + 3] = cp;
+    ++n;
+    t = s;
+    c = cp;
+  }
+  seg_count[b] = n;
+}
+
 }  // namespace
+
+int launch_backtrace_fact(const Plan& pl, const int32_t* bp, const float* fin, const int64_t* lengths,
+                          int32_t* seg_count, int32_t* segs, hipStream_t s) {
+  TimedLaunch tl(kKBacktrace, s);
+  hipLaunchKernelGGL(backtrace_fact_kernel, dim3((pl.B + 63) / 64), dim3(64), 0, s, bp, fin, lengths, pl.B, pl.T,
+                     pl.C, seg_count, segs);
+  return hipGetLastError();
+}
 
 size_t viterbi_lds_bytes(int C, int Kmax, int RS, int has_ps) { return vit_lds_layout(C, Kmax, RS, has_ps).total; }
 

@@ -17,6 +17,9 @@ _lib = None
 
 TSM_SEMIRING_LOG = 0
 TSM_SEMIRING_MAX = 1
+TSM_VITERBI_AUTO = 0
+TSM_VITERBI_EXACT = 1
+TSM_VITERBI_FACTORISED = 2
 _ERRORS = {1: ValueError, 2: NotImplementedError, 3: RuntimeError, 4: RuntimeError}
 
 PLAN_FIELDS = (
@@ -43,7 +46,7 @@ _SIGNATURES = {
          _p, _p, _p, _p, _p, _p, _p, _sz, _p], _i32),
     "tsm_viterbi_workspace": ([_i64, _i64, _i64, _i64, _i32, ctypes.POINTER(_sz)], _i32),
     "tsm_viterbi": (
-        [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _i32, _p, _p, _p, _sz, _p], _i32),
+        [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _i32, _i32, _p, _p, _p, _sz, _p], _i32),
     "tsm_ring_checkpoints": ([_p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p], _i32),
     "tsm_timing_enable": ([_i32], _i32),
     "tsm_timing_read": ([ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i64), _i32], _i32),

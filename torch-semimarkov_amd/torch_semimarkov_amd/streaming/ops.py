@@ -126,10 +126,11 @@ def _(cum, transition, duration_bias, lengths, K, semiring, proj_start, proj_end
 @torch.library.custom_op("tsm_amd::viterbi", mutates_args=())
 def viterbi(
     cum: Tensor, transition: Tensor, duration_bias: Tensor, lengths: Tensor, K: int,
-    proj_start: Optional[Tensor], proj_end: Optional[Tensor], traceback: bool,
+    proj_start: Optional[Tensor], proj_end: Optional[Tensor], traceback: bool, algorithm: int = 0,
 ) -> tuple[Tensor, Tensor, Tensor]:
     """Score (B,) fp32; with ``traceback`` also seg_count (B,) int32 and segments (B,T,4) int32
-    (start, end, label, previous label; last segment first)."""
+    (start, end, label, previous label; last segment first).  ``algorithm``: 0 auto, 1 exact
+    (the reference's fp32 operation order), 2 factorised (see include/tsm_hip.h)."""
     lib = N.lib()
     B, Tp1, C = cum.shape
     T = Tp1 - 1
@@ -146,7 +147,7 @@ def viterbi(
     with torch.cuda.device(dev):
         rc = lib.tsm_viterbi(
             N.ptr(cum), N.ptr(transition), N.ptr(duration_bias), N.ptr(lengths),
-            N.ptr(proj_start), N.ptr(proj_end), B, T, C, K, N.ptr(score), int(traceback),
+            N.ptr(proj_start), N.ptr(proj_end), B, T, C, K, N.ptr(score), int(traceback), int(algorithm),
             N.ptr(cnt) if traceback else None, N.ptr(segs) if traceback else None,
             N.ptr(ws), ws.numel(), _stream(dev),
         )
@@ -155,7 +156,7 @@ def viterbi(
 
 
 @viterbi.register_fake
-def _(cum, transition, duration_bias, lengths, K, proj_start, proj_end, traceback):
+def _(cum, transition, duration_bias, lengths, K, proj_start, proj_end, traceback, algorithm=0):
     B, Tp1, C = cum.shape
     if traceback:
         return (cum.new_empty(B), cum.new_empty(B, dtype=torch.int32),
