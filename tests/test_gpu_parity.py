@@ -341,6 +341,24 @@ def test_viterbi_factorised_vs_fp64_optimum(B, T, K, C, lengths, tie_free):
         assert N.plan_info(B, T, C, K)["P"] > 1
 
 
+@pytest.mark.parametrize("B,T,K,C,lengths", [(3, 150, 9, 5, [150, 64, 1]), (2, 1200, 16, 12, [1200, 700])])
+def test_viterbi_factorised_with_projections(B, T, K, C, lengths):
+    """Factorised Viterbi with proj_start / proj_end: scores within 1e-5 of the
+    fp64 optimum, and on tie-free inputs the same segments as the exact kernel
+    (the reference's fp32 operation order)."""
+    cum, tr, db, L, ps, pe = rand_problem(B, T, K, C, 71 + C, lengths, proj=True, tscale=0.5, dscale=0.5)
+    tr = tr - 30.0 * torch.eye(C)
+    args = to_dev(cum, tr, db, L) + [K] + to_dev(ps, pe) + [True]
+    s_f, c_f, g_f = ops.viterbi(*args, N.TSM_VITERBI_FACTORISED)
+    s_e, c_e, g_e = ops.viterbi(*args, N.TSM_VITERBI_EXACT)
+    want, _, _ = R.forward(cum.double(), tr.double(), db.double(), L, K, "max", ps.double(), pe.double())
+    np.testing.assert_allclose(s_f.cpu().double().numpy(), want.numpy(), rtol=1e-5)
+    assert torch.equal(c_f, c_e)
+    for b in range(B):
+        n = int(c_f[b])
+        assert torch.equal(g_f[b, :n], g_e[b, :n]), b
+
+
 def test_viterbi_auto_picks_factorised_for_large_problems():
     B, T, K, C = 2, 20000, 64, 32
     cum, tr, db, L, _, _ = rand_problem(B, T, K, C, 91, tscale=0.5, dscale=0.5)
