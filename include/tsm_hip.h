@@ -13,7 +13,12 @@
  * Conventions (reference: biobenkj/torch-semimarkov README.md:96-125,
  * src/torch_semimarkov/streaming/pytorch_reference.py:86-111):
  *   cum_scores      (B, T+1, C)  cumulative projected scores, row 0 = 0
- *   transition      (C, C)       transition[c_src][c_dst]
+ *   transition      (C, C)       transition[c_src][c_dst], or with trans_rows > 0
+ *                   (trans_rows, C, C)  transition[k][c_src][c_dst] for a segment of
+ *                                duration k (reference pytorch_reference.py:104-109,
+ *                                triton_forward.py:613-616 has_duration_transitions);
+ *                                durations 1..max(K-1,1) are used, so trans_rows
+ *                                must be >= max(K-1,1)+1; C <= 128
  *   duration_bias   (K, C)       K = max_duration; durations 1..K-1 use row
  *                                min(k, K-1); K = 1 uses duration 1, row 0
  *   lengths         (B,) int64   0 <= lengths[b] <= T (clamped on device)
@@ -53,13 +58,16 @@ const char* tsm_last_error(void);
  * Launch plan for a problem shape, for diagnostics and tests.  Fills up to
  * `n` int64 host values: J, NT, RS, P, Lc, W, global_rings, scan_lds, NB, TB,
  * CB, NCB, JM, NTM, marg_lds, Kmax, n_cu, R, KP, RMAX, fast, FJ, FR, FNT,
- * fast_lds, mfast, MR (fast = 1: log-semiring scans use the register-resident
- * kernels with FJ lanes per label and FR durations per lane; mfast = 1: the
- * marginals use the register-resident kernel with MR durations per lane; the
- * environment variable TSM_SCAN_PATH=generic turns both off).
+ * fast_lds, mfast, MR, dense, DJ, DNT, dtrl, dense_lds, DG, DNTM, DNB, DTB,
+ * dmarg_lds (fast = 1: log-semiring scans use the register-resident kernels with
+ * FJ lanes per label and FR durations per lane; mfast = 1: the marginals use
+ * the register-resident kernel with MR durations per lane; the environment
+ * variable TSM_SCAN_PATH=generic turns both off; dense = 1: duration-dependent
+ * transitions, dense scans with DJ lanes per label, transitions in LDS when
+ * dtrl = 1, dense marginals in DNB blocks of DTB positions).
  */
-int tsm_plan_info(int64_t B, int64_t T, int64_t C, int64_t K, int has_proj_start, int has_proj_end,
-                  int64_t* out, int n);
+int tsm_plan_info(int64_t B, int64_t T, int64_t C, int64_t K, int64_t trans_rows, int has_proj_start,
+                  int has_proj_end, int64_t* out, int n);
 
 /* ---------------------------------------------------------------------------
  * Forward: log partition (semiring LOG) or Viterbi score of the factorised,
@@ -76,11 +84,11 @@ int tsm_plan_info(int64_t B, int64_t T, int64_t C, int64_t K, int has_proj_start
  *   state a later tsm_backward() call needs; pass both NULL for inference.
  *   recomputed      (B,) int32  chunks recomputed by the verifier, or NULL
  * ------------------------------------------------------------------------- */
-int tsm_forward_workspace(int64_t B, int64_t T, int64_t C, int64_t K, int semiring, int has_proj_start,
-                          int has_proj_end, size_t* bytes);
+int tsm_forward_workspace(int64_t B, int64_t T, int64_t C, int64_t K, int64_t trans_rows, int semiring,
+                          int has_proj_start, int has_proj_end, size_t* bytes);
 int tsm_forward(const float* cum_scores, const float* transition, const float* duration_bias,
                 const int64_t* lengths, const float* proj_start, const float* proj_end, int64_t B, int64_t T,
-                int64_t C, int64_t K, int semiring, float* partition, double* log2_partition,
+                int64_t C, int64_t K, int64_t trans_rows, int semiring, float* partition, double* log2_partition,
                 float* alpha_hat, double* alpha_level, int32_t* recomputed, void* workspace,
                 size_t workspace_bytes, void* stream);
 
@@ -95,14 +103,17 @@ int tsm_forward(const float* cum_scores, const float* transition, const float* d
  * Outputs (all fully written):
  *   grad_cum        (B, T+1, C)  already scaled by grad_output[b]
  *   grad_transition (C, C)       sum_b grad_output[b] * d/dtransition
+ *                   (trans_rows, C, C) with duration-dependent transitions (matrices
+ *                                that no duration uses get zeros)
  *   grad_duration_bias (K, C)
  *   grad_proj_start, grad_proj_end (B, T, C) or NULL
  * ------------------------------------------------------------------------- */
-int tsm_backward_workspace(int64_t B, int64_t T, int64_t C, int64_t K, int has_proj_start, int has_proj_end,
-                           size_t* bytes);
+int tsm_backward_workspace(int64_t B, int64_t T, int64_t C, int64_t K, int64_t trans_rows, int has_proj_start,
+                           int has_proj_end, size_t* bytes);
 int tsm_backward(const float* cum_scores, const float* transition, const float* duration_bias,
                  const int64_t* lengths, const float* proj_start, const float* proj_end, int64_t B, int64_t T,
-                 int64_t C, int64_t K, int semiring, const float* alpha_hat, const double* alpha_level,
+                 int64_t C, int64_t K, int64_t trans_rows, int semiring, const float* alpha_hat,
+                 const double* alpha_level,
                  const double* log2_partition, const float* grad_output, float* grad_cum,
                  float* grad_transition, float* grad_duration_bias, float* grad_proj_start,
                  float* grad_proj_end, int32_t* recomputed, void* workspace, size_t workspace_bytes,
@@ -124,6 +135,8 @@ int tsm_backward(const float* cum_scores, const float* transition, const float* 
  *   TSM_VITERBI_AUTO        factorised for problems of >= 2^28 cells
  *                           (B*T*K*C^2) when the register-resident scan fits,
  *                           exact otherwise.
+ * Duration-dependent transitions (trans_rows > 0) always run the exact kernel
+ * (the factorisation does not hold; TSM_VITERBI_FACTORISED is refused).
  * Ties: the smallest duration, then the first source label, then the first
  * final label (nn.py:472-501).
  * Outputs:
@@ -132,10 +145,12 @@ int tsm_backward(const float* cum_scores, const float* transition, const float* 
  *   segments   (B, T, 4) int32 rows (start, end inclusive, label, previous
  *              label), last segment first (with_traceback only)
  * ------------------------------------------------------------------------- */
-int tsm_viterbi_workspace(int64_t B, int64_t T, int64_t C, int64_t K, int with_traceback, size_t* bytes);
+int tsm_viterbi_workspace(int64_t B, int64_t T, int64_t C, int64_t K, int64_t trans_rows, int with_traceback,
+                          size_t* bytes);
 int tsm_viterbi(const float* cum_scores, const float* transition, const float* duration_bias,
                 const int64_t* lengths, const float* proj_start, const float* proj_end, int64_t B, int64_t T,
-                int64_t C, int64_t K, float* score, int with_traceback, int algorithm, int32_t* seg_count,
+                int64_t C, int64_t K, int64_t trans_rows, float* score, int with_traceback, int algorithm,
+                int32_t* seg_count,
                 int32_t* segments, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------

@@ -30,7 +30,7 @@ GRAD_TOL = dict(rtol=1e-5, atol=1e-4)
 
 STREAM_FIXTURES = [
     "stream_basic", "stream_varlen", "stream_k1", "stream_c24", "stream_t1", "stream_t2",
-    "stream_proj", "stream_max", "stream_nocentre", "stream_medium",
+    "stream_proj", "stream_max", "stream_nocentre", "stream_medium", "stream_durtrans",
 ]
 
 
@@ -152,11 +152,98 @@ def test_inference_matches_reference_golden(name):
     assert torch.equal(vit.cpu(), want_max)
 
 
-def test_duration_dependent_transitions_not_supported():
-    z = load_golden("stream_durtrans")
-    cum, tr, db, L, K, sr, ps, pe = fixture_inputs(z)
-    with pytest.raises(NotImplementedError):
-        tsa.semi_crf_streaming_forward(cum, tr, db, L, K)
+# --------------------------------------------------------------------------- (K, C, C) transitions
+def rand_trans3(rows, C, seed, scale=0.3):
+    g = torch.Generator().manual_seed(seed)
+    return scale * torch.randn(rows, C, C, generator=g)
+
+
+# B, T, K, C, lengths, proj, semiring, expected plan entries.  Together they cover
+# 4 / 16 / 64 lanes per label, transitions in LDS and in global memory, label
+# groups with several destination labels (C = 40) and several source labels per
+# lane (C = 70) in the marginal kernel, projections and the max semiring.
+DURTRANS_CASES = [
+    (2, 30, 5, 4, [30, 17], False, "log", dict(DJ=4, dtrl=1)),
+    (2, 50, 9, 3, [50, 50], True, "log", dict(DJ=4)),
+    (2, 45, 12, 6, [45, 30], False, "max", dict(DJ=16)),
+    (2, 40, 40, 5, [40, 33], True, "log", dict(DJ=64)),
+    (1, 60, 10, 40, None, False, "log", dict(DJ=16, DG=64)),
+    (1, 40, 6, 70, None, True, "log", dict(DJ=4, DG=64)),
+    (1, 80, 60, 24, None, False, "log", dict(DJ=16, dtrl=0)),
+    (3, 28, 7, 4, [28, 6, 0], False, "log", dict()),
+]
+
+
+@pytest.mark.parametrize("B,T,K,C,lengths,proj,sr,plan", DURTRANS_CASES)
+def test_duration_dependent_transitions_vs_fp64_oracle(B, T, K, C, lengths, proj, sr, plan):
+    got = N.plan_info(B, T, C, K, proj, proj, trans_rows=K)
+    assert got["dense"] == 1
+    for key, v in plan.items():
+        assert got[key] == v, (key, got)
+    cum, _, db, L, ps, pe = rand_problem(B, T, K, C, 4000 + T + K + C, lengths, proj)
+    tr = rand_trans3(K, C, 17 + C)
+    g = torch.linspace(0.5, 2.0, B)
+    p64, g64 = oracle_fp64(cum, tr, db, L, K, sr, ps, pe, g)
+    part, grads = run_hip(cum, tr, db, L, K, sr, ps, pe, g)
+    np.testing.assert_allclose(part.double().numpy(), p64.numpy(), rtol=RTOL_Z, atol=1e-6)
+    assert grads[1].shape == (K, C, C)
+    assert_grads(grads, g64)
+
+
+def test_duration_dependent_transitions_chunked_vs_fp64_oracle():
+    """Long sequences: the dense scans run chunked, speculative and verified."""
+    B, T, K, C = 2, 3000, 8, 6
+    assert N.plan_info(B, T, C, K, trans_rows=K)["P"] > 1
+    cum, _, db, L, _, _ = rand_problem(B, T, K, C, 4242, [3000, 2200])
+    tr = rand_trans3(K, C, 99)
+    g = torch.tensor([1.0, 0.5])
+    p64, g64 = oracle_fp64(cum, tr, db, L, K, "log", g=g)
+    cum_d, tr_d, db_d = to_dev(cum, tr, db)
+    out = ops.scan_forward(cum_d, tr_d, db_d, L.to(DEV), K, N.TSM_SEMIRING_LOG, None, None, True)
+    assert int(out[4].sum()) == 0  # every speculative chunk verified
+    part, grads = run_hip(cum, tr, db, L, K, "log", g=g)
+    np.testing.assert_allclose(part.double().numpy(), p64.numpy(), rtol=RTOL_Z)
+    assert_grads(grads, g64)
+
+
+def test_duration_dependent_transitions_k1_and_extra_matrices():
+    """K = 1 uses duration 1 and so transition[1] (a 2-matrix table): the same
+    problem as the static transition transition[1].  Matrices no duration uses
+    (index 0, and indices beyond max(K-1, 1)) get zero gradients."""
+    B, T, C = 2, 40, 5
+    cum, tr2, db, L, _, _ = rand_problem(B, T, 1, C, 808, [40, 29])
+    tr3 = torch.stack([torch.randn(C, C), tr2, torch.randn(C, C)])  # 3 matrices, only [1] used
+    p2, g2 = run_hip(cum, tr2, db, L, 1)
+    p3, g3 = run_hip(cum, tr3, db, L, 1)
+    np.testing.assert_allclose(p3.numpy(), p2.numpy(), rtol=1e-6)
+    np.testing.assert_allclose(g3[1][1].numpy(), g2[1].numpy(), rtol=1e-5, atol=1e-6)
+    assert torch.all(g3[1][0] == 0) and torch.all(g3[1][2] == 0)
+    for a, b in ((g3[0], g2[0]), (g3[2], g2[2])):
+        np.testing.assert_allclose(a.numpy(), b.numpy(), rtol=1e-5, atol=1e-6)
+    with pytest.raises(ValueError, match="duration-dependent transition"):
+        tsa.semi_crf_streaming_forward(cum.to(DEV), tr3[:1].to(DEV), db.to(DEV), L, 1)
+
+
+def test_duration_dependent_transitions_viterbi_exact():
+    """Inference in the max semiring with (K, C, C) transitions: the exact kernel,
+    bit-identical to the reference's fp32 recursion, with the segmentation of its
+    traceback; the factorised algorithm is refused."""
+    B, T, K, C = 3, 90, 8, 5
+    cum, _, db, L, _, _ = rand_problem(B, T, K, C, 515, [90, 61, 4], tscale=0.5, dscale=0.5)
+    tr = rand_trans3(K, C, 23, scale=0.8)
+    args = to_dev(cum, tr, db, L) + [K, None, None, True]
+    score, cnt, segs = ops.viterbi(*args, N.TSM_VITERBI_AUTO)
+    want, _, _ = R.forward(cum, tr, db, L, K, "max")
+    assert torch.equal(score.cpu(), want)
+    with torch.no_grad():
+        vit = tsa.semi_crf_streaming_forward(*to_dev(cum, tr, db), L, K, semiring="max")
+    assert torch.equal(vit.cpu(), want)
+    for b in range(B):
+        ref_segs, _ = R.viterbi_traceback_single(cum[b], tr, db, K, int(L[b]))
+        got = [tuple(int(v) for v in segs[b, i]) for i in range(int(cnt[b]) - 1, -1, -1)]
+        assert got == [tuple(s) for s in ref_segs]
+    with pytest.raises(NotImplementedError, match="static"):
+        ops.viterbi(*args, N.TSM_VITERBI_FACTORISED)
 
 
 # --------------------------------------------------------------------------- fp64 oracle

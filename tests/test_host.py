@@ -39,10 +39,10 @@ def test_version_and_error_message():
     lib = N.lib()
     assert lib.tsm_version() >= 100
     out = ctypes.c_size_t(0)
-    rc = lib.tsm_forward_workspace(0, 10, 4, 3, 0, 0, 0, ctypes.byref(out))
+    rc = lib.tsm_forward_workspace(0, 10, 4, 3, 0, 0, 0, 0, ctypes.byref(out))
     assert rc == 1
     assert b"B, T, C, K" in lib.tsm_last_error()
-    rc = lib.tsm_forward_workspace(1, 10, 4, 3, 7, 0, 0, ctypes.byref(out))
+    rc = lib.tsm_forward_workspace(1, 10, 4, 3, 0, 7, 0, 0, ctypes.byref(out))
     assert rc == 1 and b"semiring" in lib.tsm_last_error()
 
 
@@ -57,31 +57,54 @@ def test_plan_and_workspace_queries_without_gpu():
     # large label spaces split the marginal kernel into label blocks
     q = N.plan_info(8, 50_000, 128, 500)
     assert q["CB"] * q["NCB"] >= 128 and q["marg_lds"] <= 160 * 1024
-    for fn, args in (
-        (N.lib().tsm_forward_workspace, (2, 100, 8, 5, 0, 0, 0)),
-        (N.lib().tsm_backward_workspace, (2, 100, 8, 5, 1, 1)),
-        (N.lib().tsm_viterbi_workspace, (2, 100, 8, 5, 1)),
-    ):
-        out = ctypes.c_size_t(0)
-        assert fn(*args, ctypes.byref(out)) == 0 and out.value > 0
+    for tr_rows in (0, 5):
+        for fn, args in (
+            (N.lib().tsm_forward_workspace, (2, 100, 8, 5, tr_rows, 0, 0, 0)),
+            (N.lib().tsm_backward_workspace, (2, 100, 8, 5, tr_rows, 1, 1)),
+            (N.lib().tsm_viterbi_workspace, (2, 100, 8, 5, tr_rows, 1)),
+        ):
+            out = ctypes.c_size_t(0)
+            assert fn(*args, ctypes.byref(out)) == 0 and out.value > 0
+
+
+def test_duration_dependent_transition_plans_without_gpu():
+    """(K, C, C) transitions: the dense path replaces the factorised ones; one
+    matrix per duration index 1..max(K-1, 1) is required; C <= 128."""
+    p = N.plan_info(2, 3000, 8, 12, trans_rows=12)
+    assert p["dense"] == 1 and p["fast"] == 0 and p["mfast"] == 0
+    assert p["DNT"] % 64 == 0 and p["DNT"] >= 8 * p["DJ"] and p["dtrl"] == 1
+    assert p["DTB"] >= p["Kmax"] and p["DNB"] * p["DTB"] >= 3000
+    assert p["DG"] >= 8 and p["DNTM"] <= 1024
+    # transitions too large for LDS are read from the global table
+    big = N.plan_info(1, 1000, 64, 100, trans_rows=100)
+    assert big["dense"] == 1 and big["dtrl"] == 0
+    assert N.plan_info(2, 100, 8, 5)["dense"] == 0
+    lib = N.lib()
+    out = (ctypes.c_int64 * 4)()
+    assert lib.tsm_plan_info(2, 100, 8, 5, 4, 0, 0, out, 4) == 1  # needs >= Kmax + 1 = 5 matrices
+    assert b"trans_rows >= 5" in lib.tsm_last_error()
+    assert lib.tsm_plan_info(2, 100, 8, 1, 1, 0, 0, out, 4) == 1  # K = 1 uses duration 1: two matrices
+    assert lib.tsm_plan_info(2, 100, 8, 1, 2, 0, 0, out, 4) == 0
+    assert lib.tsm_plan_info(2, 100, 200, 5, 5, 0, 0, out, 4) == 2
+    assert lib.tsm_plan_info(2, 100, 8, 5, -1, 0, 0, out, 4) == 1
 
 
 def test_c_abi_rejects_bad_calls_without_touching_the_device():
     lib = N.lib()
     # missing required pointers
-    rc = lib.tsm_forward(None, None, None, None, None, None, 1, 10, 4, 3, 0, None, None, None, None, None,
+    rc = lib.tsm_forward(None, None, None, None, None, None, 1, 10, 4, 3, 0, 0, None, None, None, None, None,
                          None, 0, None)
     assert rc == 1
     # workspace too small is reported before any launch
     buf = ctypes.create_string_buffer(16)
     fake = ctypes.addressof(buf)
-    rc = lib.tsm_forward(fake, fake, fake, fake, None, None, 1, 10, 4, 3, 0, fake, None, None, None, None,
+    rc = lib.tsm_forward(fake, fake, fake, fake, None, None, 1, 10, 4, 3, 0, 0, fake, None, None, None, None,
                          fake, 1, None)
     assert rc == 4 and b"workspace" in lib.tsm_last_error()
-    rc = lib.tsm_forward(fake, fake, fake, fake, None, None, 1, 10, 4, 3, 0, fake, None, fake, None, None,
+    rc = lib.tsm_forward(fake, fake, fake, fake, None, None, 1, 10, 4, 3, 0, 0, fake, None, fake, None, None,
                          fake, 10**9, None)
     assert rc == 1 and b"alpha_hat and alpha_level" in lib.tsm_last_error()
-    rc = lib.tsm_plan_info(1, 10, 600, 3, 0, 0, None, 0)
+    rc = lib.tsm_plan_info(1, 10, 600, 3, 0, 0, 0, None, 0)
     assert rc == 2
 
 

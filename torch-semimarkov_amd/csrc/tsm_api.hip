@@ -117,13 +117,70 @@ void plan_fast(Plan& p, const DeviceInfo& di) {
   }
 }
 
+// Duration-dependent transitions: dense scans (J lanes per label, transitions
+// in LDS when they fit) and the dense marginal kernel (label groups of G lanes,
+// blocks of TB >= Kmax start positions whose start / end sums fit in LDS).
+int plan_dense(Plan& p, const DeviceInfo& di) {
+  const int C = p.C, Kmax = p.Kmax;
+  if (C > 128)
+    return fail(TSM_ERR_UNSUPPORTED, "duration-dependent transitions support C <= 128 (got C=%d)", C);
+  int kp2 = 4;
+  while (kp2 < Kmax) kp2 <<= 1;
+  int J = 4;
+  for (int cand : {64, 16})
+    if (C * cand <= 1024 && cand <= kp2) {
+      J = cand;
+      break;
+    }
+  p.DJ = J;
+  p.DNT = (int)cdiv((int64_t)C * J, 64) * 64;
+  p.DRS = Kmax + 1;
+  p.dtrl = 1;
+  size_t lds = tsm::dense_lds_layout(C, Kmax, p.DRS, 1).total;
+  if (lds > (size_t)di.max_lds) {
+    p.dtrl = 0;
+    lds = tsm::dense_lds_layout(C, Kmax, p.DRS, 0).total;
+    if (lds > (size_t)di.max_lds)
+      return fail(TSM_ERR_UNSUPPORTED, "duration-dependent transitions: C=%d, K=%d needs %zu bytes of LDS (> %d)", C,
+                  p.K, lds, di.max_lds);
+  }
+  p.dense_lds = lds;
+  int G = 1;
+  while (G < C && G < 64) G <<= 1;
+  p.DG = G;
+  p.DNTM = (int)std::min<int64_t>(1024, cdiv((int64_t)C * G, 64) * 64);
+  // about two blocks per CU, at most 512 MiB of fp64 transition partials
+  const int64_t per_block = (int64_t)Kmax * C * C * 8;
+  int64_t NB = cdiv(2 * (int64_t)di.n_cu, p.B);
+  NB = std::min<int64_t>(NB, std::max<int64_t>(1, p.T / std::max(Kmax, 64)));
+  NB = std::min<int64_t>(NB, std::max<int64_t>(1, ((int64_t)512 << 20) / (per_block * p.B)));
+  NB = std::max<int64_t>(NB, 1);
+  int64_t TB = cdiv(p.T, NB);
+  if (TB < Kmax) TB = Kmax;
+  size_t ml = tsm::dense_marg_lds_layout(C, Kmax, (int)TB).total;
+  while (ml > (size_t)di.max_lds && TB > Kmax) {
+    TB = std::max<int64_t>(Kmax, TB / 2);
+    ml = tsm::dense_marg_lds_layout(C, Kmax, (int)TB).total;
+  }
+  if (ml > (size_t)di.max_lds)
+    return fail(TSM_ERR_UNSUPPORTED, "duration-dependent transitions: marginals for C=%d, K=%d need %zu bytes of LDS (> %d)",
+                C, p.K, ml, di.max_lds);
+  p.DTB = (int)TB;
+  p.DNB = (int)cdiv(p.T, TB);
+  p.dmarg_lds = ml;
+  p.dense = 1;
+  return TSM_OK;
+}
+
 // Thread mapping, rings, chunking and marginal blocking for a problem shape.
-int make_plan(int64_t B, int64_t T, int64_t C, int64_t K, int has_ps, int has_pe, Plan* out) {
+// trows > 0: the transition is (trows, C, C), one matrix per duration index.
+int make_plan(int64_t B, int64_t T, int64_t C, int64_t K, int has_ps, int has_pe, int64_t trows, Plan* out) {
   if (B < 1 || T < 1 || C < 1 || K < 1) return fail(TSM_ERR_INVALID, "need B, T, C, K >= 1 (got %lld, %lld, %lld, %lld)",
                                                     (long long)B, (long long)T, (long long)C, (long long)K);
   if (C > 512) return fail(TSM_ERR_UNSUPPORTED, "num_classes C=%lld > 512 is not supported", (long long)C);
   if (K > 65535) return fail(TSM_ERR_UNSUPPORTED, "max_duration K=%lld > 65535 is not supported", (long long)K);
   if (T > (int64_t)1 << 30) return fail(TSM_ERR_UNSUPPORTED, "T=%lld is too long", (long long)T);
+  if (trows < 0) return fail(TSM_ERR_INVALID, "trans_rows must be >= 0 (got %lld)", (long long)trows);
   const DeviceInfo di = device_info();
   Plan p{};
   p.B = (int)B;
@@ -195,6 +252,17 @@ int make_plan(int64_t B, int64_t T, int64_t C, int64_t K, int has_ps, int has_pe
   }
   p.NB = (int)NB;
   p.TB = (int)TB;
+  p.trows = (int)trows;
+  if (trows > 0) {
+    if (trows < p.Kmax + 1)
+      return fail(TSM_ERR_INVALID,
+                  "duration-dependent transitions are indexed by duration 1..%d: need trans_rows >= %d, got %lld",
+                  p.Kmax, p.Kmax + 1, (long long)trows);
+    const int rc = plan_dense(p, di);
+    if (rc) return rc;
+    *out = p;
+    return TSM_OK;
+  }
   plan_fast(p, di);
   p.mfast = 0;
   const char* env = getenv("TSM_SCAN_PATH");
@@ -317,9 +385,30 @@ int check_common(const float* cum, const float* tr, const float* db, const int64
   return TSM_OK;
 }
 
+// log2-scaled transition tables of both directions (duration-dependent transitions)
+struct DenseTr {
+  float *trf, *trb;
+};
+
+DenseTr carve_dense(Carver& cv, const Plan& p) {
+  DenseTr d{nullptr, nullptr};
+  if (!p.dense) return d;
+  d.trf = cv.take<float>((size_t)p.Kmax * p.C * p.C);
+  d.trb = cv.take<float>((size_t)p.Kmax * p.C * p.C);
+  return d;
+}
+
+// Marginal blocking of the plan's marginal kernel
+int marg_nb(const Plan& p) { return p.dense ? p.DNB : p.NB; }
+int marg_tb(const Plan& p) { return p.dense ? p.DTB : p.TB; }
+size_t tr_part_len(const Plan& p) {
+  return (size_t)p.B * marg_nb(p) * (p.dense ? (size_t)p.Kmax : 1) * p.C * p.C;
+}
+
 size_t forward_ws_bytes(const Plan& pl) {
   Carver cv(nullptr);
   carve_scan(cv, pl);
+  carve_dense(cv, pl);
   return cv.off + 256;
 }
 
@@ -331,9 +420,10 @@ size_t backward_ws_bytes(const Plan& pl) {
   carve_scan(cv, pl);
   cv.take<float>(rows * pl.C);   // e_own
   cv.take<float>(rows * pl.C);   // s_out
-  cv.take<float>((size_t)pl.B * pl.NB * pl.Kmax * pl.C);   // halo
-  cv.take<double>((size_t)pl.B * pl.NB * pl.Kmax * pl.C);  // db_part
-  cv.take<double>((size_t)pl.B * pl.NB * pl.C * pl.C);     // tr_part
+  cv.take<float>((size_t)pl.B * marg_nb(pl) * pl.Kmax * pl.C);   // halo
+  cv.take<double>((size_t)pl.B * marg_nb(pl) * pl.Kmax * pl.C);  // db_part
+  cv.take<double>(tr_part_len(pl));                              // tr_part
+  carve_dense(cv, pl);
   return cv.off + 256;
 }
 
@@ -350,7 +440,7 @@ size_t viterbi_ws_bytes(const Plan& pl, int with_tb) {
 // Factorised Viterbi is used for algorithm 2, and for algorithm 0 on problems
 // of at least 2^28 cells (B*T*K*C^2) when the register-resident scan fits.
 bool viterbi_factorised(const Plan& pl, int algorithm) {
-  if (algorithm == TSM_VITERBI_EXACT || !pl.fast) return false;
+  if (algorithm == TSM_VITERBI_EXACT || !pl.fast || pl.dense) return false;
   if (algorithm == TSM_VITERBI_FACTORISED) return true;
   const double cells = (double)pl.B * pl.T * pl.K * (double)pl.C * pl.C;
   return cells >= (double)(1 << 28);
@@ -364,34 +454,37 @@ int tsm_version(void) { return 100; }
 
 const char* tsm_last_error(void) { return g_err.c_str(); }
 
-int tsm_plan_info(int64_t B, int64_t T, int64_t C, int64_t K, int has_ps, int has_pe, int64_t* out, int n) {
+int tsm_plan_info(int64_t B, int64_t T, int64_t C, int64_t K, int64_t trans_rows, int has_ps, int has_pe,
+                  int64_t* out, int n) {
   Plan p;
-  int rc = make_plan(B, T, C, K, has_ps, has_pe, &p);
+  int rc = make_plan(B, T, C, K, has_ps, has_pe, trans_rows, &p);
   if (rc) return rc;
   if (!out) return fail(TSM_ERR_INVALID, "out is NULL");
   const DeviceInfo di = device_info();
   const int64_t vals[] = {p.J, p.NT, p.RS, p.P, p.Lc, p.W, p.global_rings, (int64_t)p.scan_lds, p.NB, p.TB,
                           p.CB, p.NCB, p.JM, p.NTM, (int64_t)p.marg_lds, p.Kmax, di.n_cu, p.R, p.KP, p.RMAX,
-                          p.fast, p.FJ, p.FR, p.FNT, (int64_t)p.fast_lds, p.mfast, p.MR};
+                          p.fast, p.FJ, p.FR, p.FNT, (int64_t)p.fast_lds, p.mfast, p.MR,
+                          p.dense, p.DJ, p.DNT, p.dtrl, (int64_t)p.dense_lds, p.DG, p.DNTM, p.DNB, p.DTB,
+                          (int64_t)p.dmarg_lds};
   const int m = (int)(sizeof(vals) / sizeof(vals[0]));
   for (int i = 0; i < n && i < m; ++i) out[i] = vals[i];
   return TSM_OK;
 }
 
-int tsm_forward_workspace(int64_t B, int64_t T, int64_t C, int64_t K, int semiring, int has_ps, int has_pe,
-                          size_t* bytes) {
+int tsm_forward_workspace(int64_t B, int64_t T, int64_t C, int64_t K, int64_t trans_rows, int semiring, int has_ps,
+                          int has_pe, size_t* bytes) {
   if (!bytes) return fail(TSM_ERR_INVALID, "bytes is NULL");
   if (semiring != TSM_SEMIRING_LOG && semiring != TSM_SEMIRING_MAX) return fail(TSM_ERR_INVALID, "bad semiring %d", semiring);
   Plan p;
-  int rc = make_plan(B, T, C, K, has_ps, has_pe, &p);
+  int rc = make_plan(B, T, C, K, has_ps, has_pe, trans_rows, &p);
   if (rc) return rc;
   *bytes = forward_ws_bytes(p);
   return TSM_OK;
 }
 
 int tsm_forward(const float* cum, const float* tr, const float* db, const int64_t* len, const float* ps,
-                const float* pe, int64_t B, int64_t T, int64_t C, int64_t K, int semiring, float* partition,
-                double* log2_partition, float* alpha_hat, double* alpha_level, int32_t* recomputed,
+                const float* pe, int64_t B, int64_t T, int64_t C, int64_t K, int64_t trans_rows, int semiring,
+                float* partition, double* log2_partition, float* alpha_hat, double* alpha_level, int32_t* recomputed,
                 void* workspace, size_t ws_bytes, void* stream) {
   int rc = check_common(cum, tr, db, len, semiring);
   if (rc) return rc;
@@ -399,14 +492,21 @@ int tsm_forward(const float* cum, const float* tr, const float* db, const int64_
   if ((alpha_hat == nullptr) != (alpha_level == nullptr))
     return fail(TSM_ERR_INVALID, "alpha_hat and alpha_level must both be given or both be NULL");
   Plan pl;
-  rc = make_plan(B, T, C, K, ps != nullptr, pe != nullptr, &pl);
+  rc = make_plan(B, T, C, K, ps != nullptr, pe != nullptr, trans_rows, &pl);
   if (rc) return rc;
   const size_t need = forward_ws_bytes(pl);
   if (!workspace || ws_bytes < need)
     return fail(TSM_ERR_WORKSPACE, "forward workspace too small: %zu < %zu bytes", ws_bytes, need);
   Carver cv(workspace);
   ScanWs w = carve_scan(cv, pl);
+  const DenseTr dt = carve_dense(cv, pl);
   tsm::ScanParams p = scan_params(pl, w, cum, tr, db, len, ps, pe);
+  if (pl.dense) {
+    const int e = tsm::launch_dense_prep(pl, tr, dt.trf, dt.trb, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "tsm_forward (transition tables)");
+    p.trows = pl.trows;
+    p.trx = dt.trf;
+  }
   p.val = alpha_hat;
   p.lvl = alpha_level;
   if (log2_partition) p.z2 = log2_partition;
@@ -417,17 +517,19 @@ int tsm_forward(const float* cum, const float* tr, const float* db, const int64_
   return TSM_OK;
 }
 
-int tsm_backward_workspace(int64_t B, int64_t T, int64_t C, int64_t K, int has_ps, int has_pe, size_t* bytes) {
+int tsm_backward_workspace(int64_t B, int64_t T, int64_t C, int64_t K, int64_t trans_rows, int has_ps, int has_pe,
+                           size_t* bytes) {
   if (!bytes) return fail(TSM_ERR_INVALID, "bytes is NULL");
   Plan p;
-  int rc = make_plan(B, T, C, K, has_ps, has_pe, &p);
+  int rc = make_plan(B, T, C, K, has_ps, has_pe, trans_rows, &p);
   if (rc) return rc;
   *bytes = backward_ws_bytes(p);
   return TSM_OK;
 }
 
 int tsm_backward(const float* cum, const float* tr, const float* db, const int64_t* len, const float* ps,
-                 const float* pe, int64_t B, int64_t T, int64_t C, int64_t K, int semiring, const float* alpha_hat,
+                 const float* pe, int64_t B, int64_t T, int64_t C, int64_t K, int64_t trans_rows, int semiring,
+                 const float* alpha_hat,
                  const double* alpha_level, const double* log2_partition, const float* grad_output,
                  float* grad_cum, float* grad_tr, float* grad_db, float* grad_ps, float* grad_pe,
                  int32_t* recomputed, void* workspace, size_t ws_bytes, void* stream) {
@@ -438,7 +540,7 @@ int tsm_backward(const float* cum, const float* tr, const float* db, const int64
   if ((ps != nullptr) != (grad_ps != nullptr) || (pe != nullptr) != (grad_pe != nullptr))
     return fail(TSM_ERR_INVALID, "a projection gradient buffer is needed exactly when the projection is given");
   Plan pl;
-  rc = make_plan(B, T, C, K, ps != nullptr, pe != nullptr, &pl);
+  rc = make_plan(B, T, C, K, ps != nullptr, pe != nullptr, trans_rows, &pl);
   if (rc) return rc;
   const size_t need = backward_ws_bytes(pl);
   if (!workspace || ws_bytes < need)
@@ -451,11 +553,18 @@ int tsm_backward(const float* cum, const float* tr, const float* db, const int64
   ScanWs w = carve_scan(cv, pl);
   float* e_own = cv.take<float>(rows * pl.C);
   float* s_out = cv.take<float>(rows * pl.C);
-  float* halo = cv.take<float>((size_t)pl.B * pl.NB * pl.Kmax * pl.C);
-  double* db_part = cv.take<double>((size_t)pl.B * pl.NB * pl.Kmax * pl.C);
-  double* tr_part = cv.take<double>((size_t)pl.B * pl.NB * pl.C * pl.C);
+  float* halo = cv.take<float>((size_t)pl.B * marg_nb(pl) * pl.Kmax * pl.C);
+  double* db_part = cv.take<double>((size_t)pl.B * marg_nb(pl) * pl.Kmax * pl.C);
+  double* tr_part = cv.take<double>(tr_part_len(pl));
+  const DenseTr dt = carve_dense(cv, pl);
 
   tsm::ScanParams p = scan_params(pl, w, cum, tr, db, len, ps, pe);
+  if (pl.dense) {
+    const int e = tsm::launch_dense_prep(pl, tr, dt.trf, dt.trb, st);
+    if (e != hipSuccess) return hip_fail(e, "tsm_backward (transition tables)");
+    p.trows = pl.trows;
+    p.trx = dt.trb;
+  }
   p.val = bval;
   p.lvl = blvl;
   p.zout = nullptr;
@@ -477,8 +586,10 @@ int tsm_backward(const float* cum, const float* tr, const float* db, const int64
   q.Kmax = pl.Kmax;
   q.RS = pl.mfast ? pl.MRS : pl.RS;
   q.RL = pl.MRL;
-  q.NB = pl.NB;
-  q.TB = pl.TB;
+  q.NB = marg_nb(pl);
+  q.TB = marg_tb(pl);
+  q.trows = pl.trows;
+  q.trx = dt.trf;
   q.CB = pl.CB;
   q.NCB = pl.NCB;
   q.aval = alpha_hat;
@@ -501,8 +612,9 @@ int tsm_backward(const float* cum, const float* tr, const float* db, const int64
   f.C = pl.C;
   f.K = pl.K;
   f.Kmax = pl.Kmax;
-  f.NB = pl.NB;
-  f.TB = pl.TB;
+  f.NB = marg_nb(pl);
+  f.TB = marg_tb(pl);
+  f.trows = pl.trows;
   f.e_own = e_own;
   f.s_out = s_out;
   f.halo = halo;
@@ -519,18 +631,19 @@ int tsm_backward(const float* cum, const float* tr, const float* db, const int64
   return TSM_OK;
 }
 
-int tsm_viterbi_workspace(int64_t B, int64_t T, int64_t C, int64_t K, int with_tb, size_t* bytes) {
+int tsm_viterbi_workspace(int64_t B, int64_t T, int64_t C, int64_t K, int64_t trans_rows, int with_tb,
+                          size_t* bytes) {
   if (!bytes) return fail(TSM_ERR_INVALID, "bytes is NULL");
   Plan p;
-  int rc = make_plan(B, T, C, K, 0, 0, &p);
+  int rc = make_plan(B, T, C, K, 0, 0, trans_rows, &p);
   if (rc) return rc;
   *bytes = viterbi_ws_bytes(p, with_tb);
   return TSM_OK;
 }
 
 int tsm_viterbi(const float* cum, const float* tr, const float* db, const int64_t* len, const float* ps,
-                const float* pe, int64_t B, int64_t T, int64_t C, int64_t K, float* score, int with_tb,
-                int algorithm, int32_t* seg_count, int32_t* segments, void* workspace, size_t ws_bytes,
+                const float* pe, int64_t B, int64_t T, int64_t C, int64_t K, int64_t trans_rows, float* score,
+                int with_tb, int algorithm, int32_t* seg_count, int32_t* segments, void* workspace, size_t ws_bytes,
                 void* stream) {
   int rc = check_common(cum, tr, db, len, TSM_SEMIRING_MAX);
   if (rc) return rc;
@@ -540,8 +653,10 @@ int tsm_viterbi(const float* cum, const float* tr, const float* db, const int64_
     return fail(TSM_ERR_INVALID, "algorithm must be TSM_VITERBI_AUTO (0), _EXACT (1) or _FACTORISED (2), got %d",
                 algorithm);
   Plan pl;
-  rc = make_plan(B, T, C, K, ps != nullptr, pe != nullptr, &pl);
+  rc = make_plan(B, T, C, K, ps != nullptr, pe != nullptr, trans_rows, &pl);
   if (rc) return rc;
+  if (algorithm == TSM_VITERBI_FACTORISED && pl.dense)
+    return fail(TSM_ERR_UNSUPPORTED, "the factorised Viterbi needs static (C, C) transitions");
   if (algorithm == TSM_VITERBI_FACTORISED && !pl.fast)
     return fail(TSM_ERR_UNSUPPORTED, "the factorised Viterbi needs the register-resident scan (C <= 64, rings in LDS)");
   if (viterbi_factorised(pl, algorithm)) {
@@ -590,6 +705,7 @@ int tsm_viterbi(const float* cum, const float* tr, const float* db, const int64_
   v.K = pl.K;
   v.Kmax = pl.Kmax;
   v.RS = pl.RS;
+  v.trows = pl.trows;
   v.score = score;
   v.seg_count = seg_count;
   v.segs = segments;

@@ -25,7 +25,7 @@
 
 #include <float.h>
 
-#include "tsm_scan_common.hpp"
+#include "tsm_chunk_driver.hpp"
 
 namespace tsm {
 namespace fastscan {
@@ -56,6 +56,12 @@ __device__ __forceinline__ void ring_put(double* ring_c, int a, double x, int RS
 
 template <int J, int R, bool FWD, bool LOGSR>
 struct Chunk {
+  static constexpr bool kFwd = FWD;
+  static constexpr bool kLog = LOGSR;
+  static constexpr int kMaxThreads = R > 16 ? 512 : 1024;
+  __device__ static double* red(char* smem, const ScanParams& p) {
+    return reinterpret_cast<double*>(smem + fast_lds_layout(p.C, p.RL, p.RS).red);
+  }
   // ---------------------------------------------------------------------------
   // One chunk of one sequence.
   //   FWD: mode 0 exact from position 0; 1 speculative from t_lo - W; 2 exact
@@ -359,123 +365,16 @@ struct Chunk {
   }
 };
 
-// Parallel pass of one direction: one block per chunk, exact or speculative.
-template <int J, int R, bool FWD, bool LOGSR>
-__global__ void __launch_bounds__(R > 16 ? 512 : 1024) fast_scan_kernel(ScanParams p) {
-  extern __shared__ __align__(16) char smem[];
-  const int b = blockIdx.x / p.P, j = blockIdx.x % p.P;
-  const int len = seq_len(p, b);
-  const int item = b * p.P + j;
-  if (FWD ? (j > 0 && j * p.Lc >= len) : (j > bwd_last_chunk(p, len))) {
-    if (threadIdx.x == 0) p.status[item] = -1;  // empty chunk
-    return;
-  }
-  if (p.retry && retry_skip(p, item)) return;
-  const int mode = (FWD ? fwd_spec(p, j) : bwd_spec(p, j, len)) ? 1 : 0;
-  if (threadIdx.x == 0) p.status[item] = mode;
-  Chunk<J, R, FWD, LOGSR>::run(p, smem, b, j, mode, nullptr, nullptr);
-}
-
-// Sequential verification / repair of one direction: one block per sequence
-// walks its chunks, accepts a speculative chunk's frame offset when the
-// boundary spread is within tolerance, recomputes it exactly otherwise.
-template <int J, int R, bool FWD, bool LOGSR>
-__global__ void __launch_bounds__(R > 16 ? 512 : 1024) fast_fixup_kernel(ScanParams p) {
-  extern __shared__ __align__(16) char smem[];
-  const int b = blockIdx.x;
-  const int len = seq_len(p, b);
-  const FastLds L = fast_lds_layout(p.C, p.RL, p.RS);
-  double* red = reinterpret_cast<double*>(smem + L.red);
-  const int Kmax = p.Kmax, C = p.C;
-  double F = 0.0;
-  int n_re = 0;
-  bool prev_recomputed = false;
-  const int jl = bwd_last_chunk(p, len);
-  const int nch = len == 0 ? 1 : (len + p.Lc - 1) / p.Lc;
-  if (threadIdx.x == 0) p.offs[(size_t)b * p.P + (FWD ? 0 : jl)] = 0.0;
-  for (int j = FWD ? 1 : jl - 1; FWD ? j < nch : j >= 0; j += FWD ? 1 : -1) {
-    const int item = b * p.P + j;
-    if (p.status[item] != 1) {
-      F = 0.0;  // the chunk ran exactly from the sequence end
-      prev_recomputed = false;
-    } else {
-      const size_t e = FWD ? (size_t)(item - 1) : (size_t)(item + 1), sp = (size_t)item;
-      double dmax, dmin;
-      if (!prev_recomputed) {
-        // measured in parallel by verify_kernel against the neighbour's original end state
-        dmax = p.vstat[2 * sp];
-        dmin = p.vstat[2 * sp + 1];
-      } else {
-        // the neighbour was recomputed here: its end state changed, measure again
-        double hi, lo;
-        boundary_spread_part(p, e, sp, hi, lo);
-        block_minmax(hi, lo, red, dmax, dmin);
-      }
-      if (dmax - dmin <= (double)p.tol) {
-        F += 0.5 * (dmax + dmin);
-        prev_recomputed = false;
-      } else {
-        Chunk<J, R, FWD, LOGSR>::run(p, smem, b, j, 2, p.st_end + e * Kmax * C, p.lv_end + e * Kmax);
-        __syncthreads();
-        ++n_re;
-        prev_recomputed = true;
-        if (threadIdx.x == 0) p.status[item] = 2;
-      }
-    }
-    if (threadIdx.x == 0) p.offs[(size_t)item] = F;
-  }
-  __syncthreads();
-  if (FWD) {
-    finish_partition<LOGSR>(p, b, len, F, n_re);
-  } else if (threadIdx.x == 0 && p.recomputed != nullptr) {
-    p.recomputed[b] = n_re;
-  }
-}
-
-// Launch of one direction: parallel pass, verification, retry, sequential repair, level offsets.
-template <int J, int R, bool FWD, bool LOGSR>
-int launch_fast_dir(const Plan& pl, const ScanParams& p, hipStream_t st) {
-  const bool fwd = FWD;
-  auto k = fast_scan_kernel<J, R, FWD, LOGSR>;
-  auto kf = fast_fixup_kernel<J, R, FWD, LOGSR>;
-  const size_t lds = pl.fast_lds;
-  hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-  if (e != hipSuccess) return e;
-  e = hipFuncSetAttribute((const void*)kf, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-  if (e != hipSuccess) return e;
-  {
-    TimedLaunch tl(fwd ? kKScanFwd : kKScanBwd, st);
-    hipLaunchKernelGGL(k, dim3(pl.B * pl.P), dim3(pl.FNT), lds, st, p);
-  }
-  e = (hipError_t)launch_verify(pl, p, fwd, st);
-  if (e != hipSuccess) return e;
-  if (pl.P > 1) {
-    // failed speculative chunks again, in parallel, with a longer warm-up
-    {
-      TimedLaunch tl(kKRetry, st);
-      hipLaunchKernelGGL(k, dim3(pl.B * pl.P), dim3(pl.FNT), lds, st, retry_params(p));
-    }
-    e = (hipError_t)launch_verify(pl, p, fwd, st);
-    if (e != hipSuccess) return e;
-  }
-  {
-    TimedLaunch tl(fwd ? kKFwdFixup : kKBwdFixup, st);
-    hipLaunchKernelGGL(kf, dim3(pl.B), dim3(pl.FNT), lds, st, p);
-  }
-  e = (hipError_t)launch_apply_offsets(pl, p, fwd, st);
-  if (e != hipSuccess) return e;
-  return hipGetLastError();
-}
-
 template <int J, int R>
 int launch_fast_jr(const Plan& pl, const ScanParams& p, bool fwd, hipStream_t st) {
-  return fwd ? launch_fast_dir<J, R, true, true>(pl, p, st) : launch_fast_dir<J, R, false, true>(pl, p, st);
+  return fwd ? launch_chunk_dir<Chunk<J, R, true, true>>(pl, p, pl.fast_lds, pl.FNT, st)
+             : launch_chunk_dir<Chunk<J, R, false, true>>(pl, p, pl.fast_lds, pl.FNT, st);
 }
 
 // Max-semiring forward with backpointers (factorised Viterbi).
 template <int J, int R>
 int launch_fast_max_jr(const Plan& pl, const ScanParams& p, hipStream_t st) {
-  return launch_fast_dir<J, R, true, false>(pl, p, st);
+  return launch_chunk_dir<Chunk<J, R, true, false>>(pl, p, pl.fast_lds, pl.FNT, st);
 }
 
 }  // namespace fastscan

@@ -47,6 +47,11 @@ struct ScanParams {
   // duration k of a segment ending at t and the best source label c' of a
   // segment starting at t, packed (k << 16 | c'); null otherwise
   int32_t* bp;
+  // duration-dependent transitions (dense scans): number of transition
+  // matrices (0: one static matrix) and the log2-scaled table of the scan's
+  // direction, [k-1][out label][in label] for k = 1..Kmax
+  int trows;
+  const float* trx;
 };
 
 struct MargParams {
@@ -69,6 +74,9 @@ struct MargParams {
   float* halo;             // (B, NB, Kmax, C) end sums spilling into the next block
   double* db_part;         // (B, NB, Kmax, C)  duration-bias gradient partials
   double* tr_part;         // (B, NB, C, C)     transition gradient partials [c_src][c_dst]
+                           // (B, NB, Kmax, C, C) with duration-dependent transitions
+  int trows;               // number of transition matrices (0: one static matrix)
+  const float* trx;        // dense: log2-scaled transitions [k-1][c_dst][c_src]
 };
 
 struct FinalParams {
@@ -85,6 +93,7 @@ struct FinalParams {
   float* grad_pe;            // (B, T, C) or null
   float* grad_tr;            // (C, C)
   float* grad_db;            // (K, C)
+  int trows;                 // grad_tr is (trows, C, C) when > 0
 };
 
 struct ViterbiParams {
@@ -101,6 +110,7 @@ struct ViterbiParams {
   // backtrace output
   int32_t* seg_count;  // (B)
   int32_t* segs;       // (B, T, 4): start, end, label, prev label (reverse order)
+  int trows;           // transition is (trows, C, C), indexed by duration, when > 0
 };
 
 // launchers (return hipError_t as int)
@@ -133,6 +143,11 @@ int launch_margfast_j16_hi(const Plan& pl, const MargParams& q, hipStream_t s);
 int launch_marginals(const Plan& pl, const MargParams& q, hipStream_t s);
 int launch_finalize(const Plan& pl, const FinalParams& f, hipStream_t s);
 int launch_viterbi(const Plan& pl, const ViterbiParams& v, int with_traceback, hipStream_t s);
+// duration-dependent transitions: log2-scaled tables of both directions
+// (trf [k-1][c_dst][c_src], trb [k-1][c_src][c_dst]), dense scans and marginals
+int launch_dense_prep(const Plan& pl, const float* trans, float* trf, float* trb, hipStream_t s);
+int launch_dense_scan(const Plan& pl, const ScanParams& p, int semiring, bool forward, hipStream_t s);
+int launch_dense_marginals(const Plan& pl, const MargParams& q, hipStream_t s);
 int launch_checkpoints(const float* aval, const double* alvl, const int64_t* lengths, int B, int T,
                        int C, int K, int S, int n_ckpt, float* out, hipStream_t s);
 
@@ -151,6 +166,7 @@ enum KernelId : int {
   kKViterbi,
   kKBacktrace,
   kKRetry,
+  kKTransPrep,
   kNumKernels
 };
 

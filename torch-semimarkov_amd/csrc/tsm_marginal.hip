@@ -259,16 +259,23 @@ __global__ void finalize_rows_kernel(FinalParams f) {
 }
 
 // Shared gradients: sum over sequences (weighted by grad_output) and blocks, in fp64.
+// With duration-dependent transitions grad_tr is (trows, C, C): matrix k gets the
+// partials of duration k (1 <= k <= Kmax), the others are zero.
 __global__ void finalize_shared_kernel(FinalParams f) {
   const int C = f.C, K = f.K, Kmax = f.Kmax;
-  const int n_tr = C * C, n_db = K * C;
+  const int n_tr = (f.trows > 0 ? f.trows : 1) * C * C, n_db = K * C;
   const int idx = blockIdx.x * blockDim.x + threadIdx.x;
   if (idx < n_tr) {
+    const int k = idx / (C * C), e = idx % (C * C);
     double acc = 0.0;
-    for (int b = 0; b < f.B; ++b) {
-      double s = 0.0;
-      for (int i = 0; i < f.NB; ++i) s += f.tr_part[((size_t)b * f.NB + i) * C * C + idx];
-      acc += (double)f.grad_output[b] * s;
+    if (f.trows == 0 || (k >= 1 && k <= Kmax)) {
+      const size_t per = (size_t)(f.trows > 0 ? Kmax : 1) * C * C;
+      const size_t off = (f.trows > 0) ? (size_t)(k - 1) * C * C + e : (size_t)e;
+      for (int b = 0; b < f.B; ++b) {
+        double s = 0.0;
+        for (int i = 0; i < f.NB; ++i) s += f.tr_part[((size_t)b * f.NB + i) * per + off];
+        acc += (double)f.grad_output[b] * s;
+      }
     }
     f.grad_tr[idx] = (float)acc;
   } else if (idx < n_tr + n_db) {
@@ -329,6 +336,7 @@ int launch_marg_j(const Plan& pl, const MargParams& q, hipStream_t st) {
 }  // namespace
 
 int launch_marginals(const Plan& pl, const MargParams& q, hipStream_t s) {
+  if (pl.dense) return launch_dense_marginals(pl, q, s);
   if (pl.mfast) return launch_margfast_j16(pl, q, s);
   switch (pl.JM) {
     case 1: return launch_marg_j<1>(pl, q, s);
@@ -349,7 +357,7 @@ int launch_finalize(const Plan& pl, const FinalParams& f, hipStream_t s) {
     TimedLaunch tl(kKFinalizeRows, s);
     hipLaunchKernelGGL(finalize_rows_kernel, dim3(gx, pl.B), dim3(256), 0, s, f);
   }
-  const int n = pl.C * pl.C + pl.K * pl.C;
+  const int n = (f.trows > 0 ? f.trows : 1) * pl.C * pl.C + pl.K * pl.C;
   {
     TimedLaunch tl(kKFinalizeShared, s);
     hipLaunchKernelGGL(finalize_shared_kernel, dim3((n + 255) / 256), dim3(256), 0, s, f);

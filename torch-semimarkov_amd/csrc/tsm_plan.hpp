@@ -34,6 +34,14 @@ struct Plan {
   // durations per lane, one wavefront of 4 labels per workgroup, ring slots /
   // row length.  NB, TB, CB, NCB and marg_lds above then describe its blocking.
   int mfast, MR, MRS, MRL;
+  // duration-dependent (trows, C, C) transitions (trows > 0): dense scans with DJ
+  // lanes per label and DNT threads, DRS ring slots, dense_lds bytes, transition
+  // table in LDS when dtrl == 1; dense marginals with DG lanes per label group,
+  // DNTM threads, DNB blocks of DTB start positions, dmarg_lds bytes
+  int trows, dense, DJ, DNT, DRS, dtrl;
+  size_t dense_lds;
+  int DG, DNTM, DNB, DTB;
+  size_t dmarg_lds;
 };
 
 
@@ -60,6 +68,60 @@ __host__ __device__ inline MargFastLds margfast_lds_layout(int CB, int RL, int J
   L.alv = o; o = align16(o + 8 * (size_t)J);
   L.cmv = o; o = align16(o + 4 * (size_t)CB * J);
   L.psv = o; o = align16(o + 4 * (size_t)CB * J);
+  L.total = o;
+  return L;
+}
+
+// ---- dense scan LDS layout (duration-dependent transitions) ----------------
+// Rings are position-major: ring slot s (position pos, s = pos % RS) holds the
+// row of all C labels, so the source-label loop of one duration reads
+// consecutive words.
+struct DenseLds {
+  size_t ring;   // float[RS*CS]    normalised state rows (alpha-hat / beta-hat), CS = C|1
+  size_t crng;   // float[RS*CS]    cumulative scores of the ring positions
+  size_t prng;   // float[RS*CS]    projection of the ring positions (log2 units)
+  size_t lring;  // double[RS]      per-position levels
+  size_t dbt;    // float[(Kmax+1)*C] duration bias, log2 units, [k][c]
+  size_t wk;     // float[Kmax*CS]  backward: per-duration terms of the current step, [k-1][c]
+  size_t dlt;    // float[Kmax+1]   level difference per duration (-1e30 when invalid)
+  size_t wred;   // float[64]       per-wave maxima
+  size_t red;    // double[64]      block reductions (verification)
+  size_t trk;    // float[Kmax*C*CS] transitions, log2 units, rows [k-1][out] (only when in LDS)
+  size_t total;
+};
+
+__host__ __device__ inline DenseLds dense_lds_layout(int C, int Kmax, int RS, int trl) {
+  DenseLds L;
+  const size_t CS = (size_t)(C | 1);  // odd row stride (LDS banks)
+  size_t o = 0;
+  const size_t ring = sizeof(float) * (size_t)RS * CS;
+  L.ring = o; o = align16(o + ring);
+  L.crng = o; o = align16(o + ring);
+  L.prng = o; o = align16(o + ring);
+  L.lring = o; o = align16(o + sizeof(double) * RS);
+  L.dbt = o; o = align16(o + sizeof(float) * (size_t)(Kmax + 1) * C);
+  L.wk = o; o = align16(o + sizeof(float) * (size_t)Kmax * CS);
+  L.dlt = o; o = align16(o + sizeof(float) * (Kmax + 1));
+  L.wred = o; o = align16(o + sizeof(float) * 64);
+  L.red = o; o = align16(o + sizeof(double) * 64);
+  L.trk = o; o = align16(o + (trl ? sizeof(float) * (size_t)Kmax * C * CS : 0));
+  L.total = o;
+  return L;
+}
+
+// Dense marginal kernel: start sums of the block's TB positions and end sums of
+// the TB + Kmax rows its segments can end on.
+struct DenseMargLds {
+  size_t sacc;   // float[TB*C]
+  size_t eacc;   // float[(TB+Kmax)*C]
+  size_t total;
+};
+
+__host__ __device__ inline DenseMargLds dense_marg_lds_layout(int C, int Kmax, int TB) {
+  DenseMargLds L;
+  size_t o = 0;
+  L.sacc = o; o = align16(o + sizeof(float) * (size_t)TB * C);
+  L.eacc = o; o = align16(o + sizeof(float) * (size_t)(TB + Kmax) * C);
   L.total = o;
   return L;
 }

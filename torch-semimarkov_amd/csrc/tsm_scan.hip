@@ -754,6 +754,12 @@ int launch_fast(const Plan& pl, const ScanParams& p, bool fwd, hipStream_t st) {
 }
 
 int launch_any(const Plan& pl, const ScanParams& p, int semiring, bool fwd, hipStream_t st) {
+  if (pl.dense) {
+    // duration-dependent transitions: the dense scan with its own ring geometry
+    ScanParams q = p;
+    q.RS = pl.DRS;
+    return launch_dense_scan(pl, q, semiring, fwd, st);
+  }
   if (semiring == kLog && pl.fast) return launch_fast(pl, p, fwd, st);
   return semiring == kLog ? launch_sr<true>(pl, p, fwd, st) : launch_sr<false>(pl, p, fwd, st);
 }

@@ -68,9 +68,11 @@ __global__ void __launch_bounds__(512) viterbi_kernel(ViterbiParams v) {
     const int di = k < K - 1 ? k : K - 1;
     dbn[idx] = v.db[(size_t)di * C + cc];
   }
-  for (int idx = tid; idx < C * C; idx += NT) {
-    const int cd = idx / C, cs = idx % C;
-    trn[idx] = v.trans[(size_t)cs * C + cd];  // [c_dst][c_src]
+  if (v.trows == 0) {
+    for (int idx = tid; idx < C * C; idx += NT) {
+      const int cd = idx / C, cs = idx % C;
+      trn[idx] = v.trans[(size_t)cs * C + cd];  // [c_dst][c_src]
+    }
   }
   for (int cc = tid; cc < C; cc += NT) {
     araw[cc * RS] = 0.0f;  // alpha[0, :] = 0
@@ -100,7 +102,11 @@ __global__ void __launch_bounds__(512) viterbi_kernel(ViterbiParams v) {
       if (has_ps) e1 = e1 + pr[slot];
       if (has_pe) e1 = e1 + pe_t;
       float m = kMinusInf;
-      if constexpr (CMAX > 0) {
+      if (v.trows > 0) {
+        // duration-dependent transitions: transition[k][c_src][c], from global memory
+        const float* tk = v.trans + (size_t)k * C * C + c;
+        for (int i = 0; i < C; ++i) m = fmax2(m, araw[i * RS + slot] + (e1 + tk[(size_t)i * C]));
+      } else if constexpr (CMAX > 0) {
 #pragma unroll
         for (int i = 0; i < CMAX; ++i)
           if (i < C) m = fmax2(m, araw[i * RS + slot] + (e1 + tr_reg[i]));
@@ -115,16 +121,19 @@ __global__ void __launch_bounds__(512) viterbi_kernel(ViterbiParams v) {
     }
     ValIdx best = group_argmax_first<J>(ValIdx{bv, bk == 0 ? 0x7fffffff : bk});
     if (v.bp != nullptr) {
-      // first source label attaining the max at the winning duration
-      const int ks = best.i;
+      // first source label attaining the max at the winning duration (a duration
+      // in range even when no score was finite, e.g. NaN inputs: the index
+      // addresses the transition table)
+      const int ks = (best.i >= 1 && best.i <= kcap) ? best.i : 1;
       const int slot = wrap_slot(base - ks, RS);
       float e1 = (cur_cum - cr[slot]) + dr[ks];
       if (has_ps) e1 = e1 + pr[slot];
       if (has_pe) e1 = e1 + pe_t;
       float cv = kMinusInf;
       int ci = 0x7fffffff;
+      const float* tk = v.trans + (size_t)ks * C * C + c;
       for (int i = lj; i < C; i += J) {
-        const float x = araw[i * RS + slot] + (e1 + trn[c * C + i]);
+        const float x = araw[i * RS + slot] + (e1 + (v.trows > 0 ? tk[(size_t)i * C] : trn[c * C + i]));
         if (x > cv) {
           cv = x;
           ci = i;

@@ -26,6 +26,7 @@ PLAN_FIELDS = (
     "J", "NT", "RS", "P", "Lc", "W", "global_rings", "scan_lds", "NB", "TB",
     "CB", "NCB", "JM", "NTM", "marg_lds", "Kmax", "n_cu", "R", "KP", "RMAX",
     "fast", "FJ", "FR", "FNT", "fast_lds", "mfast", "MR",
+    "dense", "DJ", "DNT", "dtrl", "dense_lds", "DG", "DNTM", "DNB", "DTB", "dmarg_lds",
 )
 
 _p = ctypes.c_void_p
@@ -36,17 +37,17 @@ _sz = ctypes.c_size_t
 _SIGNATURES = {
     "tsm_version": ([], _i32),
     "tsm_last_error": ([], ctypes.c_char_p),
-    "tsm_plan_info": ([_i64, _i64, _i64, _i64, _i32, _i32, ctypes.POINTER(_i64), _i32], _i32),
-    "tsm_forward_workspace": ([_i64, _i64, _i64, _i64, _i32, _i32, _i32, ctypes.POINTER(_sz)], _i32),
+    "tsm_plan_info": ([_i64, _i64, _i64, _i64, _i64, _i32, _i32, ctypes.POINTER(_i64), _i32], _i32),
+    "tsm_forward_workspace": ([_i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32, ctypes.POINTER(_sz)], _i32),
     "tsm_forward": (
-        [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i32, _p, _p, _p, _p, _p, _p, _sz, _p], _i32),
-    "tsm_backward_workspace": ([_i64, _i64, _i64, _i64, _i32, _i32, ctypes.POINTER(_sz)], _i32),
+        [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _p, _p, _p, _p, _p, _p, _sz, _p], _i32),
+    "tsm_backward_workspace": ([_i64, _i64, _i64, _i64, _i64, _i32, _i32, ctypes.POINTER(_sz)], _i32),
     "tsm_backward": (
-        [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i32, _p, _p, _p, _p,
+        [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _p, _p, _p, _p,
          _p, _p, _p, _p, _p, _p, _p, _sz, _p], _i32),
-    "tsm_viterbi_workspace": ([_i64, _i64, _i64, _i64, _i32, ctypes.POINTER(_sz)], _i32),
+    "tsm_viterbi_workspace": ([_i64, _i64, _i64, _i64, _i64, _i32, ctypes.POINTER(_sz)], _i32),
     "tsm_viterbi": (
-        [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _i32, _i32, _p, _p, _p, _sz, _p], _i32),
+        [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _i32, _i32, _p, _p, _p, _sz, _p], _i32),
     "tsm_ring_checkpoints": ([_p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p], _i32),
     "tsm_timing_enable": ([_i32], _i32),
     "tsm_timing_read": ([ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i64), _i32], _i32),
@@ -88,9 +89,10 @@ def check(rc: int, what: str) -> None:
         raise _ERRORS.get(rc, RuntimeError)(f"{what}: {msg}")
 
 
-def plan_info(B, T, C, K, has_ps=False, has_pe=False) -> dict:
+def plan_info(B, T, C, K, has_ps=False, has_pe=False, trans_rows=0) -> dict:
     out = (_i64 * len(PLAN_FIELDS))()
-    check(lib().tsm_plan_info(B, T, C, K, int(has_ps), int(has_pe), out, len(PLAN_FIELDS)), "tsm_plan_info")
+    check(lib().tsm_plan_info(B, T, C, K, int(trans_rows), int(has_ps), int(has_pe), out, len(PLAN_FIELDS)),
+          "tsm_plan_info")
     return dict(zip(PLAN_FIELDS, [int(v) for v in out]))
 
 

@@ -17,7 +17,11 @@ Differences from the reference, all deliberate:
   reference's CPU backward computes them, ``pytorch_reference.py:458-467``).
 * Inputs are validated up front (shapes, devices, ``0 <= lengths <= T`` when
   ``lengths`` is on the host); the reference validates only the semiring.
-* Duration-dependent ``(K, C, C)`` transitions raise ``NotImplementedError``.
+* Duration-dependent ``(K, C, C)`` transitions (``transition[k]`` for a segment of
+  duration ``k``, ``pytorch_reference.py:104-109``) run dense HIP scans; they need
+  one matrix per duration ``1..max(K-1, 1)``, so ``K = 1`` needs two matrices
+  (the reference indexes ``transition[1]`` there too), and ``C <= 128``.  The
+  Viterbi of such a model always uses the exact kernel.
 """
 
 from __future__ import annotations
@@ -68,11 +72,14 @@ def prepare_inputs(cum_scores, transition, duration_bias, lengths, K, proj_start
     if K < 1:
         raise ValueError(f"K (max_duration) must be >= 1, got {K}")
     if transition.dim() == 3:
-        raise NotImplementedError(
-            "duration-dependent (K, C, C) transitions are not supported by the HIP backend yet"
-        )
-    if transition.shape != (C, C):
-        raise ValueError(f"transition must be ({C}, {C}), got {tuple(transition.shape)}")
+        kmax = max(K - 1, 1)
+        if transition.shape[1:] != (C, C) or transition.shape[0] < kmax + 1:
+            raise ValueError(
+                f"duration-dependent transition must be (>= {kmax + 1}, {C}, {C}) (one matrix per "
+                f"duration index up to {kmax}), got {tuple(transition.shape)}"
+            )
+    elif transition.shape != (C, C):
+        raise ValueError(f"transition must be ({C}, {C}) or (K, {C}, {C}), got {tuple(transition.shape)}")
     if duration_bias.dim() != 2 or duration_bias.shape[1] != C or duration_bias.shape[0] < 1:
         raise ValueError(f"duration_bias must be (K, {C}), got {tuple(duration_bias.shape)}")
     for name, t in (("transition", transition), ("duration_bias", duration_bias)):

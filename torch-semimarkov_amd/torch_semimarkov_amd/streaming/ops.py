@@ -34,6 +34,11 @@ def _size(query, *args) -> int:
     return int(out.value)
 
 
+def _trans_rows(transition: Tensor) -> int:
+    """0 for a static (C, C) transition, else the number of (C, C) matrices."""
+    return int(transition.shape[0]) if transition.dim() == 3 else 0
+
+
 # --------------------------------------------------------------------------- forward
 @torch.library.custom_op("tsm_amd::scan_forward", mutates_args=())
 def scan_forward(
@@ -54,12 +59,14 @@ def scan_forward(
     else:
         ah = torch.empty(0, device=dev, dtype=torch.float32)
         al = torch.empty(0, device=dev, dtype=torch.float64)
-    nbytes = _size(lib.tsm_forward_workspace, B, T, C, K, semiring, proj_start is not None, proj_end is not None)
+    tr_rows = _trans_rows(transition)
+    nbytes = _size(lib.tsm_forward_workspace, B, T, C, K, tr_rows, semiring, proj_start is not None,
+                   proj_end is not None)
     ws = _workspace(nbytes, dev)
     with torch.cuda.device(dev):
         rc = lib.tsm_forward(
             N.ptr(cum), N.ptr(transition), N.ptr(duration_bias), N.ptr(lengths),
-            N.ptr(proj_start), N.ptr(proj_end), B, T, C, K, semiring,
+            N.ptr(proj_start), N.ptr(proj_end), B, T, C, K, tr_rows, semiring,
             N.ptr(part), N.ptr(z2), N.ptr(ah) if store else None, N.ptr(al) if store else None,
             N.ptr(rec), N.ptr(ws), ws.numel(), _stream(dev),
         )
@@ -85,24 +92,25 @@ def scan_backward(
     proj_start: Optional[Tensor], proj_end: Optional[Tensor], alpha_hat: Tensor, alpha_level: Tensor,
     log2_partition: Tensor, grad_output: Tensor,
 ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
-    """grad_cum (B,T+1,C), grad_transition (C,C), grad_duration_bias (K,C), grad_proj_start,
-    grad_proj_end ((B,T,C) or empty), recomputed-chunk counts (B,)."""
+    """grad_cum (B,T+1,C), grad_transition (shaped like ``transition``), grad_duration_bias (K,C),
+    grad_proj_start, grad_proj_end ((B,T,C) or empty), recomputed-chunk counts (B,)."""
     lib = N.lib()
     B, Tp1, C = cum.shape
     T = Tp1 - 1
     dev = cum.device
     g_cum = torch.empty(B, Tp1, C, device=dev, dtype=torch.float32)
-    g_tr = torch.empty(C, C, device=dev, dtype=torch.float32)
+    g_tr = torch.empty(transition.shape, device=dev, dtype=torch.float32)
     g_db = torch.empty(K, C, device=dev, dtype=torch.float32)
     g_ps = torch.empty(B, T, C, device=dev, dtype=torch.float32) if proj_start is not None else None
     g_pe = torch.empty(B, T, C, device=dev, dtype=torch.float32) if proj_end is not None else None
     rec = torch.empty(B, device=dev, dtype=torch.int32)
-    nbytes = _size(lib.tsm_backward_workspace, B, T, C, K, proj_start is not None, proj_end is not None)
+    tr_rows = _trans_rows(transition)
+    nbytes = _size(lib.tsm_backward_workspace, B, T, C, K, tr_rows, proj_start is not None, proj_end is not None)
     ws = _workspace(nbytes, dev)
     with torch.cuda.device(dev):
         rc = lib.tsm_backward(
             N.ptr(cum), N.ptr(transition), N.ptr(duration_bias), N.ptr(lengths),
-            N.ptr(proj_start), N.ptr(proj_end), B, T, C, K, semiring,
+            N.ptr(proj_start), N.ptr(proj_end), B, T, C, K, tr_rows, semiring,
             N.ptr(alpha_hat), N.ptr(alpha_level), N.ptr(log2_partition), N.ptr(grad_output),
             N.ptr(g_cum), N.ptr(g_tr), N.ptr(g_db), N.ptr(g_ps), N.ptr(g_pe), N.ptr(rec),
             N.ptr(ws), ws.numel(), _stream(dev),
@@ -118,7 +126,7 @@ def _(cum, transition, duration_bias, lengths, K, semiring, proj_start, proj_end
     B, Tp1, C = cum.shape
     g_ps = cum.new_empty(B, Tp1 - 1, C) if proj_start is not None else cum.new_empty(0)
     g_pe = cum.new_empty(B, Tp1 - 1, C) if proj_end is not None else cum.new_empty(0)
-    return (cum.new_empty(B, Tp1, C), cum.new_empty(C, C), cum.new_empty(K, C), g_ps, g_pe,
+    return (cum.new_empty(B, Tp1, C), transition.new_empty(transition.shape), cum.new_empty(K, C), g_ps, g_pe,
             cum.new_empty(B, dtype=torch.int32))
 
 
@@ -142,12 +150,13 @@ def viterbi(
     else:
         cnt = torch.empty(0, device=dev, dtype=torch.int32)
         segs = torch.empty(0, device=dev, dtype=torch.int32)
-    nbytes = _size(lib.tsm_viterbi_workspace, B, T, C, K, int(traceback))
+    tr_rows = _trans_rows(transition)
+    nbytes = _size(lib.tsm_viterbi_workspace, B, T, C, K, tr_rows, int(traceback))
     ws = _workspace(nbytes, dev)
     with torch.cuda.device(dev):
         rc = lib.tsm_viterbi(
             N.ptr(cum), N.ptr(transition), N.ptr(duration_bias), N.ptr(lengths),
-            N.ptr(proj_start), N.ptr(proj_end), B, T, C, K, N.ptr(score), int(traceback), int(algorithm),
+            N.ptr(proj_start), N.ptr(proj_end), B, T, C, K, tr_rows, N.ptr(score), int(traceback), int(algorithm),
             N.ptr(cnt) if traceback else None, N.ptr(segs) if traceback else None,
             N.ptr(ws), ws.numel(), _stream(dev),
         )
