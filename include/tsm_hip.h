@@ -154,6 +154,35 @@ int tsm_viterbi(const float* cum_scores, const float* transition, const float* d
                 int32_t* segments, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Gold-path score: the score of the segmentation implied by per-position
+ * labels (the other half of the head's loss), and its gradients.
+ * Replaces:
+ *   helpers.py:365-544  score_gold_vectorized (a Python batch loop with .item()
+ *                       synchronisations, then gathers) and the autograd
+ *                       backward of its gathers
+ * Segments are the maximal runs of equal labels inside [0, len); a segment
+ * [s, e] with label c scores cum[e+1,c] - cum[s,c] + duration_bias[clamp(e-s+1,
+ * 1, K-1), c] + transition[c_prev, c] (no transition for the first segment;
+ * K = 1 uses row 0; T = 1 uses row 1 when db_rows > 1, as the reference).
+ *   labels          (B, T) int64, read inside [0, len) only
+ *   duration_bias   (db_rows, C), db_rows >= K
+ *   score           (B,) fp32, summed in fp64; NaN for a sequence holding a
+ *                   label outside [0, C)
+ *   grad_cum        (B, T+1, C) = grad_output[b] * (+1 at e+1 / -1 at s of each segment)
+ *   grad_transition (C, C), grad_duration_bias (db_rows, C): counts weighted
+ *                   by grad_output, summed over the batch
+ * One workspace size serves both calls.
+ * ------------------------------------------------------------------------- */
+int tsm_gold_score_workspace(int64_t B, int64_t T, int64_t C, int64_t K, int64_t db_rows, size_t* bytes);
+int tsm_gold_score(const float* cum_scores, const float* transition, const float* duration_bias,
+                   const int64_t* labels, const int64_t* lengths, int64_t B, int64_t T, int64_t C, int64_t K,
+                   int64_t db_rows, float* score, void* workspace, size_t workspace_bytes, void* stream);
+int tsm_gold_score_backward(const int64_t* labels, const int64_t* lengths, int64_t B, int64_t T, int64_t C,
+                            int64_t K, int64_t db_rows, const float* grad_output, float* grad_cum,
+                            float* grad_transition, float* grad_duration_bias, void* workspace,
+                            size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Ring checkpoints in the reference's layout (B, n_ckpt, K, C), raw alpha in
  * natural log units, rebuilt from tsm_forward's alpha_hat/alpha_level.
  * Replaces the ring_checkpoints output of

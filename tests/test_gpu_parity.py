@@ -461,6 +461,88 @@ def test_viterbi_auto_picks_factorised_for_large_problems():
     np.testing.assert_allclose(s_fact.cpu().numpy(), s_ex.cpu().numpy(), rtol=5e-5)
 
 
+# --------------------------------------------------------------------------- gold-path score
+GOLD_CASES = [(1, 3, 17, 4, 5), (2, 2, 9, 3, 1), (3, 4, 30, 5, 40), (4, 2, 1, 3, 4), (5, 3, 5000, 7, 300),
+              (6, 2, 2100, 4, 3), (7, 3, 64, 130, 9)]
+
+
+@pytest.mark.parametrize("seed,B,T,C,K", GOLD_CASES)
+def test_score_gold_and_grads_vs_oracle(seed, B, T, C, K):
+    """tsm_gold_score against the oracle's restatement of score_gold_vectorized
+    (fp64), and its gradients against autograd through the oracle.  Long runs,
+    runs longer than K-1, several position blocks (T = 5000) and K = 1 / T = 1."""
+    g = torch.Generator().manual_seed(seed)
+    cum = torch.zeros(B, T + 1, C)
+    cum[:, 1:] = torch.randn(B, T, C, generator=g).cumsum(1)
+    tr = torch.randn(C, C, generator=g)
+    db = torch.randn(max(K, 2), C, generator=g)[:K] if K > 1 else torch.randn(2, C, generator=g)
+    labels = torch.randint(0, C, (B, T), generator=g)
+    labels[:, T // 3: T // 2] = 1  # long runs
+    if T > 1000:
+        labels[:, 1000:1700] = torch.randint(0, 2, (1,), generator=g).item()
+    lengths = torch.randint(1, T + 1, (B,), generator=g)
+    lengths[0] = T
+    d = lambda x: x.double().requires_grad_(True)
+    c64, t64, d64 = d(cum), d(tr), d(db)
+    want = R.score_gold(c64, labels, lengths, t64, d64, K)
+    gw = torch.linspace(0.5, 1.5, B, dtype=torch.float64)
+    want_g = torch.autograd.grad((want * gw).sum(), (c64, t64, d64), allow_unused=True)
+    want_g = [torch.zeros_like(x) if w is None else w for w, x in zip(want_g, (c64, t64, d64))]  # T == 1: no transition
+    ins = [x.to(DEV).requires_grad_(True) for x in (cum, tr, db)]
+    got = tsa.score_gold_vectorized(ins[0], labels.to(DEV), lengths.to(DEV), ins[1], ins[2], K)
+    np.testing.assert_allclose(got.detach().cpu().double().numpy(), want.detach().numpy(), rtol=1e-6, atol=1e-4)
+    got_g = torch.autograd.grad((got * gw.float().to(DEV)).sum(), ins)
+    for a, w in zip(got_g, want_g):
+        np.testing.assert_allclose(a.cpu().double().numpy(), w.numpy(), rtol=1e-6, atol=1e-6)
+
+
+def test_score_gold_matches_reference_loss_fixture():
+    z = load_golden("head_small")
+    C, K = int(z["C"]), int(z["K"])
+    hidden = torch.from_numpy(z["hidden"])
+    cum = torch.zeros(hidden.shape[0], hidden.shape[1] + 1, C)
+    cum[:, 1:] = torch.cumsum(hidden, 1)
+    L = torch.from_numpy(z["lengths"])
+    tr = torch.from_numpy(z["transition"])
+    db = torch.from_numpy(z["duration_bias"])
+    part, _, _ = R.forward(cum, tr, db, L, K)
+    gold = tsa.score_gold_vectorized(cum.to(DEV), torch.from_numpy(z["labels"]).to(DEV), L.to(DEV), tr.to(DEV),
+                                     db.to(DEV), K)
+    np.testing.assert_allclose((part - gold.cpu()).numpy(), z["loss"], rtol=1e-5, atol=1e-4)
+
+
+def test_score_gold_of_viterbi_path_is_viterbi_score():
+    """Independent of the oracle: labelling the Viterbi segmentation (no two
+    neighbouring segments share a label) and scoring it gives the Viterbi score
+    minus the transition into the first segment (which the gold score omits)."""
+    B, T, K, C = 3, 400, 12, 6
+    cum, tr, db, L, _, _ = rand_problem(B, T, K, C, 6060, [400, 257, 3], tscale=0.5, dscale=0.5)
+    tr = tr - 30.0 * torch.eye(C)
+    score, cnt, segs = ops.viterbi(*to_dev(cum, tr, db, L), K, None, None, True, N.TSM_VITERBI_EXACT)
+    labels = torch.zeros(B, T, dtype=torch.long)
+    first_tr = torch.zeros(B)
+    segs = segs.cpu()
+    for b in range(B):
+        for i in range(int(cnt[b])):
+            s, e, c, cp = (int(v) for v in segs[b, i])
+            labels[b, s:e + 1] = c
+            if s == 0:
+                first_tr[b] = tr[cp, c]
+    gold = tsa.score_gold_vectorized(*to_dev(cum, labels, L, tr, db), K).cpu()
+    np.testing.assert_allclose(gold.double().numpy(), (score.cpu() - first_tr).double().numpy(), rtol=2e-6)
+
+
+def test_score_gold_flags_out_of_range_labels():
+    cum = torch.randn(2, 11, 3).cumsum(1).to(DEV)
+    labels = torch.zeros(2, 10, dtype=torch.long)
+    labels[1, 4] = 7  # outside [0, C) inside the sequence
+    labels[0, 9] = 9  # outside the sequence (length 8): ignored
+    L = torch.tensor([8, 10])
+    got = tsa.score_gold_vectorized(cum, labels.to(DEV), L.to(DEV), torch.zeros(3, 3, device=DEV),
+                                    torch.zeros(4, 3, device=DEV), 4).cpu()
+    assert torch.isfinite(got[0]) and torch.isnan(got[1])
+
+
 # --------------------------------------------------------------------------- head
 @pytest.mark.parametrize("name", ["head_small", "head_proj"])
 def test_head_matches_reference_golden(name):

@@ -446,6 +446,60 @@ bool viterbi_factorised(const Plan& pl, int algorithm) {
   return cells >= (double)(1 << 28);
 }
 
+// Gold-path scoring: sizes, LDS of the label window, workspace.
+int check_gold(int64_t B, int64_t T, int64_t C, int64_t K, int64_t Kdb) {
+  if (B < 1 || T < 1 || C < 1 || K < 1)
+    return fail(TSM_ERR_INVALID, "need B, T, C, K >= 1 (got %lld, %lld, %lld, %lld)", (long long)B, (long long)T,
+                (long long)C, (long long)K);
+  if (Kdb < K || Kdb < 1)
+    return fail(TSM_ERR_INVALID, "duration_bias has %lld rows; durations up to K-1 = %lld need >= %lld",
+                (long long)Kdb, (long long)(K - 1), (long long)K);
+  if (T > (int64_t)1 << 30 || C > 4096 || Kdb * C + C * C > (int64_t)1 << 30)
+    return fail(TSM_ERR_UNSUPPORTED, "gold score: sizes too large (T=%lld, C=%lld, K=%lld)", (long long)T,
+                (long long)C, (long long)Kdb);
+  const DeviceInfo di = device_info();
+  if (tsm::gold_lds_bytes((int)K) > (size_t)di.max_lds)
+    return fail(TSM_ERR_UNSUPPORTED, "gold score: K=%lld needs a label window larger than LDS", (long long)K);
+  return TSM_OK;
+}
+
+struct GoldWs {
+  double* part;
+  int* bad;
+  int* cnt;
+};
+
+GoldWs carve_gold(Carver& cv, int64_t B, int64_t T, int64_t C, int64_t Kdb) {
+  const size_t nch = (size_t)tsm::gold_chunks((int)T);
+  GoldWs w;
+  w.part = cv.take<double>((size_t)B * nch);
+  w.bad = cv.take<int>((size_t)B * nch);
+  w.cnt = cv.take<int>((size_t)B * (size_t)(Kdb * C + C * C));
+  return w;
+}
+
+tsm::GoldParams gold_params(const GoldWs& w, const float* cum, const float* tr, const float* db,
+                            const int64_t* labels, const int64_t* len, int64_t B, int64_t T, int64_t C, int64_t K,
+                            int64_t Kdb) {
+  tsm::GoldParams g{};
+  g.cum = cum;
+  g.tr = tr;
+  g.db = db;
+  g.labels = labels;
+  g.lengths = len;
+  g.B = (int)B;
+  g.T = (int)T;
+  g.C = (int)C;
+  g.K = (int)K;
+  g.Kdb = (int)Kdb;
+  g.NCH = tsm::gold_chunks((int)T);
+  g.part = w.part;
+  g.bad = w.bad;
+  g.cnt = w.cnt;
+  g.NHIST = (int)(Kdb * C + C * C);
+  return g;
+}
+
 }  // namespace
 
 extern "C" {
@@ -711,6 +765,59 @@ int tsm_viterbi(const float* cum, const float* tr, const float* db, const int64_
   v.segs = segments;
   const int e = tsm::launch_viterbi(pl, v, with_tb, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "tsm_viterbi");
+  return TSM_OK;
+}
+
+int tsm_gold_score_workspace(int64_t B, int64_t T, int64_t C, int64_t K, int64_t db_rows, size_t* bytes) {
+  if (!bytes) return fail(TSM_ERR_INVALID, "bytes is NULL");
+  int rc = check_gold(B, T, C, K, db_rows);
+  if (rc) return rc;
+  Carver cv(nullptr);
+  carve_gold(cv, B, T, C, db_rows);
+  *bytes = cv.off + 256;
+  return TSM_OK;
+}
+
+int tsm_gold_score(const float* cum, const float* tr, const float* db, const int64_t* labels, const int64_t* len,
+                   int64_t B, int64_t T, int64_t C, int64_t K, int64_t db_rows, float* score, void* workspace,
+                   size_t ws_bytes, void* stream) {
+  if (!cum || !tr || !db || !labels || !len || !score)
+    return fail(TSM_ERR_INVALID, "cum_scores, transition, duration_bias, labels, lengths and score are required");
+  int rc = check_gold(B, T, C, K, db_rows);
+  if (rc) return rc;
+  size_t need = 0;
+  tsm_gold_score_workspace(B, T, C, K, db_rows, &need);
+  if (!workspace || ws_bytes < need)
+    return fail(TSM_ERR_WORKSPACE, "gold score workspace too small: %zu < %zu bytes", ws_bytes, need);
+  Carver cv(workspace);
+  const GoldWs w = carve_gold(cv, B, T, C, db_rows);
+  tsm::GoldParams g = gold_params(w, cum, tr, db, labels, len, B, T, C, K, db_rows);
+  g.score = score;
+  const int e = tsm::launch_gold_score(g, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "tsm_gold_score");
+  return TSM_OK;
+}
+
+int tsm_gold_score_backward(const int64_t* labels, const int64_t* len, int64_t B, int64_t T, int64_t C, int64_t K,
+                            int64_t db_rows, const float* grad_output, float* grad_cum, float* grad_tr,
+                            float* grad_db, void* workspace, size_t ws_bytes, void* stream) {
+  if (!labels || !len || !grad_output || !grad_cum || !grad_tr || !grad_db)
+    return fail(TSM_ERR_INVALID, "labels, lengths, grad_output and the gradient outputs are required");
+  int rc = check_gold(B, T, C, K, db_rows);
+  if (rc) return rc;
+  size_t need = 0;
+  tsm_gold_score_workspace(B, T, C, K, db_rows, &need);
+  if (!workspace || ws_bytes < need)
+    return fail(TSM_ERR_WORKSPACE, "gold score workspace too small: %zu < %zu bytes", ws_bytes, need);
+  Carver cv(workspace);
+  const GoldWs w = carve_gold(cv, B, T, C, db_rows);
+  tsm::GoldParams g = gold_params(w, nullptr, nullptr, nullptr, labels, len, B, T, C, K, db_rows);
+  g.gout = grad_output;
+  g.gcum = grad_cum;
+  g.gtr = grad_tr;
+  g.gdb = grad_db;
+  const int e = tsm::launch_gold_backward(g, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "tsm_gold_score_backward");
   return TSM_OK;
 }
 

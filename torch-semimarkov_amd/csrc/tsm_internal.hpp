@@ -113,6 +113,28 @@ struct ViterbiParams {
   int trows;           // transition is (trows, C, C), indexed by duration, when > 0
 };
 
+// Gold-path score (segmentation implied by per-position labels) and its gradients.
+struct GoldParams {
+  const float* cum;        // (B, T+1, C)
+  const float* tr;         // (C, C)
+  const float* db;         // (Kdb, C)
+  const int64_t* labels;   // (B, T)
+  const int64_t* lengths;  // (B,)
+  int B, T, C, K, Kdb;
+  int NCH;                 // position blocks per sequence
+  int H;                   // label lookback staged per block (set by the launcher)
+  double* part;            // (B, NCH) block partial scores
+  int* bad;                // (B, NCH) out-of-range label flags
+  float* score;            // (B)
+  // backward
+  const float* gout;       // (B)
+  float* gcum;             // (B, T+1, C)
+  int* cnt;                // (B, NHIST) segment / transition counts
+  int NHIST;               // Kdb*C + C*C
+  float* gtr;              // (C, C)
+  float* gdb;              // (Kdb, C)
+};
+
 // launchers (return hipError_t as int)
 int launch_scan_forward(const Plan& pl, const ScanParams& p, int semiring, hipStream_t s);
 int launch_scan_backward(const Plan& pl, const ScanParams& p, int semiring, hipStream_t s);
@@ -148,6 +170,10 @@ int launch_viterbi(const Plan& pl, const ViterbiParams& v, int with_traceback, h
 int launch_dense_prep(const Plan& pl, const float* trans, float* trf, float* trb, hipStream_t s);
 int launch_dense_scan(const Plan& pl, const ScanParams& p, int semiring, bool forward, hipStream_t s);
 int launch_dense_marginals(const Plan& pl, const MargParams& q, hipStream_t s);
+int gold_chunks(int T);
+size_t gold_lds_bytes(int K);
+int launch_gold_score(const GoldParams& g, hipStream_t s);
+int launch_gold_backward(const GoldParams& g, hipStream_t s);
 int launch_checkpoints(const float* aval, const double* alvl, const int64_t* lengths, int B, int T,
                        int C, int K, int S, int n_ckpt, float* out, hipStream_t s);
 
@@ -167,6 +193,7 @@ enum KernelId : int {
   kKBacktrace,
   kKRetry,
   kKTransPrep,
+  kKGold,
   kNumKernels
 };
 

@@ -21,7 +21,7 @@ const char* const kNames[kNumKernels] = {
     "scan_fwd_kernel",   "scan_bwd_kernel",      "verify_kernel",           "fwd_fixup_kernel",
     "bwd_fixup_kernel",  "apply_offsets_kernel", "marginal_kernel",         "finalize_rows_kernel",
     "finalize_shared_kernel", "checkpoints_kernel", "viterbi_kernel",       "backtrace_kernel",
-    "retry_kernel",      "dense_prep_kernel",
+    "retry_kernel",      "dense_prep_kernel",    "gold_kernels",
 };
 
 struct Pending {

@@ -48,6 +48,10 @@ _SIGNATURES = {
     "tsm_viterbi_workspace": ([_i64, _i64, _i64, _i64, _i64, _i32, ctypes.POINTER(_sz)], _i32),
     "tsm_viterbi": (
         [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _i32, _i32, _p, _p, _p, _sz, _p], _i32),
+    "tsm_gold_score_workspace": ([_i64, _i64, _i64, _i64, _i64, ctypes.POINTER(_sz)], _i32),
+    "tsm_gold_score": ([_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _p, _sz, _p], _i32),
+    "tsm_gold_score_backward": (
+        [_p, _p, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _sz, _p], _i32),
     "tsm_ring_checkpoints": ([_p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p], _i32),
     "tsm_timing_enable": ([_i32], _i32),
     "tsm_timing_read": ([ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i64), _i32], _i32),

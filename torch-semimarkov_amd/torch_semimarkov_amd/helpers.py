@@ -1,7 +1,8 @@
 """Output types of the Viterbi traceback and gold-segmentation scoring.
 
 ``Segment`` / ``ViterbiResult`` mirror ``helpers.py:10-78`` of the reference;
-``score_gold_vectorized`` has the signature and semantics of ``helpers.py:365-544``.
+``score_gold_vectorized`` has the signature and semantics of ``helpers.py:365-544``
+and runs on the GPU (``tsm_gold_score`` of ``libtsm_hip.so``).
 """
 
 from __future__ import annotations
@@ -35,6 +36,29 @@ class ViterbiResult:
     segments: list[list[Segment]]
 
 
+class GoldScoreHIP(torch.autograd.Function):
+    """Gold-path score on the GPU (``tsm_gold_score``) with its gradients
+    (``tsm_gold_score_backward``) for ``cum_scores``, ``transition`` and ``duration_bias``."""
+
+    @staticmethod
+    def forward(ctx, cum, transition, duration_bias, labels, lengths, K):
+        from .streaming import ops
+
+        ctx.shape = (cum.shape[1] - 1, cum.shape[2], int(K), duration_bias.shape[0])
+        ctx.save_for_backward(labels, lengths)
+        return ops.gold_score(cum.detach(), transition.detach(), duration_bias.detach(), labels, lengths, int(K))
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        from .streaming import ops
+
+        labels, lengths = ctx.saved_tensors
+        T, C, K, Kdb = ctx.shape
+        g = grad_output.detach().to(torch.float32).contiguous()
+        g_cum, g_tr, g_db = ops.gold_score_backward(labels, lengths, g, T, C, K, Kdb)
+        return g_cum, g_tr, g_db, None, None, None
+
+
 def score_gold_vectorized(
     cum_scores: Tensor,
     labels: Tensor,
@@ -43,54 +67,47 @@ def score_gold_vectorized(
     duration_bias: Tensor,
     max_duration: int,
 ) -> Tensor:
-    r"""Score of the segmentation implied by per-position ``labels``.
+    r"""Score of the segmentation implied by per-position ``labels`` ``(B, T)``.
 
-    Segments are maximal runs of equal labels inside ``[0, len)``.  A segment
-    ``[s, e]`` with label ``c`` contributes ``cum[e+1, c] - cum[s, c]`` +
-    ``duration_bias[clamp(e-s+1, 1, K-1), c]`` + ``transition[c_prev, c]`` (no
-    transition for the first segment), as in ``helpers.py:365-544``.  For
-    ``T == 1`` the duration row is 1 (``helpers.py:410-419``), clamped to the
-    table for ``K == 1``.
+    Signature and semantics of the reference's ``score_gold_vectorized``
+    (``helpers.py:365-544``): segments are maximal runs of equal labels inside
+    ``[0, len)``; a segment ``[s, e]`` with label ``c`` contributes
+    ``cum[e+1, c] - cum[s, c]`` + ``duration_bias[clamp(e-s+1, 1, K-1), c]`` +
+    ``transition[c_prev, c]`` (no transition for the first segment).  ``T == 1``
+    uses duration row 1 (``helpers.py:410-419``).  A ``(K, C, C)`` transition is
+    indexed as the reference's flat ``transition.view(-1)[c_prev * C + c]``, i.e.
+    its first matrix.
 
-    Computed with position masks instead of the reference's per-sequence Python
-    loop: no host synchronisation, one pass of gathers on the input's device.
+    Runs the HIP kernels of ``libtsm_hip.so`` (one pass over the labels, no host
+    synchronisation, fp64 sums); differentiable in ``cum_scores``,
+    ``transition`` and ``duration_bias``.  A sequence holding a label outside
+    ``[0, C)`` scores NaN.
     """
     B, Tp1, C = cum_scores.shape
     T = Tp1 - 1
     dev = cum_scores.device
-    dtype = cum_scores.dtype
+    out_dtype = cum_scores.dtype if cum_scores.is_floating_point() else torch.float32
     if T == 0:
-        return torch.zeros(B, device=dev, dtype=dtype)
-    lengths = lengths.to(device=dev, dtype=torch.long)
-    labels = labels.to(device=dev, dtype=torch.long)
-    if T == 1:
-        l0 = labels[:, 0]
-        content = cum_scores[:, 1, :].gather(1, l0.unsqueeze(1)).squeeze(1)
-        content = content - cum_scores[:, 0, :].gather(1, l0.unsqueeze(1)).squeeze(1)
-        row = min(1, duration_bias.shape[0] - 1)
-        return (content + duration_bias[row, l0]) * (lengths > 0).to(dtype)
-
-    pos = torch.arange(T, device=dev)
-    valid = pos.unsqueeze(0) < lengths.unsqueeze(1)  # (B, T)
-    prev_lab = torch.cat([labels[:, :1], labels[:, :-1]], dim=1)
-    next_lab = torch.cat([labels[:, 1:], labels[:, -1:]], dim=1)
-    is_start = valid & ((pos == 0).unsqueeze(0) | (labels != prev_lab))
-    is_end = valid & ((pos.unsqueeze(0) == lengths.unsqueeze(1) - 1) | (labels != next_lab))
-
-    # content: sum over segment ends of cum[e+1, l] minus sum over starts of cum[s, l]
-    lab3 = labels.unsqueeze(-1)
-    cum_end = cum_scores[:, 1:, :].gather(2, lab3).squeeze(-1)  # cum[p+1, label[p]]
-    cum_beg = cum_scores[:, :-1, :].gather(2, lab3).squeeze(-1)  # cum[p, label[p]]
-    content = (cum_end * is_end.to(dtype)).sum(1) - (cum_beg * is_start.to(dtype)).sum(1)
-
-    # duration of the segment ending at p: p - (index of the latest start <= p) + 1
-    start_idx = torch.where(is_start, pos.unsqueeze(0).expand(B, T), torch.zeros_like(labels))
-    last_start = torch.cummax(start_idx, dim=1).values
-    dur = torch.clamp(pos.unsqueeze(0) - last_start + 1, 1, max_duration - 1)
-    dsc = duration_bias[dur, labels]  # (B, T)
-    dur_term = (dsc * is_end.to(dtype)).sum(1)
-
-    # transitions into every segment start except the first
-    tsc = transition[prev_lab, labels]
-    trans_term = (tsc * (is_start & (pos > 0).unsqueeze(0)).to(dtype)).sum(1)
-    return content + dur_term + trans_term
+        return torch.zeros(B, device=dev, dtype=out_dtype)
+    if not cum_scores.is_cuda:
+        raise RuntimeError(
+            "torch_semimarkov_amd runs on AMD GPUs only: cum_scores is on "
+            f"{cum_scores.device}; move the inputs to a ROCm device (e.g. .to('cuda'))"
+        )
+    if labels.shape != (B, T):
+        raise ValueError(f"labels must be ({B}, {T}), got {tuple(labels.shape)}")
+    if lengths.shape != (B,):
+        raise ValueError(f"lengths must be ({B},), got {tuple(lengths.shape)}")
+    tr = transition[0] if transition.dim() == 3 else transition
+    if tr.shape != (C, C):
+        raise ValueError(f"transition must be ({C}, {C}) or (K, {C}, {C}), got {tuple(transition.shape)}")
+    if duration_bias.dim() != 2 or duration_bias.shape[1] != C:
+        raise ValueError(f"duration_bias must be (K, {C}), got {tuple(duration_bias.shape)}")
+    f32 = lambda x: (x if x.dtype == torch.float32 else x.float()).contiguous()
+    score = GoldScoreHIP.apply(
+        f32(cum_scores), f32(tr), f32(duration_bias),
+        labels.to(device=dev, dtype=torch.int64).contiguous(),
+        lengths.to(device=dev, dtype=torch.int64).contiguous(),
+        int(max_duration),
+    )
+    return score if score.dtype == out_dtype else score.to(out_dtype)

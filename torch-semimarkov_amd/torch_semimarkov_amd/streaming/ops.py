@@ -173,6 +173,56 @@ def _(cum, transition, duration_bias, lengths, K, proj_start, proj_end, tracebac
     return cum.new_empty(B), cum.new_empty(0, dtype=torch.int32), cum.new_empty(0, dtype=torch.int32)
 
 
+# --------------------------------------------------------------------------- gold-path score
+@torch.library.custom_op("tsm_amd::gold_score", mutates_args=())
+def gold_score(cum: Tensor, transition: Tensor, duration_bias: Tensor, labels: Tensor, lengths: Tensor,
+               K: int) -> Tensor:
+    """Score (B,) fp32 of the segmentation implied by ``labels`` (B,T) int64; ``transition`` (C,C)."""
+    lib = N.lib()
+    B, Tp1, C = cum.shape
+    T = Tp1 - 1
+    dev = cum.device
+    Kdb = duration_bias.shape[0]
+    score = torch.empty(B, device=dev, dtype=torch.float32)
+    ws = _workspace(_size(lib.tsm_gold_score_workspace, B, T, C, K, Kdb), dev)
+    with torch.cuda.device(dev):
+        rc = lib.tsm_gold_score(N.ptr(cum), N.ptr(transition), N.ptr(duration_bias), N.ptr(labels), N.ptr(lengths),
+                                B, T, C, K, Kdb, N.ptr(score), N.ptr(ws), ws.numel(), _stream(dev))
+    N.check(rc, "tsm_gold_score")
+    return score
+
+
+@gold_score.register_fake
+def _(cum, transition, duration_bias, labels, lengths, K):
+    return cum.new_empty(cum.shape[0])
+
+
+@torch.library.custom_op("tsm_amd::gold_score_backward", mutates_args=())
+def gold_score_backward(labels: Tensor, lengths: Tensor, grad_output: Tensor, T: int, C: int, K: int,
+                        Kdb: int) -> tuple[Tensor, Tensor, Tensor]:
+    """grad_cum (B,T+1,C) (scaled by grad_output), grad_transition (C,C), grad_duration_bias (Kdb,C)."""
+    lib = N.lib()
+    B = labels.shape[0]
+    dev = labels.device
+    g_cum = torch.empty(B, T + 1, C, device=dev, dtype=torch.float32)
+    g_tr = torch.empty(C, C, device=dev, dtype=torch.float32)
+    g_db = torch.empty(Kdb, C, device=dev, dtype=torch.float32)
+    ws = _workspace(_size(lib.tsm_gold_score_workspace, B, T, C, K, Kdb), dev)
+    with torch.cuda.device(dev):
+        rc = lib.tsm_gold_score_backward(N.ptr(labels), N.ptr(lengths), B, T, C, K, Kdb, N.ptr(grad_output),
+                                         N.ptr(g_cum), N.ptr(g_tr), N.ptr(g_db), N.ptr(ws), ws.numel(),
+                                         _stream(dev))
+    N.check(rc, "tsm_gold_score_backward")
+    return g_cum, g_tr, g_db
+
+
+@gold_score_backward.register_fake
+def _(labels, lengths, grad_output, T, C, K, Kdb):
+    B = labels.shape[0]
+    f = grad_output.new_empty
+    return f(B, T + 1, C), f(C, C), f(Kdb, C)
+
+
 # --------------------------------------------------------------------------- checkpoints
 @torch.library.custom_op("tsm_amd::ring_checkpoints", mutates_args=())
 def ring_checkpoints(alpha_hat: Tensor, alpha_level: Tensor, lengths: Tensor, K: int, interval: int,
