@@ -44,6 +44,10 @@ extern "C" {
 #define TSM_SEMIRING_LOG 0
 #define TSM_SEMIRING_MAX 1
 
+#define TSM_DTYPE_F32 0
+#define TSM_DTYPE_BF16 1
+#define TSM_DTYPE_F16 2
+
 #define TSM_VITERBI_AUTO 0       /* factorised for large problems when it fits, else exact */
 #define TSM_VITERBI_EXACT 1      /* the reference's fp32 operation order, bit-identical scores */
 #define TSM_VITERBI_FACTORISED 2 /* K*C + C^2 terms per step, chunked over all CUs */
@@ -152,6 +156,26 @@ int tsm_viterbi(const float* cum_scores, const float* transition, const float* d
                 int64_t C, int64_t K, int64_t trans_rows, float* score, int with_traceback, int algorithm,
                 int32_t* seg_count,
                 int32_t* segments, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Emission prologue: projected scores (B, T, C) -> cumulative scores
+ * (B, T+1, C) fp32 with a zero first row, optionally zero-centred per (b, c)
+ * over all T positions, and its backward.
+ * Replaces:
+ *   nn.py:196-209  torch.zeros(B, T+1, C) + cumsum(scores.float(), dim=1)
+ *   streaming/autograd.py:300-340, streaming/__init__.py:85-121  the
+ *                  zero-centring recipe projected - projected.mean(dim=1)
+ * scores may be fp32, bf16 or fp16 (dtype TSM_DTYPE_*); prefix sums are carried
+ * in fp64 and rounded once to fp32.
+ *   tsm_cum_scores_backward: grad_scores[b,t,c] = sum_{u>t} grad_cum[b,u,c]
+ *   (minus its mean over t when centred), fp32.
+ * One workspace size serves both calls.
+ * ------------------------------------------------------------------------- */
+int tsm_prologue_workspace(int64_t B, int64_t T, int64_t C, size_t* bytes);
+int tsm_cum_scores(const void* scores, int dtype, int64_t B, int64_t T, int64_t C, int centre, float* cum_scores,
+                   void* workspace, size_t workspace_bytes, void* stream);
+int tsm_cum_scores_backward(const float* grad_cum, int64_t B, int64_t T, int64_t C, int centre, float* grad_scores,
+                            void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Gold-path score: the score of the segmentation implied by per-position

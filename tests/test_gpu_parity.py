@@ -461,6 +461,57 @@ def test_viterbi_auto_picks_factorised_for_large_problems():
     np.testing.assert_allclose(s_fact.cpu().numpy(), s_ex.cpu().numpy(), rtol=5e-5)
 
 
+# --------------------------------------------------------------------------- emission prologue
+PROLOGUE_CASES = [(2, 37, 5, torch.float32), (3, 1000, 24, torch.float32), (1, 700, 300, torch.float32),
+                  (2, 513, 8, torch.bfloat16), (2, 257, 6, torch.float16), (1, 1, 3, torch.float32)]
+
+
+@pytest.mark.parametrize("B,T,C,dtype", PROLOGUE_CASES)
+@pytest.mark.parametrize("centre", [False, True])
+def test_emission_prologue_vs_fp64(B, T, C, dtype, centre):
+    """Cumulative scores = the fp32 rounding of the fp64 prefix sums (zero row
+    first; zero-centred per (b, c) over T when asked), and the gradient of the
+    scores = autograd through the fp64 restatement."""
+    from torch_semimarkov_amd.streaming import emission_cum_scores
+
+    g = torch.Generator().manual_seed(B * 1000 + T + C)
+    x = (torch.randn(B, T, C, generator=g) + 0.3).to(dtype)
+    x64 = x.double().requires_grad_(True)
+    xs = x64 - x64.mean(dim=1, keepdim=True) if centre else x64
+    want = torch.cat([torch.zeros(B, 1, C, dtype=torch.float64), xs.cumsum(1)], dim=1)
+    xd = x.to(DEV).requires_grad_(True)
+    got = emission_cum_scores(xd, zero_centre=centre)
+    assert got.dtype == torch.float32 and got.shape == (B, T + 1, C)
+    np.testing.assert_allclose(got.detach().cpu().double().numpy(), want.detach().numpy(), rtol=1e-7, atol=1e-6)
+    gw = torch.randn(B, T + 1, C, generator=g)
+    (gx,) = torch.autograd.grad((got * gw.to(DEV)).sum(), xd)
+    (gx64,) = torch.autograd.grad((want * gw.double()).sum(), x64)
+    assert gx.dtype == dtype
+    tol = dict(rtol=1e-6, atol=1e-5) if dtype == torch.float32 else dict(rtol=1e-2, atol=1e-1)
+    np.testing.assert_allclose(gx.cpu().double().numpy(), gx64.numpy(), **tol)
+
+
+def test_emission_prologue_full_length_invariants():
+    """T = 10^6, C = 24 (the headline shape): row 0 is zero, the last row is the
+    column total (fp64 reference), centred columns end at ~0, and the head's
+    cumulative scores are the prologue's."""
+    from torch_semimarkov_amd.streaming import emission_cum_scores
+
+    B, T, C = 1, 1_000_000, 24
+    g = torch.Generator().manual_seed(77)
+    x = torch.randn(B, T, C, generator=g)
+    cum = emission_cum_scores(x.to(DEV)).cpu()
+    assert torch.all(cum[:, 0] == 0)
+    np.testing.assert_allclose(cum[:, -1].double().numpy(), x.double().sum(1).numpy(), rtol=1e-7, atol=1e-3)
+    mid = x[:, :123457].double().sum(1)
+    np.testing.assert_allclose(cum[:, 123457].double().numpy(), mid.numpy(), rtol=1e-7, atol=1e-3)
+    cen = emission_cum_scores(x.to(DEV), zero_centre=True).cpu()
+    assert cen[:, -1].abs().max() < 1e-3
+    head = tsa.SemiMarkovCRFHead(C, 4).to(DEV)
+    torch.testing.assert_close(head._cum_scores(x[:, :5000].to(DEV)), emission_cum_scores(x[:, :5000].to(DEV)),
+                               rtol=0, atol=0)
+
+
 # --------------------------------------------------------------------------- gold-path score
 GOLD_CASES = [(1, 3, 17, 4, 5), (2, 2, 9, 3, 1), (3, 4, 30, 5, 40), (4, 2, 1, 3, 4), (5, 3, 5000, 7, 300),
               (6, 2, 2100, 4, 3), (7, 3, 64, 130, 9)]

@@ -768,6 +768,66 @@ int tsm_viterbi(const float* cum, const float* tr, const float* db, const int64_
   return TSM_OK;
 }
 
+int tsm_prologue_workspace(int64_t B, int64_t T, int64_t C, size_t* bytes) {
+  if (!bytes) return fail(TSM_ERR_INVALID, "bytes is NULL");
+  if (B < 1 || T < 1 || C < 1)
+    return fail(TSM_ERR_INVALID, "need B, T, C >= 1 (got %lld, %lld, %lld)", (long long)B, (long long)T, (long long)C);
+  if (T > (int64_t)1 << 30 || B * C > (int64_t)1 << 30)
+    return fail(TSM_ERR_UNSUPPORTED, "prologue: sizes too large (B=%lld, T=%lld, C=%lld)", (long long)B,
+                (long long)T, (long long)C);
+  const size_t nbl = (size_t)tsm::prologue_blocks((int)T);
+  Carver cv(nullptr);
+  cv.take<double>((size_t)B * nbl * C);
+  cv.take<double>((size_t)B * nbl * C);
+  cv.take<double>((size_t)B * C);
+  *bytes = cv.off + 256;
+  return TSM_OK;
+}
+
+static int run_prologue(const void* x, int dtype, const float* g, int64_t B, int64_t T, int64_t C, int centre,
+                        float* cum, float* gx, void* workspace, size_t ws_bytes, void* stream, const char* what) {
+  size_t need = 0;
+  int rc = tsm_prologue_workspace(B, T, C, &need);
+  if (rc) return rc;
+  if (!workspace || ws_bytes < need)
+    return fail(TSM_ERR_WORKSPACE, "%s: workspace too small: %zu < %zu bytes", what, ws_bytes, need);
+  const size_t nbl = (size_t)tsm::prologue_blocks((int)T);
+  Carver cv(workspace);
+  tsm::PrologueParams q{};
+  q.part = cv.take<double>((size_t)B * nbl * C);
+  q.part2 = cv.take<double>((size_t)B * nbl * C);
+  q.mean = cv.take<double>((size_t)B * C);
+  q.x = x;
+  q.dtype = dtype;
+  q.g = g;
+  q.cum = cum;
+  q.gx = gx;
+  q.B = (int)B;
+  q.T = (int)T;
+  q.C = (int)C;
+  q.NBL = (int)nbl;
+  q.centre = centre ? 1 : 0;
+  const int e = tsm::launch_prologue(q, g != nullptr, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, what);
+  return TSM_OK;
+}
+
+int tsm_cum_scores(const void* scores, int dtype, int64_t B, int64_t T, int64_t C, int centre, float* cum,
+                   void* workspace, size_t ws_bytes, void* stream) {
+  if (!scores || !cum) return fail(TSM_ERR_INVALID, "scores and cum_scores are required");
+  if (dtype != TSM_DTYPE_F32 && dtype != TSM_DTYPE_BF16 && dtype != TSM_DTYPE_F16)
+    return fail(TSM_ERR_INVALID, "dtype must be TSM_DTYPE_F32 (0), _BF16 (1) or _F16 (2), got %d", dtype);
+  return run_prologue(scores, dtype, nullptr, B, T, C, centre, cum, nullptr, workspace, ws_bytes, stream,
+                      "tsm_cum_scores");
+}
+
+int tsm_cum_scores_backward(const float* grad_cum, int64_t B, int64_t T, int64_t C, int centre, float* grad_scores,
+                            void* workspace, size_t ws_bytes, void* stream) {
+  if (!grad_cum || !grad_scores) return fail(TSM_ERR_INVALID, "grad_cum and grad_scores are required");
+  return run_prologue(nullptr, TSM_DTYPE_F32, grad_cum, B, T, C, centre, nullptr, grad_scores, workspace, ws_bytes,
+                      stream, "tsm_cum_scores_backward");
+}
+
 int tsm_gold_score_workspace(int64_t B, int64_t T, int64_t C, int64_t K, int64_t db_rows, size_t* bytes) {
   if (!bytes) return fail(TSM_ERR_INVALID, "bytes is NULL");
   int rc = check_gold(B, T, C, K, db_rows);

@@ -135,6 +135,20 @@ struct GoldParams {
   float* gdb;              // (Kdb, C)
 };
 
+// Emission prologue: projected scores -> cumulative scores (and backward).
+struct PrologueParams {
+  const void* x;     // (B, T, C) scores, dtype TSM_DTYPE_*
+  int dtype;
+  const float* g;    // backward: (B, T+1, C) gradient of cum
+  float* cum;        // (B, T+1, C)
+  float* gx;         // backward: (B, T, C)
+  double* part;      // (B, NBL, C) block sums, then carries
+  double* part2;     // (B, NBL, C) backward: position-weighted block sums
+  double* mean;      // (B, C) centring term
+  int B, T, C, NBL;
+  int centre;
+};
+
 // launchers (return hipError_t as int)
 int launch_scan_forward(const Plan& pl, const ScanParams& p, int semiring, hipStream_t s);
 int launch_scan_backward(const Plan& pl, const ScanParams& p, int semiring, hipStream_t s);
@@ -170,6 +184,8 @@ int launch_viterbi(const Plan& pl, const ViterbiParams& v, int with_traceback, h
 int launch_dense_prep(const Plan& pl, const float* trans, float* trf, float* trb, hipStream_t s);
 int launch_dense_scan(const Plan& pl, const ScanParams& p, int semiring, bool forward, hipStream_t s);
 int launch_dense_marginals(const Plan& pl, const MargParams& q, hipStream_t s);
+int prologue_blocks(int T);
+int launch_prologue(const PrologueParams& q, bool bwd, hipStream_t s);
 int gold_chunks(int T);
 size_t gold_lds_bytes(int K);
 int launch_gold_score(const GoldParams& g, hipStream_t s);
@@ -194,6 +210,7 @@ enum KernelId : int {
   kKRetry,
   kKTransPrep,
   kKGold,
+  kKPrologue,
   kNumKernels
 };
 

@@ -22,6 +22,7 @@ const char* const kNames[kNumKernels] = {
     "bwd_fixup_kernel",  "apply_offsets_kernel", "marginal_kernel",         "finalize_rows_kernel",
     "finalize_shared_kernel", "checkpoints_kernel", "viterbi_kernel",       "backtrace_kernel",
     "retry_kernel",      "dense_prep_kernel",    "gold_kernels",
+    "prologue_kernels",
 };
 
 struct Pending {

@@ -17,6 +17,9 @@ _lib = None
 
 TSM_SEMIRING_LOG = 0
 TSM_SEMIRING_MAX = 1
+TSM_DTYPE_F32 = 0
+TSM_DTYPE_BF16 = 1
+TSM_DTYPE_F16 = 2
 TSM_VITERBI_AUTO = 0
 TSM_VITERBI_EXACT = 1
 TSM_VITERBI_FACTORISED = 2
@@ -48,6 +51,9 @@ _SIGNATURES = {
     "tsm_viterbi_workspace": ([_i64, _i64, _i64, _i64, _i64, _i32, ctypes.POINTER(_sz)], _i32),
     "tsm_viterbi": (
         [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _i32, _i32, _p, _p, _p, _sz, _p], _i32),
+    "tsm_prologue_workspace": ([_i64, _i64, _i64, ctypes.POINTER(_sz)], _i32),
+    "tsm_cum_scores": ([_p, _i32, _i64, _i64, _i64, _i32, _p, _p, _sz, _p], _i32),
+    "tsm_cum_scores_backward": ([_p, _i64, _i64, _i64, _i32, _p, _p, _sz, _p], _i32),
     "tsm_gold_score_workspace": ([_i64, _i64, _i64, _i64, _i64, ctypes.POINTER(_sz)], _i32),
     "tsm_gold_score": ([_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _p, _sz, _p], _i32),
     "tsm_gold_score_backward": (

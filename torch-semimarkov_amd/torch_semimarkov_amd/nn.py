@@ -21,6 +21,7 @@ from .duration import DurationDistribution, LearnedDuration
 from .helpers import Segment, ViterbiResult, score_gold_vectorized
 from .streaming import ops
 from .streaming.autograd import prepare_inputs, semi_crf_streaming_forward
+from .streaming.prologue import emission_cum_scores
 
 
 class SemiMarkovCRFHead(nn.Module):
@@ -71,12 +72,12 @@ class SemiMarkovCRFHead(nn.Module):
 
     # ------------------------------------------------------------------ helpers
     def _cum_scores(self, hidden_states: Tensor) -> Tensor:
-        """``(B, T+1, C)`` fp32 prefix sums of the projected scores, row 0 = 0 (``nn.py:196-209``)."""
-        B, T, _ = hidden_states.shape
+        """``(B, T+1, C)`` fp32 prefix sums of the projected scores, row 0 = 0 (``nn.py:196-209``),
+        built by the HIP emission prologue (fp64 prefix sums rounded once)."""
         scores = self.projection(hidden_states) if self.projection is not None else hidden_states
-        cum = torch.zeros(B, T + 1, self.num_classes, dtype=torch.float32, device=scores.device)
-        cum[:, 1:] = torch.cumsum(scores.float(), dim=1)
-        return cum
+        if scores.shape[-1] != self.num_classes:
+            raise ValueError(f"scores have {scores.shape[-1]} labels, the head {self.num_classes}")
+        return emission_cum_scores(scores)
 
     # ------------------------------------------------------------------ API
     def forward(self, hidden_states: Tensor, lengths: Tensor, use_triton: bool = True) -> dict:
@@ -155,12 +156,10 @@ class SemiMarkovCRFHead(nn.Module):
                 rows_h = rows.cpu().numpy()
                 for b in want:
                     n = counts[b]
-                    out = []
-                    for i in range(n - 1, -1, -1):
-                        c_, d_, t_ = host[b, i]
-                        out.append(Segment(start=int(rows_h[b, i, 0]), end=int(rows_h[b, i, 1]),
-                                           label=int(rows_h[b, i, 2]), score=float((c_ + d_) + t_)))
-                    all_segments[b] = out
+                    # first segment first; plain Python ints / floats via tolist()
+                    r = rows_h[b, :n][::-1].tolist()
+                    h = host[b, :n][::-1].tolist()
+                    all_segments[b] = [Segment(s_, e_, l_, (c_ + d_) + t_) for (s_, e_, l_, _), (c_, d_, t_) in zip(r, h)]
         return ViterbiResult(scores=score, segments=all_segments)
 
     def extra_repr(self) -> str:

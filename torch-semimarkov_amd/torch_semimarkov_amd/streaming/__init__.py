@@ -6,7 +6,8 @@ autograd function, ``compute_edge_block_streaming``,
 ``_compute_checkpoint_interval`` and ``NEG_INF``.  The launchers are
 ``launch_streaming_hip_kernel`` / ``launch_streaming_hip_backward`` (the
 reference's Triton launchers' contracts); ``HAS_HIP`` reports whether the
-native library is built.
+native library is built.  ``emission_cum_scores`` builds the cumulative scores
+from projected scores on the GPU (optionally zero-centred).
 """
 
 from __future__ import annotations
@@ -25,6 +26,7 @@ from .autograd import (
     semi_crf_streaming_forward,
 )
 from .constants import NEG_INF
+from .prologue import emission_cum_scores
 
 HAS_HIP = os.path.exists(_native.library_path())
 

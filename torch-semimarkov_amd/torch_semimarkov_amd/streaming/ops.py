@@ -173,6 +173,52 @@ def _(cum, transition, duration_bias, lengths, K, proj_start, proj_end, tracebac
     return cum.new_empty(B), cum.new_empty(0, dtype=torch.int32), cum.new_empty(0, dtype=torch.int32)
 
 
+# --------------------------------------------------------------------------- emission prologue
+_DTYPES = {torch.float32: N.TSM_DTYPE_F32, torch.bfloat16: N.TSM_DTYPE_BF16, torch.float16: N.TSM_DTYPE_F16}
+
+
+@torch.library.custom_op("tsm_amd::cum_scores", mutates_args=())
+def cum_scores(scores: Tensor, centre: bool) -> Tensor:
+    """(B, T+1, C) fp32 prefix sums of ``scores`` (B, T, C) (fp32 / bf16 / fp16), row 0 = 0."""
+    lib = N.lib()
+    B, T, C = scores.shape
+    dev = scores.device
+    out = torch.empty(B, T + 1, C, device=dev, dtype=torch.float32)
+    ws = _workspace(_size(lib.tsm_prologue_workspace, B, T, C), dev)
+    with torch.cuda.device(dev):
+        rc = lib.tsm_cum_scores(N.ptr(scores), _DTYPES[scores.dtype], B, T, C, int(centre), N.ptr(out), N.ptr(ws),
+                                ws.numel(), _stream(dev))
+    N.check(rc, "tsm_cum_scores")
+    return out
+
+
+@cum_scores.register_fake
+def _(scores, centre):
+    B, T, C = scores.shape
+    return scores.new_empty(B, T + 1, C, dtype=torch.float32)
+
+
+@torch.library.custom_op("tsm_amd::cum_scores_backward", mutates_args=())
+def cum_scores_backward(grad_cum: Tensor, centre: bool) -> Tensor:
+    """(B, T, C) fp32 gradient of the scores from the gradient of the cumulative scores."""
+    lib = N.lib()
+    B, Tp1, C = grad_cum.shape
+    dev = grad_cum.device
+    out = torch.empty(B, Tp1 - 1, C, device=dev, dtype=torch.float32)
+    ws = _workspace(_size(lib.tsm_prologue_workspace, B, Tp1 - 1, C), dev)
+    with torch.cuda.device(dev):
+        rc = lib.tsm_cum_scores_backward(N.ptr(grad_cum), B, Tp1 - 1, C, int(centre), N.ptr(out), N.ptr(ws),
+                                         ws.numel(), _stream(dev))
+    N.check(rc, "tsm_cum_scores_backward")
+    return out
+
+
+@cum_scores_backward.register_fake
+def _(grad_cum, centre):
+    B, Tp1, C = grad_cum.shape
+    return grad_cum.new_empty(B, Tp1 - 1, C)
+
+
 # --------------------------------------------------------------------------- gold-path score
 @torch.library.custom_op("tsm_amd::gold_score", mutates_args=())
 def gold_score(cum: Tensor, transition: Tensor, duration_bias: Tensor, labels: Tensor, lengths: Tensor,
