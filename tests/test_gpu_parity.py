@@ -512,6 +512,72 @@ def test_emission_prologue_full_length_invariants():
                                rtol=0, atol=0)
 
 
+# --------------------------------------------------------------------------- uncertainty consumers
+def _oracle_uncertainty(head, hidden, L):
+    """The reference's streaming uncertainty formulas (uncertainty.py:92-160, 263-368)
+    evaluated with the fp64 oracle's backward."""
+    with torch.no_grad():
+        scores = head.projection(hidden) if head.projection is not None else hidden
+    s = scores.detach().cpu().double().requires_grad_(True)
+    B, T, C = s.shape
+    cum = torch.cat([torch.zeros(B, 1, C, dtype=torch.float64), s.cumsum(1)], dim=1)
+    tr = head.transition.detach().cpu().double()
+    db = head.duration_bias.detach().cpu().double()
+    part = R.streaming_oracle(cum, tr, db, L.cpu(), head.max_duration, "log")
+    g_cum, g_s = torch.autograd.grad(part.sum(), (cum, s))
+    boundary = g_cum[:, 1:].abs().sum(-1)
+    pos = torch.softmax(g_s.abs(), dim=-1)
+    p = boundary / (boundary.sum(-1, keepdim=True) + 1e-8)
+    entropy = -(p * torch.log(p.clamp(min=1e-10))).sum(-1)
+    return boundary, pos, entropy
+
+
+@pytest.mark.parametrize("hidden_dim", [None, 16])
+def test_uncertainty_consumers_vs_fp64_oracle(hidden_dim):
+    B, T, C, K = 3, 80, 5, 9
+    torch.manual_seed(11)
+    head = tsa.UncertaintySemiMarkovCRFHead(C, K, hidden_dim=hidden_dim).to(DEV)
+    g = torch.Generator().manual_seed(12)
+    hidden = torch.randn(B, T, hidden_dim or C, generator=g).to(DEV)
+    L = torch.tensor([80, 51, 7])
+    want_b, want_p, want_h = _oracle_uncertainty(head, hidden, L)
+    got_b = head.compute_boundary_marginals(hidden, L.to(DEV), normalize=False)
+    np.testing.assert_allclose(got_b.cpu().double().numpy(), want_b.numpy(), rtol=1e-5, atol=1e-4)
+    got_n = head.compute_boundary_marginals(hidden, L.to(DEV))
+    want_n = want_b / (want_b.max(-1, keepdim=True)[0] + 1e-8)
+    np.testing.assert_allclose(got_n.cpu().double().numpy(), want_n.numpy(), rtol=1e-5, atol=1e-5)
+    got_p = head.compute_position_marginals(hidden, L.to(DEV))
+    np.testing.assert_allclose(got_p.cpu().double().numpy(), want_p.numpy(), rtol=1e-5, atol=1e-5)
+    got_h = head.compute_entropy_streaming(hidden, L.to(DEV))
+    np.testing.assert_allclose(got_h.cpu().double().numpy(), want_h.numpy(), rtol=1e-5, atol=1e-5)
+    labels = torch.randint(0, C, (B, T), generator=g).to(DEV)
+    for mode in ("high_uncertainty", "boundary_regions"):
+        lw = head.compute_loss_uncertainty_weighted(hidden, L.to(DEV), labels, 0.7, mode, reduction="none")
+        nll = head.compute_loss(hidden, L.to(DEV), labels, reduction="none")
+        u = got_h / (got_h.max() + 1e-8) if mode == "high_uncertainty" else got_n.mean(-1)
+        torch.testing.assert_close(lw, nll * (1.0 + 0.7 * u), rtol=1e-5, atol=1e-5)
+        lw.sum().backward()
+    with pytest.raises(NotImplementedError):
+        head.compute_boundary_marginals(hidden, L.to(DEV), use_streaming=False)
+    with pytest.raises(NotImplementedError):
+        head.compute_entropy_exact(hidden, L.to(DEV))
+
+
+def test_uncertainty_marginals_are_probabilities():
+    """Properties the forward-backward fixes: boundary signal at every interior
+    position = 2 * P(boundary) summed over labels is in [0, 2]; position
+    marginals sum to one."""
+    B, T, C, K = 2, 500, 6, 20
+    torch.manual_seed(3)
+    head = tsa.UncertaintySemiMarkovCRFHead(C, K).to(DEV)
+    hidden = torch.randn(B, T, C, device=DEV)
+    L = torch.tensor([500, 320], device=DEV)
+    sig = head.compute_boundary_marginals(hidden, L, normalize=False)
+    assert sig.shape == (B, T) and bool((sig >= 0).all()) and bool((sig <= 2.0 + 1e-4).all())
+    pm = head.compute_position_marginals(hidden, L)
+    torch.testing.assert_close(pm.sum(-1), torch.ones(B, T, device=DEV), rtol=1e-5, atol=1e-5)
+
+
 # --------------------------------------------------------------------------- gold-path score
 GOLD_CASES = [(1, 3, 17, 4, 5), (2, 2, 9, 3, 1), (3, 4, 30, 5, 40), (4, 2, 1, 3, 4), (5, 3, 5000, 7, 300),
               (6, 2, 2100, 4, 3), (7, 3, 64, 130, 9)]

@@ -8,6 +8,9 @@ Public API (same names and meanings as the reference package for this path):
   ``decode_with_traceback``
 * :class:`Segment`, :class:`ViterbiResult`, :func:`score_gold_vectorized`
 * :func:`compute_edge_block_streaming`, :class:`SemiCRFStreamingHIP`
+* :class:`UncertaintyMixin`, :class:`UncertaintySemiMarkovCRFHead` -- boundary /
+  position marginals, streaming entropy, uncertainty-weighted loss
+* :func:`emission_cum_scores` -- projected scores to cumulative scores on the GPU
 """
 
 from .duration import DurationDistribution, LearnedDuration
@@ -18,8 +21,10 @@ from .streaming import (
     NEG_INF,
     SemiCRFStreamingHIP,
     compute_edge_block_streaming,
+    emission_cum_scores,
     semi_crf_streaming_forward,
 )
+from .uncertainty import UncertaintyMixin, UncertaintySemiMarkovCRFHead
 
 __version__ = "0.1.0"
 
@@ -35,4 +40,7 @@ __all__ = [
     "LearnedDuration",
     "NEG_INF",
     "HAS_HIP",
+    "UncertaintyMixin",
+    "UncertaintySemiMarkovCRFHead",
+    "emission_cum_scores",
 ]
