@@ -28,7 +28,7 @@
 
 #include "tsm_device.hpp"
 #include "tsm_internal.hpp"
-#include "tsm_scan_common.hpp"
+#include "tsm_chunk_driver.hpp"
 
 namespace tsm {
 namespace {
@@ -494,37 +494,21 @@ __device__ void backward_chunk(const ScanParams& p, char* smem_base, int b, int 
 }
 
 
-template <int J, int RMAX, bool LOGSR, bool GR>
-__global__ void __launch_bounds__(512) scan_fwd_kernel(ScanParams p) {
-  extern __shared__ __align__(16) char smem[];
-  const int b = blockIdx.x / p.P, j = blockIdx.x % p.P;
-  const int len = seq_len(p, b);
-  const int item = b * p.P + j;
-  if (j > 0 && j * p.Lc >= len) {
-    if (threadIdx.x == 0) p.status[item] = -1;  // empty chunk
-    return;
+// Chunk type of the generic scans for the shared chunk driver (tsm_chunk_driver.hpp).
+template <int J, int RMAX, bool LOGSR, bool GR, bool FWD>
+struct GenericChunk {
+  static constexpr bool kFwd = FWD;
+  static constexpr bool kLog = LOGSR;
+  static constexpr int kMaxThreads = 512;
+  __device__ static double* red(char* smem, const ScanParams& p) {
+    return reinterpret_cast<double*>(smem + scan_lds_layout(p.C, p.KP, p.RS, p.RL, GR).red);
   }
-  if (p.retry && retry_skip(p, item)) return;
-  const int mode = fwd_spec(p, j) ? 1 : 0;
-  if (threadIdx.x == 0) p.status[item] = mode;
-  forward_chunk<J, RMAX, LOGSR, GR>(p, smem, b, j, mode, nullptr, nullptr);
-}
-
-template <int J, int RMAX, bool LOGSR, bool GR>
-__global__ void __launch_bounds__(512) scan_bwd_kernel(ScanParams p) {
-  extern __shared__ __align__(16) char smem[];
-  const int b = blockIdx.x / p.P, j = blockIdx.x % p.P;
-  const int len = seq_len(p, b);
-  const int item = b * p.P + j;
-  if (j > bwd_last_chunk(p, len)) {
-    if (threadIdx.x == 0) p.status[item] = -1;
-    return;
+  __device__ static void run(const ScanParams& p, char* smem, int b, int j, int mode, const float* init_st,
+                             const double* init_lv) {
+    if constexpr (FWD) forward_chunk<J, RMAX, LOGSR, GR>(p, smem, b, j, mode, init_st, init_lv);
+    else backward_chunk<J, RMAX, LOGSR, GR>(p, smem, b, j, mode, init_st, init_lv);
   }
-  if (p.retry && retry_skip(p, item)) return;
-  const int mode = bwd_spec(p, j, len) ? 1 : 0;
-  if (threadIdx.x == 0) p.status[item] = mode;
-  backward_chunk<J, RMAX, LOGSR, GR>(p, smem, b, j, mode, nullptr, nullptr);
-}
+};
 
 // Spread of (exact - speculative) over the boundary state of every speculative
 // chunk, all boundaries in parallel: vstat[item] = (max, min) of
@@ -553,99 +537,6 @@ __global__ void __launch_bounds__(256) verify_kernel(ScanParams p, int forward) 
 }
 
 // Sequential verification / repair of a sequence's chunks (one block per sequence).
-template <int J, int RMAX, bool LOGSR, bool GR>
-__global__ void __launch_bounds__(512) fwd_fixup_kernel(ScanParams p) {
-  extern __shared__ __align__(16) char smem[];
-  const int b = blockIdx.x;
-  const int len = seq_len(p, b);
-  const ScanLds L = scan_lds_layout(p.C, p.KP, p.RS, p.RL, GR);
-  double* red = reinterpret_cast<double*>(smem + L.red);
-  const int Kmax = p.Kmax, C = p.C;
-  const int nch = len == 0 ? 1 : (len + p.Lc - 1) / p.Lc;
-  double F = 0.0;
-  int n_re = 0;
-  if (threadIdx.x == 0) p.offs[(size_t)b * p.P] = 0.0;
-  bool prev_recomputed = false;
-  for (int j = 1; j < nch; ++j) {
-    const int item = b * p.P + j;
-    if (p.status[item] != 1) {
-      F = 0.0;  // chunk ran exactly from position 0
-      prev_recomputed = false;
-    } else {
-      const size_t e = (size_t)(item - 1), sp = (size_t)item;
-      double dmax, dmin;
-      if (!prev_recomputed) {
-        // measured in parallel by verify_kernel against chunk j-1's original end state
-        dmax = p.vstat[2 * sp];
-        dmin = p.vstat[2 * sp + 1];
-      } else {
-        // chunk j-1 was recomputed here: its end state changed, measure again
-        double hi, lo;
-        boundary_spread_part(p, e, sp, hi, lo);
-        block_minmax(hi, lo, red, dmax, dmin);
-      }
-      if (dmax - dmin <= (double)p.tol) {
-        F += 0.5 * (dmax + dmin);
-        prev_recomputed = false;
-      } else {
-        forward_chunk<J, RMAX, LOGSR, GR>(p, smem, b, j, 2, p.st_end + e * Kmax * C, p.lv_end + e * Kmax);
-        __syncthreads();
-        ++n_re;
-        prev_recomputed = true;
-        if (threadIdx.x == 0) p.status[item] = 2;
-      }
-    }
-    if (threadIdx.x == 0) p.offs[(size_t)item] = F;
-  }
-  __syncthreads();
-  finish_partition<LOGSR>(p, b, len, F, n_re);
-}
-
-template <int J, int RMAX, bool LOGSR, bool GR>
-__global__ void __launch_bounds__(512) bwd_fixup_kernel(ScanParams p) {
-  extern __shared__ __align__(16) char smem[];
-  const int b = blockIdx.x;
-  const int len = seq_len(p, b);
-  const ScanLds L = scan_lds_layout(p.C, p.KP, p.RS, p.RL, GR);
-  double* red = reinterpret_cast<double*>(smem + L.red);
-  const int Kmax = p.Kmax, C = p.C;
-  const int jl = bwd_last_chunk(p, len);
-  double F = 0.0;
-  int n_re = 0;
-  if (threadIdx.x == 0) p.offs[(size_t)b * p.P + jl] = 0.0;
-  bool prev_recomputed = false;
-  for (int j = jl - 1; j >= 0; --j) {
-    const int item = b * p.P + j;
-    if (p.status[item] != 1) {
-      F = 0.0;  // chunk ran exactly from position len
-      prev_recomputed = false;
-    } else {
-      const size_t e = (size_t)(item + 1), sp = (size_t)item;
-      double dmax, dmin;
-      if (!prev_recomputed) {
-        dmax = p.vstat[2 * sp];
-        dmin = p.vstat[2 * sp + 1];
-      } else {
-        double hi, lo;
-        boundary_spread_part(p, e, sp, hi, lo);
-        block_minmax(hi, lo, red, dmax, dmin);
-      }
-      if (dmax - dmin <= (double)p.tol) {
-        F += 0.5 * (dmax + dmin);
-        prev_recomputed = false;
-      } else {
-        backward_chunk<J, RMAX, LOGSR, GR>(p, smem, b, j, 2, p.st_end + e * Kmax * C, p.lv_end + e * Kmax);
-        __syncthreads();
-        ++n_re;
-        prev_recomputed = true;
-        if (threadIdx.x == 0) p.status[item] = 2;
-      }
-    }
-    if (threadIdx.x == 0) p.offs[(size_t)item] = F;
-  }
-  if (threadIdx.x == 0 && p.recomputed != nullptr) p.recomputed[b] = n_re;
-}
-
 // Add each chunk's frame offset to the levels it owns (global frame afterwards).
 __global__ void apply_offsets_kernel(ScanParams p, int forward) {
   const int b = blockIdx.y;
@@ -660,54 +551,8 @@ __global__ void apply_offsets_kernel(ScanParams p, int forward) {
 
 template <int J, int RMAX, bool LOGSR, bool GR>
 int launch_dir(const Plan& pl, const ScanParams& p, bool forward, hipStream_t st) {
-  const size_t lds = pl.scan_lds;
-  if (forward) {
-    auto k1 = scan_fwd_kernel<J, RMAX, LOGSR, GR>;
-    auto k2 = fwd_fixup_kernel<J, RMAX, LOGSR, GR>;
-    hipError_t e = hipFuncSetAttribute((const void*)k1, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    e = hipFuncSetAttribute((const void*)k2, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    {
-      TimedLaunch tl(kKScanFwd, st);
-      hipLaunchKernelGGL(k1, dim3(pl.B * pl.P), dim3(pl.NT), lds, st, p);
-    }
-    launch_verify(pl, p, true, st);
-    if (pl.P > 1) {
-      const ScanParams q = retry_params(p);
-      TimedLaunch tl(kKRetry, st);
-      hipLaunchKernelGGL(k1, dim3(pl.B * pl.P), dim3(pl.NT), lds, st, q);
-    }
-    if (pl.P > 1) launch_verify(pl, p, true, st);
-    {
-      TimedLaunch tl(kKFwdFixup, st);
-      hipLaunchKernelGGL(k2, dim3(pl.B), dim3(pl.NT), lds, st, p);
-    }
-  } else {
-    auto k1 = scan_bwd_kernel<J, RMAX, LOGSR, GR>;
-    auto k2 = bwd_fixup_kernel<J, RMAX, LOGSR, GR>;
-    hipError_t e = hipFuncSetAttribute((const void*)k1, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    e = hipFuncSetAttribute((const void*)k2, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    {
-      TimedLaunch tl(kKScanBwd, st);
-      hipLaunchKernelGGL(k1, dim3(pl.B * pl.P), dim3(pl.NT), lds, st, p);
-    }
-    launch_verify(pl, p, false, st);
-    if (pl.P > 1) {
-      const ScanParams q = retry_params(p);
-      TimedLaunch tl(kKRetry, st);
-      hipLaunchKernelGGL(k1, dim3(pl.B * pl.P), dim3(pl.NT), lds, st, q);
-    }
-    if (pl.P > 1) launch_verify(pl, p, false, st);
-    {
-      TimedLaunch tl(kKBwdFixup, st);
-      hipLaunchKernelGGL(k2, dim3(pl.B), dim3(pl.NT), lds, st, p);
-    }
-  }
-  launch_apply_offsets(pl, p, forward, st);
-  return hipGetLastError();
+  return forward ? launch_chunk_dir<GenericChunk<J, RMAX, LOGSR, GR, true>>(pl, p, pl.scan_lds, pl.NT, st)
+                 : launch_chunk_dir<GenericChunk<J, RMAX, LOGSR, GR, false>>(pl, p, pl.scan_lds, pl.NT, st);
 }
 
 template <int RMAX, bool LOGSR, bool GR>
