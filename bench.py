@@ -187,6 +187,7 @@ def bench_head(args):
 def bench_viterbi(args):
     """cfg4: Viterbi with backtrace (max semiring), 64 ragged sequences."""
     import torch_semimarkov_amd as tsa
+    from torch_semimarkov_amd import _native as N
     from torch_semimarkov_amd.streaming import ops
 
     seed = 20261204
@@ -207,11 +208,14 @@ def bench_viterbi(args):
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    N.timing_enable(True)  # per-kernel HIP events on the launch stream
     t0 = time.perf_counter()
     for _ in range(args.steps):
         out = step()
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    ktimes = N.timing_read()
+    N.timing_enable(False)
     cells_sum = int(lengths.sum()) * K * C * C
     print(json.dumps({
         "metric": "Viterbi + backtrace cells/s (sum_b L_b*K*C^2), 1 GPU", "value": cells_sum / (ms / 1e3),
@@ -220,6 +224,7 @@ def bench_viterbi(args):
         "config": {"workload": "cfg4: Viterbi with traceback, ragged lengths in [4096, 8192]", "B": B,
                    "T_max": T, "C": C, "K": K, "seed": seed},
         "cells_B_Tmax": B * T * K * C * C, "value_B_Tmax": B * T * K * C * C / (ms / 1e3),
+        "kernel_avg_ms": {k: v[0] / v[1] for k, v in sorted(ktimes.items())},
     }))
 
 

@@ -433,7 +433,10 @@ size_t viterbi_ws_bytes(const Plan& pl, int with_tb) {
   Carver cv(nullptr);
   if (with_tb) cv.take<int32_t>((size_t)pl.B * (pl.T + 1) * pl.C);
   cv.take<int32_t>(pl.B);
-  if (pl.fast) carve_scan(cv, pl);
+  if (pl.fast) {
+    carve_scan(cv, pl);
+    if (with_tb) cv.take<int32_t>((size_t)pl.B * (pl.T + 1) * pl.C);  // factorised backpointers, exact format
+  }
   return cv.off + 256;
 }
 
@@ -721,6 +724,7 @@ int tsm_viterbi(const float* cum, const float* tr, const float* db, const int64_
     int32_t* bp = with_tb ? cv.take<int32_t>((size_t)pl.B * (pl.T + 1) * pl.C) : nullptr;
     cv.take<int32_t>(pl.B);
     ScanWs w = carve_scan(cv, pl);
+    int32_t* bp_exact = with_tb ? cv.take<int32_t>((size_t)pl.B * (pl.T + 1) * pl.C) : nullptr;
     tsm::ScanParams p = scan_params(pl, w, cum, tr, db, len, ps, pe);
     p.val = nullptr;
     p.lvl = nullptr;
@@ -730,7 +734,7 @@ int tsm_viterbi(const float* cum, const float* tr, const float* db, const int64_
     int e = tsm::launch_scan_viterbi(pl, p, st);
     if (e != hipSuccess) return hip_fail(e, "tsm_viterbi (factorised scan)");
     if (with_tb) {
-      e = tsm::launch_backtrace_fact(pl, bp, w.fin, len, seg_count, segments, st);
+      e = tsm::launch_backtrace_fact(pl, bp, bp_exact, w.fin, len, seg_count, segments, st);
       if (e != hipSuccess) return hip_fail(e, "tsm_viterbi (backtrace)");
     }
     return TSM_OK;

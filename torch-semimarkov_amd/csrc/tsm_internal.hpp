@@ -170,8 +170,8 @@ int launch_fast_max_j16_hi(const Plan& pl, const ScanParams& p, hipStream_t s);
 int launch_fast_max_j32(const Plan& pl, const ScanParams& p, hipStream_t s);
 int launch_fast_max_j64(const Plan& pl, const ScanParams& p, hipStream_t s);
 int launch_scan_viterbi(const Plan& pl, const ScanParams& p, hipStream_t s);
-int launch_backtrace_fact(const Plan& pl, const int32_t* bp, const float* fin, const int64_t* lengths,
-                          int32_t* seg_count, int32_t* segs, hipStream_t s);
+int launch_backtrace_fact(const Plan& pl, const int32_t* bp, int32_t* bp_exact, const float* fin,
+                          const int64_t* lengths, int32_t* seg_count, int32_t* segs, hipStream_t s);
 // register-resident marginals (16 lanes per label, pl.MR durations per lane)
 int launch_margfast_j16(const Plan& pl, const MargParams& q, hipStream_t s);
 int launch_margfast_j16_lo(const Plan& pl, const MargParams& q, hipStream_t s);
