@@ -264,6 +264,18 @@ int make_plan(int64_t B, int64_t T, int64_t C, int64_t K, int has_ps, int has_pe
     return TSM_OK;
   }
   plan_fast(p, di);
+  if (p.fast) {
+    // the register-resident scan keeps a chunk's state in LDS: when several fit
+    // on a CU, give each CU that many chunks (their step chains overlap)
+    const int64_t per_cu = std::max<int64_t>(1, std::min<int64_t>(4, (int64_t)di.max_lds / (int64_t)p.fast_lds));
+    const int64_t min_lc = std::max<int64_t>(4 * (int64_t)p.W, 512);
+    int64_t P2 = cdiv((int64_t)di.n_cu * per_cu, B);
+    P2 = std::max<int64_t>(1, std::min<int64_t>(P2, std::max<int64_t>(1, T / min_lc)));
+    if (P2 > p.P) {
+      p.P = (int)P2;
+      p.Lc = (int)cdiv(T, P2);
+    }
+  }
   p.mfast = 0;
   const char* env = getenv("TSM_SCAN_PATH");
   const bool generic_only = env != nullptr && strcmp(env, "generic") == 0;
