@@ -260,38 +260,43 @@ __global__ void finalize_rows_kernel(FinalParams f) {
 
 // Shared gradients: sum over sequences (weighted by grad_output) and blocks, in fp64.
 // With duration-dependent transitions grad_tr is (trows, C, C): matrix k gets the
-// partials of duration k (1 <= k <= Kmax), the others are zero.
-__global__ void finalize_shared_kernel(FinalParams f) {
+// partials of duration k (1 <= k <= Kmax), the others are zero.  One wavefront
+// per output element: lane l takes the (sequence, block) partials l, l+64, ...
+// and the wave sums them in a fixed order (deterministic).
+__global__ void __launch_bounds__(256) finalize_shared_kernel(FinalParams f) {
   const int C = f.C, K = f.K, Kmax = f.Kmax;
   const int n_tr = (f.trows > 0 ? f.trows : 1) * C * C, n_db = K * C;
-  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  const int idx = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (idx >= n_tr + n_db) return;
+  const int nparts = f.B * f.NB;
+  const double* src = nullptr;
+  size_t per = 0, off = 0;
   if (idx < n_tr) {
     const int k = idx / (C * C), e = idx % (C * C);
-    double acc = 0.0;
     if (f.trows == 0 || (k >= 1 && k <= Kmax)) {
-      const size_t per = (size_t)(f.trows > 0 ? Kmax : 1) * C * C;
-      const size_t off = (f.trows > 0) ? (size_t)(k - 1) * C * C + e : (size_t)e;
-      for (int b = 0; b < f.B; ++b) {
-        double s = 0.0;
-        for (int i = 0; i < f.NB; ++i) s += f.tr_part[((size_t)b * f.NB + i) * per + off];
-        acc += (double)f.grad_output[b] * s;
-      }
+      per = (size_t)(f.trows > 0 ? Kmax : 1) * C * C;
+      off = (f.trows > 0) ? (size_t)(k - 1) * C * C + e : (size_t)e;
+      src = f.tr_part;
     }
-    f.grad_tr[idx] = (float)acc;
-  } else if (idx < n_tr + n_db) {
+  } else {
     const int e = idx - n_tr;
     const int k = e / C, c = e % C;
     // durations mapping to duration-bias row k: k itself (K >= 2, k >= 1) or 1 (K == 1)
     const int dur = (K == 1) ? 1 : k;
-    double acc = 0.0;
     if (dur >= 1 && dur <= Kmax) {
-      for (int b = 0; b < f.B; ++b) {
-        double s = 0.0;
-        for (int i = 0; i < f.NB; ++i) s += f.db_part[(((size_t)b * f.NB + i) * Kmax + dur - 1) * C + c];
-        acc += (double)f.grad_output[b] * s;
-      }
+      per = (size_t)Kmax * C;
+      off = (size_t)(dur - 1) * C + c;
+      src = f.db_part;
     }
-    f.grad_db[e] = (float)acc;
+  }
+  double acc = 0.0;
+  if (src != nullptr)
+    for (int j = lane; j < nparts; j += 64) acc += (double)f.grad_output[j / f.NB] * src[(size_t)j * per + off];
+  for (int m = 32; m >= 1; m >>= 1) acc += __shfl_xor(acc, m, 64);
+  if (lane == 0) {
+    if (idx < n_tr) f.grad_tr[idx] = (float)acc;
+    else f.grad_db[idx - n_tr] = (float)acc;
   }
 }
 
@@ -360,7 +365,7 @@ int launch_finalize(const Plan& pl, const FinalParams& f, hipStream_t s) {
   const int n = (f.trows > 0 ? f.trows : 1) * pl.C * pl.C + pl.K * pl.C;
   {
     TimedLaunch tl(kKFinalizeShared, s);
-    hipLaunchKernelGGL(finalize_shared_kernel, dim3((n + 255) / 256), dim3(256), 0, s, f);
+    hipLaunchKernelGGL(finalize_shared_kernel, dim3((n + 3) / 4), dim3(256), 0, s, f);
   }
   return hipGetLastError();
 }
