@@ -220,7 +220,7 @@ int make_plan(int64_t B, int64_t T, int64_t C, int64_t K, int has_ps, int has_pe
   // chunking: about one work item per CU; chunks long enough that the warm-up
   // (W steps) costs at most ~25%.
   p.W = p.Kmax + 64;
-  const int64_t min_lc = std::max<int64_t>(4 * (int64_t)p.W, 512);
+  const int64_t min_lc = std::max<int64_t>(4 * (int64_t)p.W, 128);
   int64_t P = cdiv(di.n_cu, B);
   P = std::min<int64_t>(P, std::max<int64_t>(1, T / min_lc));
   P = std::max<int64_t>(P, 1);
@@ -268,7 +268,7 @@ int make_plan(int64_t B, int64_t T, int64_t C, int64_t K, int has_ps, int has_pe
     // the register-resident scan keeps a chunk's state in LDS: when several fit
     // on a CU, give each CU that many chunks (their step chains overlap)
     const int64_t per_cu = std::max<int64_t>(1, std::min<int64_t>(4, (int64_t)di.max_lds / (int64_t)p.fast_lds));
-    const int64_t min_lc = std::max<int64_t>(4 * (int64_t)p.W, 512);
+    const int64_t min_lc = std::max<int64_t>(4 * (int64_t)p.W, 128);
     int64_t P2 = cdiv((int64_t)di.n_cu * per_cu, B);
     P2 = std::max<int64_t>(1, std::min<int64_t>(P2, std::max<int64_t>(1, T / min_lc)));
     if (P2 > p.P) {
