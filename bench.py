@@ -1,6 +1,6 @@
 """Benchmark of the streaming semi-CRF scan on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg3] [--cpu-sample T] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg3] [--cpu-sample T] [--no-cpu] [--no-passes]
 
 A step is one forward + backward (log semiring) over the whole synthetic
 workload "cfg3" by default: B=1, T=1,000,000, C=24, K=300, emissions N(0,1)
@@ -77,18 +77,35 @@ def profiled_executed(kernel, workload):
     """Executed VALU lane-op and transcendental rates of `kernel` from the committed
     SQ-counter summary (lines `executed <kernel> <workload> <lane-ops/s> <trans/s>`)."""
     path = os.path.join(PROFILES, f"pmc_instructions_{workload}.txt")
+    out = None
     try:
         with open(path) as f:
             for ln in f:
                 parts = ln.split()
                 if len(parts) == 5 and parts[0] == "executed" and parts[1] == kernel and parts[2] == workload:
                     v, t = float(parts[3]), float(parts[4])
-                    return {"valu_lane_ops_per_s": v, "valu_frac_nonpacked_peak": v / V_PEAK_NONPACKED,
-                            "transcendental_per_s": t, "transcendental_frac": t / T_PEAK,
-                            "source": os.path.relpath(path, ROOT)}
+                    out = {"valu_lane_ops_per_s": v, "valu_frac_nonpacked_peak": v / V_PEAK_NONPACKED,
+                           "transcendental_per_s": t, "transcendental_frac": t / T_PEAK,
+                           "source": os.path.relpath(path, ROOT)}
+                    break
     except OSError:
         pass
-    return None
+    # VALU-busy and LDS bank-conflict figures of the same kernel (lines
+    # `busy <kernel> <workload> <VALUBusy%> <LDSBankConflict%> <conflicts/access>`)
+    bpath = os.path.join(PROFILES, f"pmc_lds_valu_{workload}.txt")
+    try:
+        with open(bpath) as f:
+            for ln in f:
+                parts = ln.split()
+                if len(parts) == 6 and parts[0] == "busy" and parts[1] == kernel and parts[2] == workload:
+                    out = dict(out or {})
+                    out.update({"valu_busy_pct": float(parts[3]), "lds_bank_conflict_pct": float(parts[4]),
+                                "lds_conflicts_per_access": float(parts[5]),
+                                "busy_source": os.path.relpath(bpath, ROOT)})
+                    break
+    except OSError:
+        pass
+    return out
 
 
 def copy_calibration(mib=256, reps=3):
@@ -264,6 +281,38 @@ def cpu_baseline(name, cum, tr, db, K, t_sample):
     }
 
 
+def measure_passes(args, cum, tr, db, L, K, cells, fwdbwd_ms, plan):
+    """Per-pass rates on the same resident inputs: the no-grad forward (log
+    partition only), forward + backward (the timed step) and Viterbi with
+    backtrace (max semiring), each as nominal cells/s and as a fraction of that
+    pass's roofline (ops per cell fixed in OPS).  Viterbi is timed only where
+    the register-resident plan exists (plan["fast"]); otherwise the exact
+    kernel would run K*C^2 terms per step on one workgroup per sequence."""
+    from torch_semimarkov_amd.streaming import ops
+
+    def timed(fn):
+        for _ in range(max(1, args.warmup)):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3 / args.steps
+
+    with torch.no_grad():
+        fwd = timed(lambda: ops.scan_forward(cum, tr, db, L, K, 0, None, None, False))
+        vit = timed(lambda: ops.viterbi(cum, tr, db, L, K, None, None, True)) if plan.get("fast") else None
+
+    def entry(ms, kind):
+        rate = cells / (ms / 1e3)
+        return {"ms": ms, "cells_per_s": rate, "nominal_roofline_frac": rate / roofline_cells_per_s(kind),
+                "roofline_cells_per_s": roofline_cells_per_s(kind)}
+
+    return {"forward_log": entry(fwd, "fwd_log"), "forward_backward_log": entry(fwdbwd_ms, "fwdbwd_log"),
+            "viterbi_traceback": entry(vit, "max") if vit is not None else None}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -272,6 +321,8 @@ def main():
     ap.add_argument("--config", default="cfg3", choices=sorted(list(CONFIGS) + ["cfg1", "cfg4"]))
     ap.add_argument("--cpu-sample", type=int, default=4000)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-passes", action="store_true",
+                    help="skip the per-pass timings (forward only, Viterbi), e.g. under a profiler")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 256 MiB device copy (PMC counter calibration)")
     args = ap.parse_args()
@@ -336,12 +387,15 @@ def main():
 
     cells = B * T * K * C * C
     value = cells / (ms_step / 1e3)
+    passes = None if args.no_passes else measure_passes(args, cum.detach(), tr.detach(), db.detach(), L, K, cells,
+                                                          ms_step, plan)
     # dominant kernel: the largest total time over the timed steps
     dom = max((k for k in ktimes if k in KERNEL_OPS), key=lambda k: ktimes[k][0])
     dom_total, dom_launches = ktimes[dom]
     dom_avg_ms = dom_total / dom_launches
     nv, nt = KERNEL_OPS[dom]
     achieved = cells * (nv + nt * V_PEAK / T_PEAK) / (dom_avg_ms / 1e3) / 1e12
+    traffic = profiled_traffic(dom, args.config)
     peak = V_PEAK / 1e12
     out = {
         "metric": "fwd+bwd scan cells/s (B*T*K*C^2), 1 GPU",
@@ -367,7 +421,12 @@ def main():
             "peak": peak,
             "unit": "TFLOP/s",
             "frac": achieved / peak,
-            "traffic": profiled_traffic(dom, args.config),
+            "traffic": traffic,
+            # achieved HBM rate of the dominant kernel (profiled bytes / launch time) and of its
+            # emission stream alone (the (B, T+1, C) fp32 cumulative scores, read once per pass)
+            "hbm_gb_per_s": traffic / (dom_avg_ms / 1e3) / 1e9 if traffic else None,
+            "emission_stream_gb_per_s": B * (T + 1) * C * 4 / (dom_avg_ms / 1e3) / 1e9,
+            "hbm_peak_gb_per_s": 8000.0,
             "executed": profiled_executed(dom, args.config),
             "avg_launch_ms": dom_avg_ms,
             "ops_per_cell": {"valu": nv, "transcendental": nt},
@@ -376,6 +435,7 @@ def main():
                     "(K*C + C^2 instead of K*C^2 terms per position), so frac can exceed 1",
         },
         "nominal_roofline_frac_fwdbwd": value / roofline_cells_per_s("fwdbwd_log"),
+        "passes": passes,
         "fwd_ms": fwd_ms,
         "bwd_ms": bwd_ms,
         "kernel_avg_ms": {k: v[0] / v[1] for k, v in sorted(ktimes.items())},
