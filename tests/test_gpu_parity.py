@@ -461,6 +461,73 @@ def test_viterbi_auto_picks_factorised_for_large_problems():
     np.testing.assert_allclose(s_fact.cpu().numpy(), s_ex.cpu().numpy(), rtol=5e-5)
 
 
+# --------------------------------------------------------------------------- chunked backtrace
+def _sticky_problem(B, T, K, C, lengths, winner, seed):
+    """Label chains that never merge.  A self-transition bonus of +100 dwarfs every
+    emission difference, so each label's best path stays in that label and is made
+    of unit segments (two of them beat one of duration 2 by ~100); `winner` gains
+    0.01 per position and is the optimum.  Walks that start at label 0 therefore
+    never meet the true path, and every chunk below the top one is walked again
+    from its true entry node."""
+    g = torch.Generator().manual_seed(seed)
+    em = 0.05 * torch.randn(B, T, C, generator=g)
+    em[:, :, winner] += 0.01
+    cum = torch.zeros(B, T + 1, C)
+    cum[:, 1:] = em.cumsum(1)
+    tr = torch.full((C, C), -5.0) + 105.0 * torch.eye(C)
+    db = 0.1 * torch.randn(K, C, generator=g)
+    db[1] = 0.0  # unit segments: no label gains on duration bias
+    return cum, tr, db, torch.tensor(lengths, dtype=torch.long)
+
+
+@pytest.mark.parametrize("algorithm", ["exact", "factorised"])
+@pytest.mark.parametrize("walk", ["lds", "global"])
+def test_backtrace_rewalks_chunks_that_never_merge(algorithm, walk, monkeypatch):
+    """Chunked backtrace where no speculative walk merges: the result must still be
+    the true path (unit segments of the winning label, every chunk's record full)."""
+    if walk == "global":
+        monkeypatch.setenv("TSM_BACKTRACE_PATH", "global")
+    B, T, K, C, winner = 2, 5000, 6, 4, 2
+    lengths = [5000, 3333]
+    cum, tr, db, L = _sticky_problem(B, T, K, C, lengths, winner, 123)
+    alg = N.TSM_VITERBI_EXACT if algorithm == "exact" else N.TSM_VITERBI_FACTORISED
+    score, cnt, segs = ops.viterbi(*to_dev(cum, tr, db, L), K, None, None, True, alg)
+    want, _, _ = R.forward(cum.double(), tr.double(), db.double(), L, K, "max")
+    np.testing.assert_allclose(score.cpu().double().numpy(), want.numpy(), rtol=1e-5)
+    cnt, segs = cnt.cpu(), segs.cpu()
+    for b in range(B):
+        n = lengths[b]
+        assert int(cnt[b]) == n
+        expect = torch.tensor([[t, t, winner, winner] for t in range(n - 1, -1, -1)], dtype=torch.int32)
+        assert torch.equal(segs[b, :n], expect), b
+
+
+@pytest.mark.parametrize("walk", ["lds", "global"])
+def test_backtrace_many_chunks_vs_oracle(walk, monkeypatch):
+    """Chunked backtrace on long random sequences (several chunks each, ragged):
+    the exact algorithm's segments equal the fp32 restatement's traceback, and
+    the factorised algorithm's path is a valid segmentation at the fp64 optimum."""
+    if walk == "global":
+        monkeypatch.setenv("TSM_BACKTRACE_PATH", "global")
+    B, T, K, C = 3, 6000, 12, 8
+    lengths = [6000, 4500, 2100]
+    cum, tr, db, L, _, _ = rand_problem(B, T, K, C, 202, lengths, tscale=0.5, dscale=0.5)
+    args = to_dev(cum, tr, db, L) + [K, None, None, True]
+    s_e, c_e, g_e = ops.viterbi(*args, N.TSM_VITERBI_EXACT)
+    s_f, c_f, g_f = ops.viterbi(*args, N.TSM_VITERBI_FACTORISED)
+    want, _, _ = R.forward(cum.double(), tr.double(), db.double(), L, K, "max")
+    np.testing.assert_allclose(s_f.cpu().double().numpy(), want.numpy(), rtol=1e-5)
+    c_e, g_e, c_f, g_f = c_e.cpu(), g_e.cpu(), c_f.cpu(), g_f.cpu()
+    for b in range(B):
+        n = lengths[b]
+        ref, _ = R.viterbi_traceback_single(cum[b], tr, db, K, n)
+        got = [tuple(int(v) for v in g_e[b, i]) for i in range(int(c_e[b]) - 1, -1, -1)]
+        assert got == [tuple(s) for s in ref], b
+        fact = [tuple(int(v) for v in g_f[b, i]) for i in range(int(c_f[b]) - 1, -1, -1)]
+        total = _path_total_fp64(cum[b].double(), tr.double(), db.double(), K, n, fact)
+        assert abs(total - float(want[b])) <= 1e-5 * abs(float(want[b])) + 1e-6, b
+
+
 # --------------------------------------------------------------------------- emission prologue
 PROLOGUE_CASES = [(2, 37, 5, torch.float32), (3, 1000, 24, torch.float32), (1, 700, 300, torch.float32),
                   (2, 513, 8, torch.bfloat16), (2, 257, 6, torch.float16), (1, 1, 3, torch.float32)]

@@ -449,6 +449,7 @@ size_t viterbi_ws_bytes(const Plan& pl, int with_tb) {
     carve_scan(cv, pl);
     if (with_tb) cv.take<int32_t>((size_t)pl.B * (pl.T + 1) * pl.C);  // factorised backpointers, exact format
   }
+  if (with_tb) cv.take<char>(tsm::backtrace_ws_bytes(tsm::backtrace_plan(pl.B, pl.T, pl.C, pl.Kmax), pl.B));
   return cv.off + 256;
 }
 
@@ -737,6 +738,8 @@ int tsm_viterbi(const float* cum, const float* tr, const float* db, const int64_
     cv.take<int32_t>(pl.B);
     ScanWs w = carve_scan(cv, pl);
     int32_t* bp_exact = with_tb ? cv.take<int32_t>((size_t)pl.B * (pl.T + 1) * pl.C) : nullptr;
+    const tsm::BtPlan btp = tsm::backtrace_plan(pl.B, pl.T, pl.C, pl.Kmax);
+    void* bt_ws = with_tb ? cv.take<char>(tsm::backtrace_ws_bytes(btp, pl.B)) : nullptr;
     tsm::ScanParams p = scan_params(pl, w, cum, tr, db, len, ps, pe);
     p.val = nullptr;
     p.lvl = nullptr;
@@ -746,7 +749,10 @@ int tsm_viterbi(const float* cum, const float* tr, const float* db, const int64_
     int e = tsm::launch_scan_viterbi(pl, p, st);
     if (e != hipSuccess) return hip_fail(e, "tsm_viterbi (factorised scan)");
     if (with_tb) {
-      e = tsm::launch_backtrace_fact(pl, bp, bp_exact, w.fin, len, seg_count, segments, st);
+      e = tsm::launch_fact_to_exact(bp, len, pl.B, pl.T, pl.C, bp_exact, st);
+      if (e != hipSuccess) return hip_fail(e, "tsm_viterbi (backpointer format)");
+      e = tsm::launch_backtrace(btp, bp_exact, w.fin, nullptr, len, pl.B, pl.T, pl.C, pl.Kmax, bt_ws, seg_count,
+                                segments, st);
       if (e != hipSuccess) return hip_fail(e, "tsm_viterbi (backtrace)");
     }
     return TSM_OK;
@@ -777,10 +783,20 @@ int tsm_viterbi(const float* cum, const float* tr, const float* db, const int64_
   v.RS = pl.RS;
   v.trows = pl.trows;
   v.score = score;
-  v.seg_count = seg_count;
-  v.segs = segments;
-  const int e = tsm::launch_viterbi(pl, v, with_tb, (hipStream_t)stream);
+  void* bt_ws = nullptr;
+  tsm::BtPlan btp{};
+  if (with_tb) {
+    btp = tsm::backtrace_plan(pl.B, pl.T, pl.C, pl.Kmax);
+    bt_ws = cv.take<char>(tsm::backtrace_ws_bytes(btp, pl.B));
+  }
+  hipStream_t st = (hipStream_t)stream;
+  int e = tsm::launch_viterbi(pl, v, st);
   if (e != hipSuccess) return hip_fail(e, "tsm_viterbi");
+  if (with_tb) {
+    e = tsm::launch_backtrace(btp, v.bp, nullptr, v.final_c, len, pl.B, pl.T, pl.C, pl.Kmax, bt_ws, seg_count,
+                              segments, st);
+    if (e != hipSuccess) return hip_fail(e, "tsm_viterbi (backtrace)");
+  }
   return TSM_OK;
 }
 

@@ -107,9 +107,6 @@ struct ViterbiParams {
   float* score;        // (B) Viterbi score (max over final labels)
   int32_t* bp;         // (B, T+1, C) packed backpointer (k << 16 | c_src), or null
   int32_t* final_c;    // (B) first argmax label at position len
-  // backtrace output
-  int32_t* seg_count;  // (B)
-  int32_t* segs;       // (B, T, 4): start, end, label, prev label (reverse order)
   int trows;           // transition is (trows, C, C), indexed by duration, when > 0
 };
 
@@ -170,15 +167,30 @@ int launch_fast_max_j16_hi(const Plan& pl, const ScanParams& p, hipStream_t s);
 int launch_fast_max_j32(const Plan& pl, const ScanParams& p, hipStream_t s);
 int launch_fast_max_j64(const Plan& pl, const ScanParams& p, hipStream_t s);
 int launch_scan_viterbi(const Plan& pl, const ScanParams& p, hipStream_t s);
-int launch_backtrace_fact(const Plan& pl, const int32_t* bp, int32_t* bp_exact, const float* fin,
-                          const int64_t* lengths, int32_t* seg_count, int32_t* segs, hipStream_t s);
+// Chunked speculative backtrace (tsm_backtrace.hip): P chunks of Lc positions per
+// sequence, walks starting D positions above their chunk, TCH backpointer rows
+// per LDS stage (0: rows read from global memory).
+constexpr int kBtMaxChunks = 512;
+struct BtPlan {
+  int P, Lc, D, TCH;
+};
+BtPlan backtrace_plan(int B, int T, int C, int Kmax);
+size_t backtrace_ws_bytes(const BtPlan& bp, int B);
+// bp in the exact format (k << 16 | c_prev); the path starts at (len, first
+// maximiser of fin[b, :]) when fin is given, else at (len, final_c[b])
+int launch_backtrace(const BtPlan& bpl, const int32_t* bp, const float* fin, const int32_t* final_c,
+                     const int64_t* lengths, int B, int T, int C, int Kmax, void* ws, int32_t* seg_count,
+                     int32_t* segs, hipStream_t s);
+// factorised backpointers (k* ending at t | c'* starting at t) to the exact format
+int launch_fact_to_exact(const int32_t* bp, const int64_t* lengths, int B, int T, int C, int32_t* out,
+                         hipStream_t s);
 // register-resident marginals (16 lanes per label, pl.MR durations per lane)
 int launch_margfast_j16(const Plan& pl, const MargParams& q, hipStream_t s);
 int launch_margfast_j16_lo(const Plan& pl, const MargParams& q, hipStream_t s);
 int launch_margfast_j16_hi(const Plan& pl, const MargParams& q, hipStream_t s);
 int launch_marginals(const Plan& pl, const MargParams& q, hipStream_t s);
 int launch_finalize(const Plan& pl, const FinalParams& f, hipStream_t s);
-int launch_viterbi(const Plan& pl, const ViterbiParams& v, int with_traceback, hipStream_t s);
+int launch_viterbi(const Plan& pl, const ViterbiParams& v, hipStream_t s);
 // duration-dependent transitions: log2-scaled tables of both directions
 // (trf [k-1][c_dst][c_src], trb [k-1][c_src][c_dst]), dense scans and marginals
 int launch_dense_prep(const Plan& pl, const float* trans, float* trf, float* trb, hipStream_t s);
