@@ -12,7 +12,7 @@
 //
 // One workgroup per sequence; the K x C alpha ring lives in LDS.  Lanes of a
 // label group split the durations; the transition row of the label sits in
-// registers when it is short enough (CMAX > 0).
+// registers (CMAX >= C, a multiple of 8) when the group has at least 16 lanes.
 
 #include "tsm_device.hpp"
 #include "tsm_internal.hpp"
@@ -24,11 +24,15 @@ struct VLds {
   size_t araw, crng, prng, dbn, trn, red, total;
 };
 
+// araw is position-major, [slot][c] with the odd row stride C|1: the source
+// labels of one ring position are consecutive (immediate-offset loads) and the
+// rows a label group reads at once fall on different banks.  crng / prng are
+// label-major, [c][slot].
 __host__ __device__ inline VLds vit_lds_layout(int C, int Kmax, int RS, int has_ps) {
   VLds L;
   size_t o = 0;
   const size_t ring = sizeof(float) * (size_t)C * RS;
-  L.araw = o; o = align16(o + ring);
+  L.araw = o; o = align16(o + sizeof(float) * (size_t)(C | 1) * RS);
   L.crng = o; o = align16(o + ring);
   L.prng = o; o = align16(o + (has_ps ? ring : 0));
   L.dbn = o; o = align16(o + sizeof(float) * (size_t)C * (Kmax + 1));
@@ -39,10 +43,10 @@ __host__ __device__ inline VLds vit_lds_layout(int C, int Kmax, int RS, int has_
 }
 
 template <int J, int CMAX>
-__global__ void __launch_bounds__(512) viterbi_kernel(ViterbiParams v) {
+__global__ void __launch_bounds__(1024) viterbi_kernel(ViterbiParams v) {
   extern __shared__ __align__(16) char smem[];
   const int b = blockIdx.x;
-  const int C = v.C, K = v.K, Kmax = v.Kmax, RS = v.RS, T = v.T;
+  const int C = v.C, K = v.K, Kmax = v.Kmax, RS = v.RS, T = v.T, CS = C | 1;
   int64_t L64 = v.lengths[b];
   const int len = (int)(L64 < 0 ? 0 : (L64 > T ? T : L64));
   const bool has_ps = v.ps != nullptr, has_pe = v.pe != nullptr;
@@ -75,7 +79,7 @@ __global__ void __launch_bounds__(512) viterbi_kernel(ViterbiParams v) {
     }
   }
   for (int cc = tid; cc < C; cc += NT) {
-    araw[cc * RS] = 0.0f;  // alpha[0, :] = 0
+    araw[cc] = 0.0f;  // alpha[0, :] = 0 (slot 0)
     crng[cc * RS] = cum_b[cc];
     if (has_ps && T > 0) prng[cc * RS] = ps_b[cc];
   }
@@ -83,17 +87,27 @@ __global__ void __launch_bounds__(512) viterbi_kernel(ViterbiParams v) {
   float tr_reg[CMAX > 0 ? CMAX : 1];
   if constexpr (CMAX > 0) {
 #pragma unroll
-    for (int i = 0; i < CMAX; ++i) tr_reg[i] = (i < C) ? trn[c * C + i] : 0.0f;
+    for (int i = 0; i < CMAX; ++i) tr_reg[i] = trn[c * C + min(i, C - 1)];  // padding repeats the last label
   }
   const float* dr = dbn + c * (Kmax + 1);
   const float* cr = crng + c * RS;
   const float* pr = prng + c * RS;
 
+  // this step's cumulative score and projections, loaded one step ahead
+  float cum_n = len >= 1 ? cum_b[(size_t)C + c] : 0.0f;
+  float pe_n = (has_pe && len >= 1) ? pe_b[c] : 0.0f;
+  float ps_n = (has_ps && len >= 1 && T > 1) ? ps_b[(size_t)C + c] : 0.0f;
   for (int t = 1; t <= len; ++t) {
     const int kcap = (K == 1) ? 1 : min(K - 1, t);
     const int base = t % RS;
-    const float cur_cum = cum_b[(size_t)t * C + c];
-    const float pe_t = has_pe ? pe_b[(size_t)(t - 1) * C + c] : 0.0f;
+    const float cur_cum = cum_n;
+    const float pe_t = pe_n;
+    const float ps_t = ps_n;  // proj_start of position t (ring entry of position t)
+    if (t < len) {
+      cum_n = cum_b[(size_t)(t + 1) * C + c];
+      if (has_pe) pe_n = pe_b[(size_t)t * C + c];
+      if (has_ps && t + 1 < T) ps_n = ps_b[(size_t)(t + 1) * C + c];
+    }
     float bv = kMinusInf;
     int bk = 0;
     for (int k = 1 + lj; k <= kcap; k += J) {
@@ -101,19 +115,46 @@ __global__ void __launch_bounds__(512) viterbi_kernel(ViterbiParams v) {
       float e1 = (cur_cum - cr[slot]) + dr[k];
       if (has_ps) e1 = e1 + pr[slot];
       if (has_pe) e1 = e1 + pe_t;
-      float m = kMinusInf;
+      // max over source labels; the loads of a block are issued together (indices
+      // past C repeat the last label's term, which leaves the max unchanged), and
+      // four running maxima keep the max chain short (max is exact in any order)
+      const float* arow = araw + (size_t)slot * CS;
+      float m4[4] = {kMinusInf, kMinusInf, kMinusInf, kMinusInf};
       if (v.trows > 0) {
         // duration-dependent transitions: transition[k][c_src][c], from global memory
         const float* tk = v.trans + (size_t)k * C * C + c;
-        for (int i = 0; i < C; ++i) m = fmax2(m, araw[i * RS + slot] + (e1 + tk[(size_t)i * C]));
-      } else if constexpr (CMAX > 0) {
+        for (int i0 = 0; i0 < C; i0 += 8) {
+          float a[8], tt[8];
 #pragma unroll
-        for (int i = 0; i < CMAX; ++i)
-          if (i < C) m = fmax2(m, araw[i * RS + slot] + (e1 + tr_reg[i]));
+          for (int u = 0; u < 8; ++u) {
+            const int i = min(i0 + u, C - 1);
+            a[u] = arow[i];
+            tt[u] = tk[(size_t)i * C];
+          }
+#pragma unroll
+          for (int u = 0; u < 8; ++u) m4[u & 3] = fmax2(m4[u & 3], a[u] + (e1 + tt[u]));
+        }
+      } else if constexpr (CMAX > 0) {
+        float a[CMAX];
+#pragma unroll
+        for (int i = 0; i < CMAX; ++i) a[i] = arow[min(i, C - 1)];
+#pragma unroll
+        for (int i = 0; i < CMAX; ++i) m4[i & 3] = fmax2(m4[i & 3], a[i] + (e1 + tr_reg[i]));
       } else {
         const float* trow = trn + c * C;
-        for (int i = 0; i < C; ++i) m = fmax2(m, araw[i * RS + slot] + (e1 + trow[i]));
+        for (int i0 = 0; i0 < C; i0 += 8) {
+          float a[8], tt[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            const int i = min(i0 + u, C - 1);
+            a[u] = arow[i];
+            tt[u] = trow[i];
+          }
+#pragma unroll
+          for (int u = 0; u < 8; ++u) m4[u & 3] = fmax2(m4[u & 3], a[u] + (e1 + tt[u]));
+        }
       }
+      const float m = fmax2(fmax2(m4[0], m4[1]), fmax2(m4[2], m4[3]));
       if (m > bv) {
         bv = m;
         bk = k;
@@ -133,7 +174,7 @@ __global__ void __launch_bounds__(512) viterbi_kernel(ViterbiParams v) {
       int ci = 0x7fffffff;
       const float* tk = v.trans + (size_t)ks * C * C + c;
       for (int i = lj; i < C; i += J) {
-        const float x = araw[i * RS + slot] + (e1 + (v.trows > 0 ? tk[(size_t)i * C] : trn[c * C + i]));
+        const float x = araw[(size_t)slot * CS + i] + (e1 + (v.trows > 0 ? tk[(size_t)i * C] : trn[c * C + i]));
         if (x > cv) {
           cv = x;
           ci = i;
@@ -145,9 +186,9 @@ __global__ void __launch_bounds__(512) viterbi_kernel(ViterbiParams v) {
     // slot t % RS holds position t - RS, which step t never reads (RS >= Kmax+1),
     // so the ring can be updated without waiting for the other labels' reads.
     if (cval && lj == 0) {
-      araw[c * RS + base] = best.v;
+      araw[(size_t)base * CS + c] = best.v;
       crng[c * RS + base] = cur_cum;
-      if (has_ps && t < T) prng[c * RS + base] = ps_b[(size_t)t * C + c];
+      if (has_ps && t < T) prng[c * RS + base] = ps_t;
     }
     __syncthreads();
   }
@@ -157,7 +198,7 @@ __global__ void __launch_bounds__(512) viterbi_kernel(ViterbiParams v) {
     float mv = kMinusInf;
     int mi = 0x7fffffff;
     for (int cc = tid; cc < C; cc += NT) {
-      const float x = araw[cc * RS + slot];
+      const float x = araw[(size_t)slot * CS + cc];
       if (x > mv || (x == mv && cc < mi)) {
         mv = x;
         mi = cc;
@@ -185,29 +226,52 @@ __global__ void __launch_bounds__(512) viterbi_kernel(ViterbiParams v) {
 }
 
 template <int J, int CMAX>
-int launch_vit_j(const Plan& pl, const ViterbiParams& v, hipStream_t st) {
+int launch_vit_j(const Plan& pl, const ViterbiParams& v, int nt, hipStream_t st) {
   const VLds L = vit_lds_layout(pl.C, pl.Kmax, pl.RS, v.ps != nullptr);
   auto k = viterbi_kernel<J, CMAX>;
   hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)L.total);
   if (e != hipSuccess) return e;
   TimedLaunch tl(kKViterbi, st);
-  hipLaunchKernelGGL(k, dim3(pl.B), dim3(pl.NT), L.total, st, v);
+  hipLaunchKernelGGL(k, dim3(pl.B), dim3(nt), L.total, st, v);
   return hipGetLastError();
+}
+
+// Transition row in registers, C rounded up to a multiple of 8 (CM), for J >= 16.
+template <int J>
+int launch_vit_cm(const Plan& pl, const ViterbiParams& v, int nt, hipStream_t st) {
+  const int cm = (pl.C + 7) / 8 * 8;
+  switch (cm) {
+    case 8: return launch_vit_j<J, 8>(pl, v, nt, st);
+    case 16: return launch_vit_j<J, 16>(pl, v, nt, st);
+    case 24: if constexpr (J <= 32) return launch_vit_j<J, 24>(pl, v, nt, st); break;
+    case 32: if constexpr (J <= 32) return launch_vit_j<J, 32>(pl, v, nt, st); break;
+    case 40: if constexpr (J <= 16) return launch_vit_j<J, 40>(pl, v, nt, st); break;
+    case 48: if constexpr (J <= 16) return launch_vit_j<J, 48>(pl, v, nt, st); break;
+    case 56: if constexpr (J <= 16) return launch_vit_j<J, 56>(pl, v, nt, st); break;
+    case 64: if constexpr (J <= 16) return launch_vit_j<J, 64>(pl, v, nt, st); break;
+    default: break;
+  }
+  return (int)hipErrorInvalidValue;
 }
 
 }  // namespace
 
 size_t viterbi_lds_bytes(int C, int Kmax, int RS, int has_ps) { return vit_lds_layout(C, Kmax, RS, has_ps).total; }
 
+// J lanes per label: the largest power of two <= 64 with C*J <= 1024 threads,
+// so a sequence's K*C^2 terms per step spread over up to 16 waves.
 int launch_viterbi(const Plan& pl, const ViterbiParams& v, hipStream_t s) {
-  switch (pl.J) {
-    case 1: return launch_vit_j<1, 0>(pl, v, s);
-    case 2: return launch_vit_j<2, 0>(pl, v, s);
-    case 4: return launch_vit_j<4, 0>(pl, v, s);
-    case 8: return launch_vit_j<8, 64>(pl, v, s);
-    case 16: return launch_vit_j<16, 32>(pl, v, s);
-    case 32: return launch_vit_j<32, 16>(pl, v, s);
-    case 64: return launch_vit_j<64, 8>(pl, v, s);
+  int J = 64;
+  while (J > 1 && pl.C * J > 1024) J >>= 1;
+  const int nt = (pl.C * J + 63) / 64 * 64;
+  switch (J) {
+    case 1: return launch_vit_j<1, 0>(pl, v, nt, s);
+    case 2: return launch_vit_j<2, 0>(pl, v, nt, s);
+    case 4: return launch_vit_j<4, 0>(pl, v, nt, s);
+    case 8: return launch_vit_j<8, 0>(pl, v, nt, s);
+    case 16: return launch_vit_cm<16>(pl, v, nt, s);
+    case 32: return launch_vit_cm<32>(pl, v, nt, s);
+    case 64: return launch_vit_cm<64>(pl, v, nt, s);
     default: return (int)hipErrorInvalidValue;
   }
 }
