@@ -279,10 +279,11 @@ int make_plan(int64_t B, int64_t T, int64_t C, int64_t K, int has_ps, int has_pe
   p.mfast = 0;
   const char* env = getenv("TSM_SCAN_PATH");
   const bool generic_only = env != nullptr && strcmp(env, "generic") == 0;
-  if (!generic_only && p.C <= 64 && (p.Kmax + 15) / 16 <= 32) {
+  if (!generic_only && p.C <= 128 && (p.Kmax + 15) / 16 <= 32) {
     // register-resident marginals: 16 lanes per label, one wavefront of 4 labels
-    // per workgroup, rings hold the KP positions of a step plus the 16 staged ahead
-    const int J = 16, MR = (p.Kmax + 15) / 16, KP = J * MR;
+    // per workgroup, rings hold the KP positions of a step plus the 16 staged ahead;
+    // above 64 labels the instances come in steps of 4 durations per lane
+    const int J = 16, MR = p.C > 64 ? ((p.Kmax + 15) / 16 + 3) / 4 * 4 : (p.Kmax + 15) / 16, KP = J * MR;
     const int CBm = 64 / J;
     const int RSm = std::max(p.Kmax + 2, KP + J);
     int RLm = RSm + KP;

@@ -54,6 +54,7 @@ int launch_margfast_j16_hi(const Plan& pl, const MargParams& q, hipStream_t st) 
 }
 
 int launch_margfast_j16(const Plan& pl, const MargParams& q, hipStream_t st) {
+  if (pl.C > 64) return launch_margfast_j16_wide(pl, q, st);
   return pl.MR <= 16 ? launch_margfast_j16_lo(pl, q, st) : launch_margfast_j16_hi(pl, q, st);
 }
 

@@ -188,6 +188,7 @@ int launch_fact_to_exact(const int32_t* bp, const int64_t* lengths, int B, int T
 int launch_margfast_j16(const Plan& pl, const MargParams& q, hipStream_t s);
 int launch_margfast_j16_lo(const Plan& pl, const MargParams& q, hipStream_t s);
 int launch_margfast_j16_hi(const Plan& pl, const MargParams& q, hipStream_t s);
+int launch_margfast_j16_wide(const Plan& pl, const MargParams& q, hipStream_t s);  // 64 < C <= 128
 int launch_marginals(const Plan& pl, const MargParams& q, hipStream_t s);
 int launch_finalize(const Plan& pl, const FinalParams& f, hipStream_t s);
 int launch_viterbi(const Plan& pl, const ViterbiParams& v, hipStream_t s);

@@ -36,8 +36,6 @@ namespace tsm {
 namespace margfast {
 
 constexpr double kInvD = -1e30;
-constexpr int kCJ = 4;  // labels per lane in the label mix (plans keep C <= 4*J)
-constexpr int kRowLoads = 16;  // alpha-hat row loads per lane per batch: J*C <= 1024
 constexpr double kLog2eD = 1.4426950408889634;
 
 __device__ __forceinline__ void wave_lds_order() { __asm__ volatile("" ::: "memory"); }
@@ -51,9 +49,13 @@ __device__ __forceinline__ int mlen(const int64_t* lengths, int b, int T) {
 
 constexpr int kDppRowRor15 = 0x12F;  // row_ror:15 -- lane i reads lane (i+1) mod 16 of its row
 
-template <int J, int R>
+// CJ source labels per lane in the label mix (C <= CJ * J); the batch's alpha-hat
+// rows (J * C floats) are staged with 4 * CJ loads per lane.
+template <int J, int R, int CJ>
 __global__ void __launch_bounds__(64) margfast_kernel(MargParams q) {
   static_assert(J == 16, "end sums slide along one 16-lane DPP row");
+  constexpr int kCJ = CJ;
+  constexpr int kRowLoads = 4 * CJ;
   extern __shared__ __align__(16) char smem[];
   constexpr int KP = J * R;
   constexpr int CB = 64 / J;
@@ -297,9 +299,9 @@ __global__ void __launch_bounds__(64) margfast_kernel(MargParams q) {
   }
 }
 
-template <int J, int R>
+template <int J, int R, int CJ = 4>
 int launch_margfast_jr(const Plan& pl, const MargParams& q, hipStream_t st) {
-  auto k = margfast_kernel<J, R>;
+  auto k = margfast_kernel<J, R, CJ>;
   hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)pl.marg_lds);
   if (e != hipSuccess) return e;
   TimedLaunch tl(kKMarginal, st);
