@@ -286,6 +286,68 @@ def test_generic_scan_paths_vs_fp64_oracle(B, T, K, C, lengths, proj, sr, plan, 
     assert_grads(grads, g64)
 
 
+# Cooperative scans (rings too large for one CU): groups of CG blocks, CCL labels
+# each, exchanging their row of results every step.
+COOP_CASES = [
+    (2, 300, 40, 128, [300, 177], False, dict(CG=4, CR=8)),
+    (2, 240, 40, 128, [240, 0], True, dict(CG=4, CR=8)),
+    (1, 150, 300, 128, None, False, dict(CG=8, CR=24)),
+    (1, 80, 500, 128, None, True, dict(CG=8, CR=32)),   # the C=128, K=500 configuration's instance
+    (1, 300, 200, 96, None, False, dict(CG=4, CR=16)),
+    (3, 200, 9, 80, [200, 150, 7], True, dict(CG=4, CR=8)),
+]
+
+
+@pytest.mark.parametrize("B,T,K,C,lengths,proj,plan", COOP_CASES)
+def test_coop_scan_vs_fp64_oracle(B, T, K, C, lengths, proj, plan):
+    got = N.plan_info(B, T, C, K, proj, proj)
+    assert got["coop"] == 1 and got["fast"] == 0, got
+    for key, v in plan.items():
+        assert got[key] == v, (key, got)
+    cum, tr, db, L, ps, pe = rand_problem(B, T, K, C, 4000 + T + K + C, lengths, proj)
+    g = torch.linspace(0.5, 2.0, B)
+    p64, g64 = oracle_fp64(cum, tr, db, L, K, "log", ps, pe, g)
+    part, grads = run_hip(cum, tr, db, L, K, "log", ps, pe, g)
+    live = L > 0
+    np.testing.assert_allclose(part[live].double().numpy(), p64[live].numpy(), rtol=RTOL_Z, atol=1e-6)
+    assert_grads(grads, g64)
+
+
+def test_coop_scan_chunked_vs_fp64_oracle():
+    """Several speculative chunks per sequence on the cooperative scan."""
+    B, T, K, C = 2, 4000, 12, 72
+    got = N.plan_info(B, T, C, K)
+    assert got["coop"] == 1 and got["P"] > 1, got
+    cum, tr, db, L, _, _ = rand_problem(B, T, K, C, 4321, [4000, 2900])
+    p64, g64 = oracle_fp64(cum, tr, db, L, K)
+    part, grads = run_hip(cum, tr, db, L, K)
+    np.testing.assert_allclose(part.double().numpy(), p64.numpy(), rtol=RTOL_Z)
+    assert_grads(grads, g64)
+
+
+def test_coop_scan_recomputes_non_mixing_chunks():
+    """Sticky transitions on the cooperative scan: speculative chunks fail
+    verification and the group recomputes them in the sequential repair pass."""
+    B, T, K, C = 1, 2400, 5, 72
+    assert N.plan_info(B, T, C, K)["coop"] == 1
+    g = torch.Generator().manual_seed(6)
+    em = 0.01 * torch.randn(B, T, C, generator=g)
+    em[:, :50, 0] += 2.0
+    cum = torch.zeros(B, T + 1, C)
+    cum[:, 1:] = em.cumsum(1)
+    tr = torch.full((C, C), -40.0)
+    tr.fill_diagonal_(0.0)
+    db = torch.zeros(K, C)
+    L = torch.tensor([T])
+    with torch.no_grad():
+        _, _, _, _, rec = ops.scan_forward(cum.to(DEV), tr.to(DEV), db.to(DEV), L.to(DEV), K, 0, None, None, False)
+    assert int(rec.sum()) > 0
+    p64, g64 = oracle_fp64(cum, tr, db, L, K)
+    part, grads = run_hip(cum, tr, db, L, K)
+    np.testing.assert_allclose(part.double().numpy(), p64.numpy(), rtol=RTOL_Z)
+    assert_grads(grads, g64)
+
+
 @pytest.mark.parametrize("B,T,K,C,lengths,proj,sr", CASES)
 def test_random_problems_vs_fp64_oracle(B, T, K, C, lengths, proj, sr, scan_path):
     cum, tr, db, L, ps, pe = rand_problem(B, T, K, C, 1000 + T + K + C, lengths, proj)

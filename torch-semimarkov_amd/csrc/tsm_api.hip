@@ -117,6 +117,48 @@ void plan_fast(Plan& p, const DeviceInfo& di) {
   }
 }
 
+// Cooperative log-semiring scan when no single-block plan holds the rings:
+// the smallest group size G (fewest blocks exchanging per step) whose per-block
+// rings fit LDS, 16 lanes per label, durations per lane rounded up to a
+// multiple of 8 (the compiled instances), at most 128 labels.  The group count
+// is what stays co-resident with one block per CU.
+void plan_coop(Plan& p, const DeviceInfo& di) {
+  p.coop = 0;
+  const char* env = getenv("TSM_SCAN_PATH");
+  if (env != nullptr && strcmp(env, "generic") == 0) return;
+  if (p.C > 128) return;
+  const int J = 16;
+  int R = (p.Kmax + J - 1) / J;
+  R = (R + 7) / 8 * 8;
+  if (R > 32) return;
+  const int KP = J * R;
+  const int RS = std::max(p.Kmax + 2, KP + 1);
+  int RL = RS + KP;
+  while (RL % 32 != J % 32) ++RL;
+  for (int G : {2, 4, 8, 16}) {
+    const int CL = (p.C + G - 1) / G;
+    // the instances' launch bounds (tsm_coopscan.hpp), and every member owns a label
+    if (CL * J > (R > 16 ? 256 : 512) || CL * (G - 1) >= p.C) continue;
+    const size_t lds = tsm::coop_lds_layout(CL, p.C, RL, RS).total;
+    if (lds > (size_t)di.max_lds) continue;
+    const int NQ = di.n_cu / G;
+    if (NQ < 1) continue;
+    p.coop = 1;
+    p.CG = G;
+    p.CCL = CL;
+    p.CR = R;
+    p.CNT = (int)cdiv((int64_t)CL * J, 64) * 64;
+    p.CRS = RS;
+    p.CRL = RL;
+    p.coop_lds = lds;
+    // members share blockIdx % 8 (one XCD) when whole groups of 8 fit the CUs
+    p.cxmap = (di.n_cu % (8 * G) == 0) ? 1 : 0;
+    p.CNQ = NQ;
+    p.CGRID = NQ * G;
+    return;
+  }
+}
+
 // Duration-dependent transitions: dense scans (J lanes per label, transitions
 // in LDS when they fit) and the dense marginal kernel (label groups of G lanes,
 // blocks of TB >= Kmax start positions whose start / end sums fit in LDS).
@@ -264,6 +306,17 @@ int make_plan(int64_t B, int64_t T, int64_t C, int64_t K, int has_ps, int has_pe
     return TSM_OK;
   }
   plan_fast(p, di);
+  if (!p.fast) plan_coop(p, di);
+  if (p.coop) {
+    // fewer, longer chunks (one per group): a 4x longer warm-up up front, which
+    // long segment durations need, at a small share of the chunk
+    p.W = 4 * (p.Kmax + 64);
+    const int64_t min_lc = 4 * (int64_t)p.W;
+    int64_t P = cdiv(p.CNQ, B);
+    P = std::max<int64_t>(1, std::min<int64_t>(P, std::max<int64_t>(1, T / min_lc)));
+    p.P = (int)P;
+    p.Lc = (int)cdiv(T, P);
+  }
   if (p.fast) {
     // the register-resident scan keeps a chunk's state in LDS: when several fit
     // on a CU, give each CU that many chunks (their step chains overlap)
@@ -336,6 +389,8 @@ struct ScanWs {
   float *st_spec, *st_end, *fin, *gring;
   double *lv_spec, *lv_end, *offs, *vstat, *fin_lvl, *z2;
   int* status;
+  unsigned long long* xch;
+  int* xabort;
 };
 
 ScanWs carve_scan(Carver& cv, const Plan& p) {
@@ -352,6 +407,8 @@ ScanWs carve_scan(Carver& cv, const Plan& p) {
   w.fin_lvl = cv.take<double>(p.B);
   w.z2 = cv.take<double>(p.B);
   w.gring = p.global_rings ? cv.take<float>(items * tsm::scan_gring_floats(p.C, p.KP, p.RL)) : nullptr;
+  w.xch = p.coop ? cv.take<unsigned long long>((size_t)p.CNQ * 2 * p.C) : nullptr;
+  w.xabort = p.coop ? cv.take<int>(1) : nullptr;
   return w;
 }
 
@@ -388,6 +445,12 @@ tsm::ScanParams scan_params(const Plan& pl, const ScanWs& w, const float* cum, c
   p.fin_lvl = w.fin_lvl;
   p.z2 = w.z2;
   p.gring = w.gring;
+  p.xch = w.xch;
+  p.xabort = w.xabort;
+  p.G = pl.CG;
+  p.CL = pl.CCL;
+  p.NQ = pl.CNQ;
+  p.xmap = pl.cxmap;
   return p;
 }
 
@@ -536,7 +599,7 @@ int tsm_plan_info(int64_t B, int64_t T, int64_t C, int64_t K, int64_t trans_rows
                           p.CB, p.NCB, p.JM, p.NTM, (int64_t)p.marg_lds, p.Kmax, di.n_cu, p.R, p.KP, p.RMAX,
                           p.fast, p.FJ, p.FR, p.FNT, (int64_t)p.fast_lds, p.mfast, p.MR,
                           p.dense, p.DJ, p.DNT, p.dtrl, (int64_t)p.dense_lds, p.DG, p.DNTM, p.DNB, p.DTB,
-                          (int64_t)p.dmarg_lds};
+                          (int64_t)p.dmarg_lds, p.coop, p.CG, p.CCL, p.CR, p.CNQ, (int64_t)p.coop_lds};
   const int m = (int)(sizeof(vals) / sizeof(vals[0]));
   for (int i = 0; i < n && i < m; ++i) out[i] = vals[i];
   return TSM_OK;

@@ -52,6 +52,12 @@ struct ScanParams {
   // direction, [k-1][out label][in label] for k = 1..Kmax
   int trows;
   const float* trx;
+  // cooperative scan: G blocks per group, CL labels per block, NQ groups,
+  // xmap = 1 when members share blockIdx % 8; per-group exchange buffers
+  // (NQ, 2, C) of (fp32 value | step stamp) words and the give-up flag
+  int G, CL, NQ, xmap;
+  unsigned long long* xch;
+  int* xabort;
 };
 
 struct MargParams {
@@ -166,6 +172,8 @@ int launch_fast_max_j16_lo(const Plan& pl, const ScanParams& p, hipStream_t s);
 int launch_fast_max_j16_hi(const Plan& pl, const ScanParams& p, hipStream_t s);
 int launch_fast_max_j32(const Plan& pl, const ScanParams& p, hipStream_t s);
 int launch_fast_max_j64(const Plan& pl, const ScanParams& p, hipStream_t s);
+// cooperative log-semiring scan (tsm_coop.hip), pl.CR durations per lane
+int launch_coop_scan(const Plan& pl, const ScanParams& p, bool forward, hipStream_t s);
 int launch_scan_viterbi(const Plan& pl, const ScanParams& p, hipStream_t s);
 // Chunked speculative backtrace (tsm_backtrace.hip): P chunks of Lc positions per
 // sequence, walks starting D positions above their chunk, TCH backpointer rows

@@ -42,6 +42,13 @@ struct Plan {
   size_t dense_lds;
   int DG, DNTM, DNB, DTB;
   size_t dmarg_lds;
+  // cooperative log-semiring scan (coop == 1, tsm_coopscan.hpp) when the rings of
+  // all labels do not fit one CU: groups of CG blocks, CCL labels per block with
+  // 16 lanes each (CNT threads), CR durations per lane, CRS ring slots, CRL ring
+  // row length, coop_lds bytes; CNQ co-resident groups, CGRID blocks, cxmap = 1
+  // when members share blockIdx % 8
+  int coop, CG, CCL, CR, CNT, CRS, CRL, CNQ, CGRID, cxmap;
+  size_t coop_lds;
 };
 
 
@@ -145,6 +152,26 @@ __host__ __device__ inline FastLds fast_lds_layout(int C, int RL, int RS) {
   L.lring = o; o = align16(o + sizeof(double) * RS);
   L.row = o; o = align16(o + sizeof(float) * 2 * C);
   L.red = o; o = align16(o + sizeof(double) * 64);
+  L.total = o;
+  return L;
+}
+
+// ---- cooperative scan LDS layout (one member of a group) -------------------
+// Rings of the member's CL labels (mirrored like the fast scan's), per-position
+// levels, the double-buffered row of all C labels, block reductions and the
+// give-up flag.
+struct CoopLds {
+  size_t ring, lring, row, red, flag, total;
+};
+
+__host__ __device__ inline CoopLds coop_lds_layout(int CL, int C, int RL, int RS) {
+  CoopLds L;
+  size_t o = 0;
+  L.ring = o; o = align16(o + 8 * (size_t)CL * RL);
+  L.lring = o; o = align16(o + sizeof(double) * RS);
+  L.row = o; o = align16(o + sizeof(float) * 2 * C);
+  L.red = o; o = align16(o + sizeof(double) * 64);
+  L.flag = o; o = align16(o + sizeof(int));
   L.total = o;
   return L;
 }

@@ -30,6 +30,7 @@ PLAN_FIELDS = (
     "CB", "NCB", "JM", "NTM", "marg_lds", "Kmax", "n_cu", "R", "KP", "RMAX",
     "fast", "FJ", "FR", "FNT", "fast_lds", "mfast", "MR",
     "dense", "DJ", "DNT", "dtrl", "dense_lds", "DG", "DNTM", "DNB", "DTB", "dmarg_lds",
+    "coop", "CG", "CCL", "CR", "CNQ", "coop_lds",
 )
 
 _p = ctypes.c_void_p
