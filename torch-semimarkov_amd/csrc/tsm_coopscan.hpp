@@ -172,6 +172,15 @@ struct CoopChunk {
       const int ci = lj + J * i;
       trr[i] = (ci < C) ? (FWD ? p.trans[(size_t)ci * C + c] : p.trans[(size_t)c * C + ci]) * kLog2e : 0.0f;
     }
+    // duration-bias factors relative to the lane's first duration (as in Chunk::run)
+    float edb[R];
+    bool lane_exact = false;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const double d = dbr[r] - dbr[0];
+      edb[r] = exp2_hw((float)d);
+      lane_exact = lane_exact || (d > 64.0);
+    }
 
     // ---- empty rings ----
     for (int idx = tid; idx < CL * RL; idx += NT) ring[idx] = kInvD;
@@ -278,10 +287,15 @@ struct CoopChunk {
 #pragma unroll
       for (int r = 0; r < R; ++r) e[r] = rb[J * r];
       double y0 = e[0] + dbr[0];
-      float sacc = 1.0f;
+      float s0 = 1.0f, s1 = 0.0f;
 #pragma unroll
-      for (int r = 1; r < R; ++r) sacc += exp2_hw((float)((e[r] + dbr[r]) - y0));
-      if (__ballot(!(sacc <= FLT_MAX))) {
+      for (int r = 1; r < R; ++r) {
+        const float x = exp2_hw((float)(e[r] - e[0]));
+        if (r & 1) s1 = fmaf(x, edb[r], s1);
+        else s0 = fmaf(x, edb[r], s0);
+      }
+      float sacc = s0 + s1;
+      if (__ballot(!(sacc <= FLT_MAX) || lane_exact)) {
         double mx2 = y0;
 #pragma unroll
         for (int r = 1; r < R; ++r) mx2 = fmax(mx2, e[r] + dbr[r]);

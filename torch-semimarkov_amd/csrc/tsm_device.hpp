@@ -73,9 +73,47 @@ __device__ __forceinline__ float group_reduce(float v, Op op) {
   return v;
 }
 
+// max(v, DPP-permuted v) as one v_max_f32 with a DPP source.  fmaxf of a DPP
+// move costs four instructions (old-value fill, move, canonicalising max,
+// max); v_max_f32 already returns the non-NaN operand, as fmaxf does.  The
+// s_nop gives the two wait states a DPP read needs after a VALU write, which
+// the compiler does not track across inline asm.  All lanes must be active
+// (as for every group reduction here).
+template <int CTRL>
+__device__ __forceinline__ float dpp_max(float v) {
+  float r;
+  if constexpr (CTRL == 0xB1) {
+    asm("s_nop 1\n\tv_max_f32_dpp %0, %1, %1 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf bound_ctrl:1"
+        : "=v"(r) : "v"(v));
+  } else if constexpr (CTRL == 0x4E) {
+    asm("s_nop 1\n\tv_max_f32_dpp %0, %1, %1 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf bound_ctrl:1"
+        : "=v"(r) : "v"(v));
+  } else if constexpr (CTRL == 0x141) {
+    asm("s_nop 1\n\tv_max_f32_dpp %0, %1, %1 row_half_mirror row_mask:0xf bank_mask:0xf bound_ctrl:1"
+        : "=v"(r) : "v"(v));
+  } else {
+    static_assert(CTRL == 0x140, "dpp_max: unsupported DPP pattern");
+    asm("s_nop 1\n\tv_max_f32_dpp %0, %1, %1 row_mirror row_mask:0xf bank_mask:0xf bound_ctrl:1"
+        : "=v"(r) : "v"(v));
+  }
+  return r;
+}
+
 template <int G>
 __device__ __forceinline__ float group_max(float v) {
-  return group_reduce<G>(v, OpMax{});
+  if constexpr (G >= 2) v = dpp_max<kDppXor1>(v);
+  if constexpr (G >= 4) v = dpp_max<kDppXor2>(v);
+  if constexpr (G >= 8) v = dpp_max<kDppHalfMirror>(v);
+  if constexpr (G >= 16) v = dpp_max<kDppMirror>(v);
+  if constexpr (G >= 32) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_int(v), __float_as_int(v), false, false);
+    v = fmax2(__int_as_float(r[0]), __int_as_float(r[1]));
+  }
+  if constexpr (G >= 64) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false);
+    v = fmax2(__int_as_float(r[0]), __int_as_float(r[1]));
+  }
+  return v;
 }
 
 template <int G>

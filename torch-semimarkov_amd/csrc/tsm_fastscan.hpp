@@ -119,6 +119,19 @@ struct Chunk {
       // forward mix: own label c is the destination, ci the source; backward: c is the source
       trr[i] = (ci < C) ? (FWD ? p.trans[(size_t)ci * C + c] : p.trans[(size_t)c * C + ci]) * kLog2e : 0.0f;
     }
+    // duration-bias factors relative to the lane's first duration: the pull's term r
+    // is 2^(e[r] - e[0]) * edb[r] = 2^((e[r] + dbr[r]) - (e[0] + dbr[0])), one fp64
+    // subtraction, conversion, exponential and FMA.  Padded durations get 0.  A lane
+    // whose factors span more than 2^64 (an underflowed 2^(e[r]-e[0]) could then
+    // still matter) always takes the exact two-pass path.
+    float edb[R];
+    bool lane_exact = false;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const double d = dbr[r] - dbr[0];
+      edb[r] = exp2_hw((float)d);
+      lane_exact = lane_exact || (d > 64.0);
+    }
 
     // ---- empty rings ----
     for (int idx = tid; idx < C * RL; idx += NT) ring[idx] = kInvD;
@@ -244,10 +257,16 @@ struct Chunk {
       int kbest = 0;
       if constexpr (LOGSR) {
         double y0 = e[0] + dbr[0];
-        float s = 1.0f;
+        float s0 = 1.0f, s1 = 0.0f;
 #pragma unroll
-        for (int r = 1; r < R; ++r) s += exp2_hw((float)((e[r] + dbr[r]) - y0));
-        if (__ballot(!(s <= FLT_MAX))) {
+        for (int r = 1; r < R; ++r) {
+          const float x = exp2_hw((float)(e[r] - e[0]));
+          if (r & 1) s1 = fmaf(x, edb[r], s1);
+          else s0 = fmaf(x, edb[r], s0);
+        }
+        float s = s0 + s1;
+        // overflow (inf, or inf * 0 = NaN on a padded duration) or extreme factors
+        if (__ballot(!(s <= FLT_MAX) || lane_exact)) {
           // a later term exceeds the first by more than the fp32 exponent range
           double m = y0;
 #pragma unroll
