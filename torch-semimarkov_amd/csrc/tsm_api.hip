@@ -98,11 +98,23 @@ void plan_fast(Plan& p, const DeviceInfo& di) {
     const int NT = (int)cdiv((int64_t)p.C * J, 64) * 64;
     if (NT > (R > 16 ? 512 : 1024)) continue;  // the kernels' launch bounds
     const int KP = J * R;
-    const int RS = std::max(p.Kmax + 2, KP + 1);
-    int RL = RS + KP;
-    while (RL % 32 != J % 32) ++RL;  // label rows of a half-wave start on distinct banks
+    const int RS = p.Kmax + 2;  // levels of the positions a step reads (pos % RS)
+    // linear ring of RL > KP entries, compacted every RL - KP steps: about 2*KP+1
+    // entries, fewer when LDS is short (at least 32 steps between compactions).
+    // (Shrinking it further so that two long chunks share a CU was measured at
+    // cfg3: the same steps per CU per second and twice the warm-up share.)
+    // RL % 32 == J % 32 puts the label rows of a half-wave on distinct banks.
+    auto ring_fits = [&](int rl, int per) { return (size_t)per * tsm::fast_lds_layout(p.C, rl, RS).total <= (size_t)di.max_lds; };
+    auto bank_down = [&](int rl) { while (rl > 0 && rl % 32 != J % 32) --rl; return rl; };
+    int RL = bank_down(2 * KP + 1 + 31);
+    if (!ring_fits(RL, 1)) {
+      int hi = RL;
+      while (hi > KP && !ring_fits(hi, 1)) --hi;
+      hi = bank_down(hi);
+      if (hi < KP + 33) continue;
+      RL = hi;
+    }
     const size_t lds = tsm::fast_lds_layout(p.C, RL, RS).total;
-    if (lds > (size_t)di.max_lds) continue;
     const double cost = (double)((NT / 64 + 3) / 4) * (R + 12);  // waves per SIMD x work per wave
     if (cost < best) {
       best = cost;

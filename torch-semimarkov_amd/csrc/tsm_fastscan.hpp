@@ -9,6 +9,11 @@
 //     durations are masked through the duration bias register);
 //   * the ring of label c holds, per position s, one fp64 value
 //       x[s] = lvl[s] + v[s] - sgn*cum[s,c]*log2(e)
+//     in a linear buffer of RL > KP entries: each step's position sits one index
+//     below the previous one, so a step's KP reads are contiguous, and when the
+//     index would drop below 0 the group copies its KP newest entries to the top
+//     (once every RL - KP steps) -- half the LDS of a mirrored ring, so more
+//     chunks share a CU;
 //     (v = normalised state plus the projection a segment starting / ending at
 //     s contributes, lvl = the position's fp64 level), so the term of duration
 //     k at step t is x[s] + db[k] + sgn*cum[t,c]*log2(e) with s = t -/+ k;
@@ -43,16 +48,6 @@ __device__ __forceinline__ void lds_barrier() { __asm__ volatile("s_waitcnt lgkm
 // Compiler-only ordering point between a wave's LDS writes and its later reads
 // of the same words by other lanes (LDS executes a wave's operations in order).
 __device__ __forceinline__ void wave_lds_order() { __asm__ volatile("" ::: "memory"); }
-
-template <bool FWD>
-__device__ __forceinline__ int slot_of(int pos, int RS) {
-  return FWD ? RS - 1 - pos % RS : pos % RS;
-}
-
-__device__ __forceinline__ void ring_put(double* ring_c, int a, double x, int RS, int KP) {
-  ring_c[a] = x;
-  if (a < KP) ring_c[a + RS] = x;
-}
 
 template <int J, int R, bool FWD, bool LOGSR>
 struct Chunk {
@@ -139,6 +134,8 @@ struct Chunk {
     __syncthreads();
 
     double* rc = ring + (size_t)c * RL;
+    // position t_start at index A0, the positions behind it at A0 + i
+    const int A0 = RL - KP;
     double lvl_prev;
     // ---- initial state ----
     if (mode == 0) {
@@ -188,7 +185,7 @@ struct Chunk {
         if (cval && lj == 0 && store) p.val[((size_t)b * (T + 1) + len) * C + c] = 0.0f;
         if (tid == 0 && store) p.lvl[(size_t)b * (T + 1) + len] = 0.0;
       }
-      if (cval && lj == 0) ring_put(rc, slot_of<FWD>(pos, RS), (double)v0 - cumx(pos), RS, KP);
+      if (cval && lj == 0) rc[A0] = (double)v0 - cumx(pos);
       if (tid == 0) lring[pos % RS] = 0.0;
     } else {
       lvl_prev = (mode == 1) ? 0.0 : init_lv[0];
@@ -204,7 +201,7 @@ struct Chunk {
             v = init_st[(size_t)i * C + c];
           }
           const double lv = (mode == 1) ? 0.0 : init_lv[i];
-          ring_put(rc, slot_of<FWD>(pos, RS), lv + (double)v - cumx(pos), RS, KP);
+          rc[A0 + i] = lv + (double)v - cumx(pos);
         }
       }
       for (int i = tid; i < Kmax; i += NT) {
@@ -236,7 +233,22 @@ struct Chunk {
     const int rec_spec = (mode == 1) ? (FWD ? t_lo : t_hi) : -1;
     const int rec_end = FWD ? ((t_hi < len) ? t_hi : -1) : ((j >= 1) ? t_lo : -1);
 
+    int A = A0;  // ring index of the current position
     for (int t = t_first; t != t_end; t += dir) {
+      if (--A < 0) {
+        // the KP newest entries (indices 0 .. KP-1) to the top; each label group
+        // copies its own ring inside its wavefront (LDS keeps a wave's order)
+        if (cval) {
+          double cp[R];
+#pragma unroll
+          for (int r = 0; r < R; ++r) cp[r] = rc[lj + J * r];
+          wave_lds_order();
+#pragma unroll
+          for (int r = 0; r < R; ++r) rc[A0 + lj + J * r] = cp[r];
+          wave_lds_order();
+        }
+        A = A0 - 1;
+      }
       const double cx_t = sgn * (double)cum_n * kLog2eD;
       const float pa_t = pa_n * ((FWD ? t >= 1 : true) ? pa_scale : 0.0f);
       const float pb_t = pb_n * ((FWD ? true : t >= 1) ? pb_scale : 0.0f);
@@ -246,7 +258,6 @@ struct Chunk {
         pa_n = pa_src[(size_t)pa_row(tn) * C + c];
         pb_n = pb_src[(size_t)pb_row(tn) * C + c];
       }
-      const int A = slot_of<FWD>(t, RS);
 
       // ---- pull over the lane's durations ----
       const double* rb = rc + A + 1 + lj;
@@ -357,7 +368,7 @@ struct Chunk {
         if (tid == 0 && store && owned) p.lvl[(size_t)b * (T + 1) + t] = lvl_t;
       }
       // ---- ring entry for position t ----
-      if (cval && lj == 0) ring_put(rc, A, (lvl_t + (double)(mixv + pb_t)) - cx_t, RS, KP);
+      if (cval && lj == 0) rc[A] = (lvl_t + (double)(mixv + pb_t)) - cx_t;
       if (tid == 0) lring[t % RS] = lvl_t;
       lvl_prev = lvl_t;
       wave_lds_order();

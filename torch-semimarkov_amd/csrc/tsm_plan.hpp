@@ -27,7 +27,7 @@ struct Plan {
   int has_ps, has_pe;
   // register-resident log-semiring scan ("fast" path), used when fast == 1:
   // FJ lanes per label, FR durations per lane (compile-time), FNT threads,
-  // FRS ring slots, FRL ring row length (float2 elements), fast_lds bytes
+  // FRS level slots, FRL ring length per label (fp64 entries), fast_lds bytes
   int fast, FJ, FR, FNT, FRS, FRL;
   size_t fast_lds;
   // register-resident marginal kernel (mfast == 1): 16 lanes per label, MR
@@ -134,9 +134,11 @@ __host__ __device__ inline DenseMargLds dense_marg_lds_layout(int C, int Kmax, i
 }
 
 // ---- fast scan LDS layout ---------------------------------------------------
-// One ring per label of RL fp64 entries: slot s < RS plus a mirror of slots
-// s < KP at s + RS.  Entry = level + normalised state (+ folded projection)
-// - sgn * cumulative score, all in log2 units.
+// One linear ring per label of RL > KP fp64 entries (the current position one
+// index below the previous one, the KP newest entries copied to the top when
+// the index runs out), and the levels of the last RS positions (pos % RS).
+// Entry = level + normalised state (+ folded projection) - sgn * cumulative
+// score, all in log2 units.
 struct FastLds {
   size_t ring;   // double[C*RL]
   size_t lring;  // double[RS]   per-position levels
