@@ -144,15 +144,19 @@ void plan_coop(Plan& p, const DeviceInfo& di) {
   R = (R + 7) / 8 * 8;
   if (R > 32) return;
   const int KP = J * R;
-  const int RS = std::max(p.Kmax + 2, KP + 1);
-  int RL = RS + KP;
-  while (RL % 32 != J % 32) ++RL;
+  const int RS = p.Kmax + 2;  // levels of the positions a step reads (pos % RS)
+  auto bank_down = [&](int rl) { while (rl > 0 && rl % 32 != J % 32) --rl; return rl; };
   for (int G : {2, 4, 8, 16}) {
     const int CL = (p.C + G - 1) / G;
     // the instances' launch bounds (tsm_coopscan.hpp), and every member owns a label
     if (CL * J > (R > 16 ? 256 : 512) || CL * (G - 1) >= p.C) continue;
+    // linear ring (as the single-block scan's): up to 2*KP+1 entries, at least
+    // 32 steps between compactions
+    int RL = bank_down(2 * KP + 1 + 31);
+    while (RL > KP && tsm::coop_lds_layout(CL, p.C, RL, RS).total > (size_t)di.max_lds) --RL;
+    RL = bank_down(RL);
+    if (RL < KP + 33) continue;
     const size_t lds = tsm::coop_lds_layout(CL, p.C, RL, RS).total;
-    if (lds > (size_t)di.max_lds) continue;
     const int NQ = di.n_cu / G;
     if (NQ < 1) continue;
     p.coop = 1;

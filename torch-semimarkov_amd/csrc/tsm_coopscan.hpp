@@ -45,16 +45,6 @@ constexpr int kSpinLimit = 1 << 22;  // polls of one word before giving up (seco
 __device__ __forceinline__ void lds_barrier() { __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 __device__ __forceinline__ void wave_lds_order() { __asm__ volatile("" ::: "memory"); }
 
-template <bool FWD>
-__device__ __forceinline__ int slot_of(int pos, int RS) {
-  return FWD ? RS - 1 - pos % RS : pos % RS;
-}
-
-__device__ __forceinline__ void ring_put(double* ring_c, int a, double x, int RS, int KP) {
-  ring_c[a] = x;
-  if (a < KP) ring_c[a + RS] = x;
-}
-
 // Group and member of a block.  xmap: members share blockIdx % 8.
 struct Member {
   int q, m;
@@ -189,6 +179,8 @@ struct CoopChunk {
     __syncthreads();
 
     double* rc = ring + (size_t)gl * RL;
+    // linear ring as in Chunk::run: position t_start at A0, compaction to the top
+    const int A0 = RL - KP;
     double lvl_prev;
     // ---- initial state ----
     if (mode == 0) {
@@ -225,7 +217,7 @@ struct CoopChunk {
         if (cval && lj == 0 && store) p.val[((size_t)b * (T + 1) + len) * C + c] = 0.0f;
         if (lead && tid == 0 && store) p.lvl[(size_t)b * (T + 1) + len] = 0.0;
       }
-      if (cval && lj == 0) ring_put(rc, slot_of<FWD>(pos, RS), (double)v0 - cumx(pos), RS, KP);
+      if (cval && lj == 0) rc[A0] = (double)v0 - cumx(pos);
       if (tid == 0) lring[pos % RS] = 0.0;
     } else {
       lvl_prev = (mode == 1) ? 0.0 : init_lv[0];
@@ -240,7 +232,7 @@ struct CoopChunk {
             v = init_st[(size_t)i * C + c];
           }
           const double lv = (mode == 1) ? 0.0 : init_lv[i];
-          ring_put(rc, slot_of<FWD>(pos, RS), lv + (double)v - cumx(pos), RS, KP);
+          rc[A0 + i] = lv + (double)v - cumx(pos);
         }
       }
       for (int i = tid; i < Kmax; i += NT) {
@@ -269,7 +261,20 @@ struct CoopChunk {
     const int rec_spec = (mode == 1) ? (FWD ? t_lo : t_hi) : -1;
     const int rec_end = FWD ? ((t_hi < len) ? t_hi : -1) : ((j >= 1) ? t_lo : -1);
 
+    int A = A0;  // ring index of the current position
     for (int t = t_first; t != t_end; t += dir) {
+      if (--A < 0) {
+        if (cval) {
+          double cp[R];
+#pragma unroll
+          for (int r = 0; r < R; ++r) cp[r] = rc[lj + J * r];
+          wave_lds_order();
+#pragma unroll
+          for (int r = 0; r < R; ++r) rc[A0 + lj + J * r] = cp[r];
+          wave_lds_order();
+        }
+        A = A0 - 1;
+      }
       const double cx_t = sgn * (double)cum_n * kLog2eD;
       const float pa_t = pa_n * ((FWD ? t >= 1 : true) ? pa_scale : 0.0f);
       const float pb_t = pb_n * ((FWD ? true : t >= 1) ? pb_scale : 0.0f);
@@ -279,7 +284,6 @@ struct CoopChunk {
         pa_n = pa_src[(size_t)pa_row(tn) * C + c];
         pb_n = pb_src[(size_t)pb_row(tn) * C + c];
       }
-      const int A = slot_of<FWD>(t, RS);
 
       // ---- pull over the lane's durations (own labels) ----
       const double* rb = rc + A + 1 + lj;
@@ -354,7 +358,7 @@ struct CoopChunk {
         if (lead && tid == 0 && store && owned) p.lvl[(size_t)b * (T + 1) + t] = lvl_t;
       }
       // ---- ring entry for position t ----
-      if (cval && lj == 0) ring_put(rc, A, (lvl_t + (double)(mixv + pb_t)) - cx_t, RS, KP);
+      if (cval && lj == 0) rc[A] = (lvl_t + (double)(mixv + pb_t)) - cx_t;
       if (tid == 0) lring[t % RS] = lvl_t;
       lvl_prev = lvl_t;
       wave_lds_order();

@@ -159,7 +159,7 @@ __host__ __device__ inline FastLds fast_lds_layout(int C, int RL, int RS) {
 }
 
 // ---- cooperative scan LDS layout (one member of a group) -------------------
-// Rings of the member's CL labels (mirrored like the fast scan's), per-position
+// Linear rings of the member's CL labels (compacted like the fast scan's), per-position
 // levels, the double-buffered row of all C labels, block reductions and the
 // give-up flag.
 struct CoopLds {
