@@ -49,6 +49,18 @@ __device__ __forceinline__ int mlen(const int64_t* lengths, int b, int T) {
 
 constexpr int kDppRowRor15 = 0x12F;  // row_ror:15 -- lane i reads lane (i+1) mod 16 of its row
 
+// a + (rot of lane (i+1) mod 16 of the row), one v_add_f32 with a DPP source.
+// The compiler does not fuse the rotation into the add here (it hoists the DPP
+// move away from it), which costs two more instructions per end sum.  The
+// s_nop gives the two wait states a DPP read needs after a VALU write, which
+// the compiler does not track across inline asm.  All lanes are active.
+__device__ __forceinline__ float add_row_ror15(float rot, float a) {
+  float r;
+  asm("s_nop 1\n\tv_add_f32_dpp %0, %1, %2 row_ror:15 row_mask:0xf bank_mask:0xf bound_ctrl:1"
+      : "=v"(r) : "v"(rot), "v"(a));
+  return r;
+}
+
 // CJ source labels per lane in the label mix (C <= CJ * J); the batch's alpha-hat
 // rows (J * C floats) are staged with 4 * CJ loads per lane.
 template <int J, int R, int CJ>
@@ -165,6 +177,7 @@ __global__ void __launch_bounds__(64) margfast_kernel(MargParams q) {
   float d32[R];
   double d64[R];
   float ea[R];  // running end sums of positions t+1+lj+16r (this block's starts)
+  const int lane0 = (lj == 0) ? -1 : 0;  // all bits set on the row's lane 0
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     d32[r] = 0.0f;
@@ -231,13 +244,26 @@ __global__ void __launch_bounds__(64) margfast_kernel(MargParams q) {
 #pragma unroll
     for (int r = 0; r < R; ++r) xv[r] = xb[J * r];
     float sp0 = 0.0f, sp1 = 0.0f;
+    float pr[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const float P = exp2_hw((float)((xv[r] + dbr[r]) + At));
+      pr[r] = P;
       d32[r] += P;
-      ea[r] += P;
       if (r & 1) sp1 += P;
       else sp0 += P;
+    }
+    // the previous step's end sums slide to positions t+1+lj+16r: lane 0 takes its
+    // next register (dropping the row it flushed), then the row rotates one lane
+    // down (lane j takes lane j+1), fused with the accumulation.  Ascending r
+    // reads ea[r+1] before it is updated.
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      // a bitwise merge: a select between ea[r + 1] and ea[r] would be turned
+      // into one register-array read at a lane-dependent index
+      const float nxt = (r + 1 < R) ? ea[r + 1] : 0.0f;
+      const float sl = __int_as_float((__float_as_int(nxt) & lane0) | (__float_as_int(ea[r]) & ~lane0));
+      ea[r] = add_row_ror15(sl, pr[r]);
     }
     const float St = group_sum<J>(sp0 + sp1);
     // ---- transition gradient: softmax weight of each source label times S[t,c] ----
@@ -251,15 +277,6 @@ __global__ void __launch_bounds__(64) margfast_kernel(MargParams q) {
       if (p < own_hi) e_own_b[(size_t)p * C + c] = ea[0];
       else halo_b[(size_t)(p - own_hi) * C + c] = ea[0];
     }
-    // slide the end sums to positions t+2+lj+16r: lane 0 takes its next register
-    // (dropping the flushed row), then each register rotates one lane down the row
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const float nxt = (r + 1 < R) ? ea[r + 1] : 0.0f;
-      ea[r] = (lj == 0) ? nxt : ea[r];
-    }
-#pragma unroll
-    for (int r = 0; r < R; ++r) ea[r] = dpp_f<kDppRowRor15>(ea[r]);
     if (((t - t0) & 63) == 63) {
 #pragma unroll
       for (int r = 0; r < R; ++r) {
@@ -274,6 +291,11 @@ __global__ void __launch_bounds__(64) margfast_kernel(MargParams q) {
     }
   }
   // ---- pending end rows t1+1 .. t1+Kmax-1 (partial sums from this block's starts) ----
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const float nxt = (r + 1 < R) ? ea[r + 1] : 0.0f;
+    ea[r] = dpp_f<kDppRowRor15>(__int_as_float((__float_as_int(nxt) & lane0) | (__float_as_int(ea[r]) & ~lane0)));
+  }
   if (cval) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
