@@ -71,9 +71,16 @@ __global__ void __launch_bounds__(64) margfast_kernel(MargParams q) {
   extern __shared__ __align__(16) char smem[];
   constexpr int KP = J * R;
   constexpr int CB = 64 / J;
-  const int cbk = blockIdx.x % q.NCB;
-  const int blk = (blockIdx.x / q.NCB) % q.NB;
-  const int b = blockIdx.x / (q.NCB * q.NB);
+  // The NCB label blocks of one position block read the same alpha-hat rows:
+  // they take block ids with equal blockIdx % 8, which the dispatcher places on
+  // one XCD (one L2), and follow each other there.  The grid is padded to whole
+  // groups of 8 position blocks; padding blocks do nothing.
+  const int xcd = blockIdx.x & 7, w = blockIdx.x >> 3;
+  const int cbk = w % q.NCB;
+  const int pb = (w / q.NCB) * 8 + xcd;
+  if (pb >= q.B * q.NB) return;
+  const int blk = pb % q.NB;
+  const int b = pb / q.NB;
   const int C = q.C, Kmax = q.Kmax, K = q.K, T = q.T, RS = q.RS, RL = q.RL;
   const int lane = threadIdx.x, g = lane / J, lj = lane % J;
   const int c_raw = cbk * CB + g;
@@ -327,7 +334,8 @@ int launch_margfast_jr(const Plan& pl, const MargParams& q, hipStream_t st) {
   hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)pl.marg_lds);
   if (e != hipSuccess) return e;
   TimedLaunch tl(kKMarginal, st);
-  hipLaunchKernelGGL(k, dim3(pl.B * pl.NB * pl.NCB), dim3(64), pl.marg_lds, st, q);
+  const int npb = (pl.B * pl.NB + 7) / 8 * 8;  // position blocks, padded to groups of 8
+  hipLaunchKernelGGL(k, dim3(npb * pl.NCB), dim3(64), pl.marg_lds, st, q);
   return hipGetLastError();
 }
 
