@@ -63,7 +63,7 @@ const char* tsm_last_error(void);
  * `n` int64 host values: J, NT, RS, P, Lc, W, global_rings, scan_lds, NB, TB,
  * CB, NCB, JM, NTM, marg_lds, Kmax, n_cu, R, KP, RMAX, fast, FJ, FR, FNT,
  * fast_lds, mfast, MR, dense, DJ, DNT, dtrl, dense_lds, DG, DNTM, DNB, DTB,
- * dmarg_lds, coop, CG, CCL, CR, CNQ, coop_lds (fast = 1: log-semiring scans use
+ * dmarg_lds, coop, CG, CCL, CR, CNQ, coop_lds, mfused, GNB, GTB (fast = 1: log-semiring scans use
  * the register-resident kernels with
  * FJ lanes per label and FR durations per lane; mfast = 1: the marginals use
  * the register-resident kernel with MR durations per lane; the environment
@@ -71,7 +71,10 @@ const char* tsm_last_error(void);
  * transitions, dense scans with DJ lanes per label, transitions in LDS when
  * dtrl = 1, dense marginals in DNB blocks of DTB positions; coop = 1: rings too
  * large for one CU, log-semiring scans run on groups of CG cooperating blocks
- * with CCL labels each and CR durations per lane, CNQ co-resident groups).
+ * with CCL labels each and CR durations per lane, CNQ co-resident groups;
+ * mfused = 1: the log-semiring backward computes the segment marginals inside
+ * the register-resident beta scan, transition gradient in GNB row blocks of GTB
+ * starts per sequence; TSM_MARGINAL_PATH=separate turns it off).
  */
 int tsm_plan_info(int64_t B, int64_t T, int64_t C, int64_t K, int64_t trans_rows, int has_proj_start,
                   int has_proj_end, int64_t* out, int n);

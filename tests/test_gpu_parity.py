@@ -418,6 +418,109 @@ def test_deterministic_bitwise(scan_path):
         assert torch.equal(x, y)
 
 
+# Backward with the segment marginals fused into the 16-lane register-resident
+# beta scan: plans with 16-lane groups (more than 32 labels, or more than 256
+# durations).  Each chunk accumulates in its own frame; the finalize rescales.
+FUSED_CASES = [
+    # B, T, K, C, lengths, proj
+    (2, 3000, 40, 40, [3000, 2211], False),       # several speculative chunks, ragged
+    (1, 4000, 120, 36, None, True),                # projections
+    (3, 1500, 300, 24, [1500, 650, 299], False),   # the headline's lane layout (19 durations per lane)
+    (2, 6000, 280, 12, [6000, 4117], True),        # long durations, few labels, projections
+    (1, 1800, 64, 64, None, False),                # 64 labels: 4096 transition pairs
+    (2, 2080, 33, 48, [2080, 1040], False),        # lengths that are multiples of the chunk length
+]
+
+
+def _fused_plan(B, T, C, K, proj):
+    info = N.plan_info(B, T, C, K, proj, proj)
+    assert info["mfused"] == 1 and info["FJ"] == 16, info
+    return info
+
+
+@pytest.mark.parametrize("B,T,K,C,lengths,proj", FUSED_CASES)
+def test_fused_backward_vs_fp64_oracle(B, T, K, C, lengths, proj, monkeypatch):
+    monkeypatch.delenv("TSM_SCAN_PATH", raising=False)
+    monkeypatch.delenv("TSM_MARGINAL_PATH", raising=False)
+    _fused_plan(B, T, C, K, proj)
+    cum, tr, db, L, ps, pe = rand_problem(B, T, K, C, 5000 + T + K + C, lengths, proj)
+    g = torch.linspace(0.5, 2.0, B)
+    p64, g64 = oracle_fp64(cum, tr, db, L, K, "log", ps, pe, g)
+    part, grads = run_hip(cum, tr, db, L, K, "log", ps, pe, g)
+    np.testing.assert_allclose(part.double().numpy(), p64.numpy(), rtol=RTOL_Z)
+    assert_grads(grads, g64)
+
+
+def _ops_backward(cum, tr, db, L, K, ps=None, pe=None, g=None):
+    """forward (storing alpha) + backward through the custom ops: grads and the
+    backward's recomputed-chunk counts."""
+    cum, tr, db, ps, pe = to_dev(cum, tr, db, ps, pe)
+    Ld = L.to(DEV)
+    with torch.no_grad():
+        part, z2, ah, al, _ = ops.scan_forward(cum, tr, db, Ld, K, 0, ps, pe, True)
+        gw = torch.ones_like(part) if g is None else g.to(DEV)
+        gc, gt, gd, gps, gpe, rec = ops.scan_backward(cum, tr, db, Ld, K, 0, ps, pe, ah, al, z2, gw)
+    return [x.cpu() for x in (gc, gt, gd, gps, gpe)], rec.cpu()
+
+
+def test_fused_backward_recomputes_non_mixing_chunks(monkeypatch):
+    """Sticky transitions and evidence at the sequence end: the beta states of
+    the speculative chunks disagree with the exact ones, chunks are recomputed
+    (in parallel, then sequentially from the neighbour's state) and their fused
+    marginals recomputed with them; gradients still match the oracle."""
+    monkeypatch.delenv("TSM_SCAN_PATH", raising=False)
+    monkeypatch.delenv("TSM_MARGINAL_PATH", raising=False)
+    B, T, K, C = 1, 6000, 300, 20
+    _fused_plan(B, T, C, K, False)
+    g = torch.Generator().manual_seed(15)
+    em = 0.01 * torch.randn(B, T, C, generator=g)
+    em[:, -50:, 0] += 2.0
+    cum = torch.zeros(B, T + 1, C)
+    cum[:, 1:] = em.cumsum(1)
+    tr = torch.full((C, C), -40.0)
+    tr.fill_diagonal_(0.0)
+    db = torch.zeros(K, C)
+    L = torch.tensor([T])
+    _, rec = _ops_backward(cum, tr, db, L, K)
+    assert int(rec.sum()) > 0
+    p64, g64 = oracle_fp64(cum, tr, db, L, K)
+    part, grads = run_hip(cum, tr, db, L, K)
+    np.testing.assert_allclose(part.double().numpy(), p64.numpy(), rtol=RTOL_Z)
+    assert_grads(grads, g64)
+
+
+def test_fused_backward_full_size_config3(monkeypatch):
+    """The headline configuration (B=1, T=10^6, C=24, K=300): the fused backward
+    against the separate marginal kernel (itself checked against the oracle
+    above), and the size-independent identities of the gradients: every
+    segment has one duration and one incoming transition (sum grad_db = sum
+    grad_transition = expected segment count) and one start and one end
+    (grad_cum sums to zero)."""
+    monkeypatch.delenv("TSM_SCAN_PATH", raising=False)
+    B, T, C, K = 1, 1_000_000, 24, 300
+    g = torch.Generator().manual_seed(20261203)
+    em = torch.randn(B, T, C, generator=g)
+    tr = 0.1 * torch.randn(C, C, generator=g)
+    db = torch.zeros(K, C)
+    db[1:] = -0.01 * torch.arange(1, K, dtype=torch.float32).unsqueeze(1) + 0.05 * torch.randn(K - 1, C, generator=g)
+    cum = torch.zeros(B, T + 1, C)
+    cum[:, 1:] = torch.cumsum(em, dim=1)
+    L = torch.full((B,), T, dtype=torch.long)
+    monkeypatch.delenv("TSM_MARGINAL_PATH", raising=False)
+    _fused_plan(B, T, C, K, False)
+    fused, _ = _ops_backward(cum, tr, db, L, K)
+    monkeypatch.setenv("TSM_MARGINAL_PATH", "separate")
+    assert N.plan_info(B, T, C, K)["mfused"] == 0
+    sep, _ = _ops_backward(cum, tr, db, L, K)
+    for a, b in zip(fused[:3], sep[:3]):
+        np.testing.assert_allclose(a.double().numpy(), b.double().numpy(), **GRAD_TOL)
+    gc, gt, gd = (x.double() for x in fused[:3])
+    n_seg = gd.sum()
+    assert 1000 < n_seg < T
+    assert abs(gt.sum() - n_seg) <= 1e-5 * n_seg
+    assert abs(gc.sum()) <= 1e-5 * gc.abs().sum()
+
+
 def test_k1_full_size_config2_vs_hmm(scan_path):
     """Config 2 of the benchmark set (B=32, T=10^4, C=8, K=1) against a probability-space HMM in fp64."""
     B, T, C, K = 32, 10_000, 8, 1

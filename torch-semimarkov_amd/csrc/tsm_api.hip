@@ -383,6 +383,19 @@ int make_plan(int64_t B, int64_t T, int64_t C, int64_t K, int has_ps, int has_pe
       p.TB = (int)tbm;
     }
   }
+  // marginals fused into the backward scan: the register-resident scan with
+  // 16-lane groups (TSM_MARGINAL_PATH=separate keeps the separate kernel)
+  p.mfused = 0;
+  const char* menv = getenv("TSM_MARGINAL_PATH");
+  const bool separate = menv != nullptr && strcmp(menv, "separate") == 0;
+  if (!separate && p.fast && p.FJ == 16 && p.C * p.C <= 4096) {
+    p.mfused = 1;
+    // transition gradient: about two blocks per CU, at least 256 starts each
+    int64_t gnb = cdiv(2 * (int64_t)di.n_cu, (int64_t)p.B);
+    gnb = std::max<int64_t>(1, std::min<int64_t>(gnb, cdiv(T, 256)));
+    p.GTB = (int)cdiv(T, gnb);
+    p.GNB = (int)cdiv(T, p.GTB);
+  }
   *out = p;
   return TSM_OK;
 }
@@ -504,19 +517,58 @@ size_t forward_ws_bytes(const Plan& pl) {
   return cv.off + 256;
 }
 
+// Backward workspace.  Separate marginals: the beta table, the scan workspace,
+// end / start sums and the marginal kernel's block partials.  Fused marginals
+// (mfused): u, the scan workspace, end / start sums, and per backward chunk the
+// halo rows, duration sums and frame estimate; transition partials per row block.
+struct BwdWs {
+  float *bval = nullptr, *uval = nullptr, *e_own, *s_out, *halo;
+  double *blvl = nullptr, *db_part, *tr_part, *mframe = nullptr;
+  ScanWs scan;
+  DenseTr dt;
+};
+
+BwdWs carve_backward(Carver& cv, const Plan& pl) {
+  BwdWs w;
+  const size_t rows = (size_t)pl.B * (pl.T + 1);
+  if (pl.mfused) {
+    const size_t items = (size_t)pl.B * pl.P;
+    w.uval = cv.take<float>(rows * pl.C);
+    w.scan = carve_scan(cv, pl);
+    w.e_own = cv.take<float>(rows * pl.C);
+    w.s_out = cv.take<float>(rows * pl.C);
+    w.halo = cv.take<float>(items * pl.Kmax * pl.C);
+    w.db_part = cv.take<double>(items * pl.Kmax * pl.C);
+    w.mframe = cv.take<double>(items);
+    w.tr_part = cv.take<double>((size_t)pl.B * pl.GNB * pl.C * pl.C);
+  } else {
+    w.bval = cv.take<float>(rows * pl.C);
+    w.blvl = cv.take<double>(rows);
+    w.scan = carve_scan(cv, pl);
+    w.e_own = cv.take<float>(rows * pl.C);
+    w.s_out = cv.take<float>(rows * pl.C);
+    w.halo = cv.take<float>((size_t)pl.B * marg_nb(pl) * pl.Kmax * pl.C);
+    w.db_part = cv.take<double>((size_t)pl.B * marg_nb(pl) * pl.Kmax * pl.C);
+    w.tr_part = cv.take<double>(tr_part_len(pl));
+  }
+  w.dt = carve_dense(cv, pl);
+  return w;
+}
+
+// (with fused marginals, also enough for the separate layout that a
+// max-semiring backward uses)
 size_t backward_ws_bytes(const Plan& pl) {
   Carver cv(nullptr);
-  const size_t rows = (size_t)pl.B * (pl.T + 1);
-  cv.take<float>(rows * pl.C);   // beta-hat
-  cv.take<double>(rows);         // beta levels
-  carve_scan(cv, pl);
-  cv.take<float>(rows * pl.C);   // e_own
-  cv.take<float>(rows * pl.C);   // s_out
-  cv.take<float>((size_t)pl.B * marg_nb(pl) * pl.Kmax * pl.C);   // halo
-  cv.take<double>((size_t)pl.B * marg_nb(pl) * pl.Kmax * pl.C);  // db_part
-  cv.take<double>(tr_part_len(pl));                              // tr_part
-  carve_dense(cv, pl);
-  return cv.off + 256;
+  carve_backward(cv, pl);
+  size_t n = cv.off;
+  if (pl.mfused) {
+    Plan q = pl;
+    q.mfused = 0;
+    Carver cs(nullptr);
+    carve_backward(cs, q);
+    n = std::max(n, cs.off);
+  }
+  return n + 256;
 }
 
 // Viterbi workspace: backpointers, final labels, and the scan workspace of the
@@ -615,7 +667,8 @@ int tsm_plan_info(int64_t B, int64_t T, int64_t C, int64_t K, int64_t trans_rows
                           p.CB, p.NCB, p.JM, p.NTM, (int64_t)p.marg_lds, p.Kmax, di.n_cu, p.R, p.KP, p.RMAX,
                           p.fast, p.FJ, p.FR, p.FNT, (int64_t)p.fast_lds, p.mfast, p.MR,
                           p.dense, p.DJ, p.DNT, p.dtrl, (int64_t)p.dense_lds, p.DG, p.DNTM, p.DNB, p.DTB,
-                          (int64_t)p.dmarg_lds, p.coop, p.CG, p.CCL, p.CR, p.CNQ, (int64_t)p.coop_lds};
+                          (int64_t)p.dmarg_lds, p.coop, p.CG, p.CCL, p.CR, p.CNQ, (int64_t)p.coop_lds,
+                          p.mfused, p.GNB, p.GTB};
   const int m = (int)(sizeof(vals) / sizeof(vals[0]));
   for (int i = 0; i < n && i < m; ++i) out[i] = vals[i];
   return TSM_OK;
@@ -696,19 +749,69 @@ int tsm_backward(const float* cum, const float* tr, const float* db, const int64
   if (!workspace || ws_bytes < need)
     return fail(TSM_ERR_WORKSPACE, "backward workspace too small: %zu < %zu bytes", ws_bytes, need);
   hipStream_t st = (hipStream_t)stream;
+  if (semiring != TSM_SEMIRING_LOG) pl.mfused = 0;  // max semiring: the separate marginals
   Carver cv(workspace);
-  const size_t rows = (size_t)pl.B * (pl.T + 1);
-  float* bval = cv.take<float>(rows * pl.C);
-  double* blvl = cv.take<double>(rows);
-  ScanWs w = carve_scan(cv, pl);
-  float* e_own = cv.take<float>(rows * pl.C);
-  float* s_out = cv.take<float>(rows * pl.C);
-  float* halo = cv.take<float>((size_t)pl.B * marg_nb(pl) * pl.Kmax * pl.C);
-  double* db_part = cv.take<double>((size_t)pl.B * marg_nb(pl) * pl.Kmax * pl.C);
-  double* tr_part = cv.take<double>(tr_part_len(pl));
-  const DenseTr dt = carve_dense(cv, pl);
+  const BwdWs bw = carve_backward(cv, pl);
+  const ScanWs& w = bw.scan;
+  const DenseTr& dt = bw.dt;
+  float* bval = bw.bval;
+  double* blvl = bw.blvl;
+  float* e_own = bw.e_own;
+  float* s_out = bw.s_out;
+  float* halo = bw.halo;
+  double* db_part = bw.db_part;
+  double* tr_part = bw.tr_part;
 
   tsm::ScanParams p = scan_params(pl, w, cum, tr, db, len, ps, pe);
+  if (pl.mfused) {
+    tsm::FusedParams f{};
+    f.lengths = len;
+    f.trans = tr;
+    f.aval = alpha_hat;
+    f.uval = bw.uval;
+    f.B = pl.B;
+    f.T = pl.T;
+    f.C = pl.C;
+    f.K = pl.K;
+    f.Kmax = pl.Kmax;
+    f.P = pl.P;
+    f.Lc = pl.Lc;
+    f.GNB = pl.GNB;
+    f.GTB = pl.GTB;
+    f.offs = w.offs;
+    f.mframe = bw.mframe;
+    f.e_own = e_own;
+    f.s_out = s_out;
+    f.halo = halo;
+    f.db_part = db_part;
+    f.tr_part = tr_part;
+    f.grad_output = grad_output;
+    f.grad_cum = grad_cum;
+    f.grad_ps = grad_ps;
+    f.grad_pe = grad_pe;
+    f.grad_tr = grad_tr;
+    f.grad_db = grad_db;
+    int e = tsm::launch_u_rows(pl, f, st);
+    if (e != hipSuccess) return hip_fail(e, "tsm_backward (u rows)");
+    p.val = nullptr;
+    p.lvl = nullptr;
+    p.zout = nullptr;
+    p.recomputed = recomputed;
+    p.uval = bw.uval;
+    p.aval = alpha_hat;
+    p.alvl = alpha_level;
+    p.mz2 = log2_partition;
+    p.e_own = e_own;
+    p.s_out = s_out;
+    p.halo = halo;
+    p.db_part = db_part;
+    p.mframe = bw.mframe;
+    e = tsm::launch_scan_backward_fused(pl, p, st);
+    if (e != hipSuccess) return hip_fail(e, "tsm_backward (beta scan with marginals)");
+    e = tsm::launch_fused_finalize(pl, f, st);
+    if (e != hipSuccess) return hip_fail(e, "tsm_backward (finalize)");
+    return TSM_OK;
+  }
   if (pl.dense) {
     const int e = tsm::launch_dense_prep(pl, tr, dt.trf, dt.trb, st);
     if (e != hipSuccess) return hip_fail(e, "tsm_backward (transition tables)");

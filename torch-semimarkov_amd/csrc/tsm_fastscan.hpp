@@ -26,6 +26,16 @@
 //     row of all labels' results: one LDS barrier per step.
 //
 // sgn = +1 forward (content cum[t]-cum[t-k]), -1 backward (cum[t+k]-cum[t]).
+//
+// MARG (backward, log semiring, 16-lane groups): the beta scan also produces the
+// segment marginals of the starts it owns.  The pull's term r of label c at
+// step t is 2^(x[t+k] + db[k] - y0); times F = 2^(y0 + A[t,c]), with A the
+// forward side of a segment starting at t (alpha level + u[t,c] + proj_start
+// - cum[t,c] - log2 Z), it is P(t,k,c).  So each term costs three more
+// multiplies/adds: the duration sums D[k,c] (per-lane registers), and the end
+// sums E[t+k,c] (per-lane registers that slide one lane up the 16-lane DPP row
+// each step, fused into the add).  The start sum S[t,c] comes from the pull's
+// own log-sum.  Marginals are accumulated in the chunk's frame (see run()).
 #pragma once
 
 #include <float.h>
@@ -49,8 +59,20 @@ __device__ __forceinline__ void lds_barrier() { __asm__ volatile("s_waitcnt lgkm
 // of the same words by other lanes (LDS executes a wave's operations in order).
 __device__ __forceinline__ void wave_lds_order() { __asm__ volatile("" ::: "memory"); }
 
-template <int J, int R, bool FWD, bool LOGSR>
+// a + (lane (i-1) mod 16 of the row of `rot`), one v_add_f32 with a DPP source
+// (row_ror:1).  The s_nop gives the two wait states a DPP read needs after a
+// VALU write, which the compiler does not track across inline asm.  All lanes
+// are active.
+__device__ __forceinline__ float add_row_ror1(float rot, float a) {
+  float r;
+  asm("s_nop 1\n\tv_add_f32_dpp %0, %1, %2 row_ror:1 row_mask:0xf bank_mask:0xf bound_ctrl:1"
+      : "=v"(r) : "v"(rot), "v"(a));
+  return r;
+}
+
+template <int J, int R, bool FWD, bool LOGSR, bool MARG = false>
 struct Chunk {
+  static_assert(!MARG || (!FWD && LOGSR && J == 16), "fused marginals: backward log scan, 16-lane DPP rows");
   static constexpr bool kFwd = FWD;
   static constexpr bool kLog = LOGSR;
   static constexpr int kMaxThreads = R > 16 ? 512 : 1024;
@@ -82,7 +104,7 @@ struct Chunk {
     const bool has_ps = p.ps != nullptr, has_pe = p.pe != nullptr;
     const float* ps_b = has_ps ? p.ps + (size_t)b * T * C : nullptr;
     const float* pe_b = has_pe ? p.pe + (size_t)b * T * C : nullptr;
-    const bool store = p.val != nullptr;
+    const bool store = !MARG && p.val != nullptr;  // the fused backward keeps no beta table
     const double sgn = FWD ? 1.0 : -1.0;
     // fp64 cumulative score of position pos (own label) in log2 units, times sgn
     auto cumx = [&](int pos) { return sgn * (double)cum_b[(size_t)pos * C + c] * kLog2eD; };
@@ -137,6 +159,55 @@ struct Chunk {
     // position t_start at index A0, the positions behind it at A0 + i
     const int A0 = RL - KP;
     double lvl_prev;
+
+    // ---- fused marginals (MARG) ----
+    // The chunk's beta values carry a frame offset d (its levels are the exact
+    // ones minus offs[item], known only after verification).  At its first
+    // owned start, t_hi - 1, the chunk takes the largest alpha*beta/Z of the
+    // positions t_hi .. t_hi+Kmax-1 in its own frame, 2^fr.  Every segmentation
+    // has a boundary among any Kmax consecutive positions, so the true value is
+    // >= 1/(Kmax*C) and d - fr lies in [0, log2(Kmax*C)]: marginals accumulate
+    // as P * 2^(d - fr) without fp32 overflow, and the finalize multiplies them
+    // by 2^(fr + offs[item]).  zd = log2 Z + fr.
+    [[maybe_unused]] const float* u_b = MARG ? p.uval + (size_t)b * (T + 1) * C : nullptr;
+    [[maybe_unused]] const double* al_b = MARG ? p.alvl + (size_t)b * (T + 1) : nullptr;
+    [[maybe_unused]] float* e_own_b = MARG ? p.e_own + (size_t)b * (T + 1) * C : nullptr;
+    [[maybe_unused]] float* s_out_b = MARG ? p.s_out + (size_t)b * (T + 1) * C : nullptr;
+    [[maybe_unused]] float* halo_i = MARG ? p.halo + (size_t)item * Kmax * C : nullptr;
+    [[maybe_unused]] const int own_hi = (FWD || j < jl) ? t_hi : len + 1;  // rows [t_lo, own_hi) are this chunk's
+    [[maybe_unused]] const int lane_last = (lj == J - 1) ? -1 : 0;       // all bits set on the row's last lane
+    // Duration sums: fp32 per lane, added every 64 owned steps (and at the end)
+    // to the chunk's fp64 partials with no-return atomics -- each (k, c) has one
+    // lane, so they never contend, and nothing waits for them.
+    double zd = 0.0;
+    float d32[MARG ? R : 1], ea[MARG ? R : 1];
+    [[maybe_unused]] double* dbp = MARG ? p.db_part + (size_t)item * Kmax * C : nullptr;
+    if constexpr (MARG) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        d32[r] = 0.0f;
+        ea[r] = 0.0f;
+        const int k = 1 + lj + J * r;
+        if (cval && k <= Kmax) dbp[(size_t)(k - 1) * C + c] = 0.0;
+      }
+      if (tid == 0) p.mframe[item] = 0.0;
+      __threadfence();  // the zeros before the first atomic add
+    }
+    auto fold_d = [&]() {
+      if constexpr (MARG) {
+        // addresses and masks from an opaque copy of the lane index: otherwise they
+        // are hoisted out of the step loop and held in registers throughout
+        int ljo = lj;
+        __asm__ volatile("" : "+v"(ljo));
+        double* a = dbp + (size_t)ljo * C + c;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          if (cval && 1 + ljo + J * r <= Kmax) unsafeAtomicAdd(a, (double)d32[r]);
+          a += (size_t)J * C;
+          d32[r] = 0.0f;
+        }
+      }
+    };
     // ---- initial state ----
     if (mode == 0) {
       const int pos = t_start;  // FWD: 0, BWD: len
@@ -229,12 +300,44 @@ struct Chunk {
     float cum_n = cum_b[(size_t)clampT(t_first) * C + c];
     float pa_n = pa_src[(size_t)pa_row(t_first) * C + c];
     float pb_n = pb_src[(size_t)pb_row(t_first) * C + c];
+    [[maybe_unused]] float u_n = 0.0f;
+    [[maybe_unused]] double la_n = 0.0;
+    if constexpr (MARG) {
+      u_n = u_b[(size_t)clampT(t_first) * C + c];
+      la_n = al_b[clampT(t_first)];
+    }
 
     const int rec_spec = (mode == 1) ? (FWD ? t_lo : t_hi) : -1;
     const int rec_end = FWD ? ((t_hi < len) ? t_hi : -1) : ((j >= 1) ? t_lo : -1);
 
     int A = A0;  // ring index of the current position
     for (int t = t_first; t != t_end; t += dir) {
+      if constexpr (MARG) {
+        if (t == t_hi - 1) {
+          // frame estimate from the ring of position t_hi (index A) and the Kmax-1 behind
+          // it; operands from an opaque copy of the sequence index, so that nothing of
+          // this once-per-chunk block is hoisted out of the step loop
+          int bo = b;
+          __asm__ volatile("" : "+s"(bo));
+          const size_t row0 = (size_t)bo * (T + 1);
+          double m = -1e300;
+          if (cval) {
+            for (int i = lj; i < Kmax; i += J) {
+              const int pos = t_hi + i;
+              if (pos <= len) {
+                const double pbv = (has_pe && pos >= 1) ? (double)(p.pe[((size_t)bo * T + pos - 1) * C + c] * kLog2e) : 0.0;
+                const double cxv = -(double)p.cum[(row0 + pos) * C + c] * kLog2eD;
+                const double lb = (rc[A + i] - pbv) + cxv;  // log2 beta(pos, c), chunk frame
+                const double la = (double)p.aval[(row0 + pos) * C + c] + p.alvl[row0 + pos];
+                m = fmax(m, la + lb);
+              }
+            }
+          }
+          double mn;
+          block_minmax(m, m, red(smem, p), zd, mn);
+          if (tid == 0) p.mframe[(size_t)bo * p.P + j] = zd - p.mz2[bo];
+        }
+      }
       if (--A < 0) {
         // the KP newest entries (indices 0 .. KP-1) to the top; each label group
         // copies its own ring inside its wavefront (LDS keeps a wave's order)
@@ -252,8 +355,14 @@ struct Chunk {
       const double cx_t = sgn * (double)cum_n * kLog2eD;
       const float pa_t = pa_n * ((FWD ? t >= 1 : true) ? pa_scale : 0.0f);
       const float pb_t = pb_n * ((FWD ? true : t >= 1) ? pb_scale : 0.0f);
+      [[maybe_unused]] const float u_t = u_n;
+      [[maybe_unused]] const double la_t = la_n;
       {
         const int tn = t + dir;
+        if constexpr (MARG) {
+          u_n = u_b[(size_t)clampT(tn) * C + c];
+          la_n = al_b[clampT(tn)];
+        }
         cum_n = cum_b[(size_t)clampT(tn) * C + c];
         pa_n = pa_src[(size_t)pa_row(tn) * C + c];
         pb_n = pb_src[(size_t)pb_row(tn) * C + c];
@@ -269,11 +378,19 @@ struct Chunk {
       if constexpr (LOGSR) {
         double y0 = e[0] + dbr[0];
         float s0 = 1.0f, s1 = 0.0f;
+        float tm[MARG ? R : 1];  // MARG: the lane's terms 2^(x + db - y0)
+        if constexpr (MARG) tm[0] = 1.0f;
 #pragma unroll
         for (int r = 1; r < R; ++r) {
           const float x = exp2_hw((float)(e[r] - e[0]));
-          if (r & 1) s1 = fmaf(x, edb[r], s1);
-          else s0 = fmaf(x, edb[r], s0);
+          if constexpr (MARG) {
+            tm[r] = x * edb[r];
+            if (r & 1) s1 += tm[r];
+            else s0 += tm[r];
+          } else {
+            if (r & 1) s1 = fmaf(x, edb[r], s1);
+            else s0 = fmaf(x, edb[r], s0);
+          }
         }
         float s = s0 + s1;
         // overflow (inf, or inf * 0 = NaN on a padded duration) or extreme factors
@@ -284,11 +401,59 @@ struct Chunk {
           for (int r = 1; r < R; ++r) m = fmax(m, e[r] + dbr[r]);
           s = 0.0f;
 #pragma unroll
-          for (int r = 0; r < R; ++r) s += exp2_hw((float)((e[r] + dbr[r]) - m));
+          for (int r = 0; r < R; ++r) {
+            const float q = exp2_hw((float)((e[r] + dbr[r]) - m));
+            if constexpr (MARG) tm[r] = q;
+            s += q;
+          }
           y0 = m;
         }
-        // the lane's terms relative to the previous position's level, combined over the group
-        a2 = group_lse2<J>((float)((y0 + cx_t) - lvl_prev), s) + pa_t;
+        // the lane's terms relative to the previous position's level
+        const double yrel = (y0 + cx_t) - lvl_prev;
+        [[maybe_unused]] double lam = 0.0;
+        if constexpr (MARG) {
+          if (t < t_hi) {
+            // P(t,k,c) = term * 2^(y0 + A[t,c]) in the chunk frame
+            lam = (lvl_prev + la_t) - zd;
+            const float yA = (float)(yrel + lam) + (u_t + pa_t);
+            float F = exp2_hw(yA);
+            if (__ballot(yA < -100.0f && s > 0x1p20f)) {
+              // F underflows while later terms (<= FLT_MAX) are large enough to matter:
+              // scale in two steps, 2^(yA+100) (no overflow) then 2^-100 (exact)
+              const float F1 = exp2_hw(yA + 100.0f);
+#pragma unroll
+              for (int r = 0; r < R; ++r) tm[r] = (tm[r] * F1) * 0x1p-100f;
+              F = 1.0f;
+            }
+            // the end sum of position t+1+KP (lane J-1, register R-1) is complete: out
+            const int pr = t + 1 + KP;
+            if (cval && lj == J - 1 && pr <= t_hi - 1 + Kmax && pr <= len) {
+              if (pr < own_hi) e_own_b[(size_t)pr * C + c] = ea[R - 1];
+              else halo_i[(size_t)(pr - t_hi) * C + c] = ea[R - 1];
+            }
+            // end sums slide to positions t+1+lj+16r: the last lane takes the previous
+            // register (register 0: the new position t+1), then the row rotates one
+            // lane up, fused with the accumulation.  Descending r reads ea[r-1] first.
+#pragma unroll
+            for (int r = R - 1; r >= 0; --r) {
+              const float P = tm[r] * F;
+              d32[r] += P;
+              const float prv = (r >= 1) ? ea[r - 1] : 0.0f;
+              // a bitwise merge: a select would become a register-array read at a lane-dependent index
+              const float sl = __int_as_float((__float_as_int(prv) & lane_last) | (__float_as_int(ea[r]) & ~lane_last));
+              ea[r] = add_row_ror1(sl, P);
+            }
+          }
+        }
+        // combined over the group
+        a2 = group_lse2<J>((float)yrel, s) + pa_t;
+        if constexpr (MARG) {
+          if (t < t_hi) {
+            // start sum: sum_k P = 2^(lvl_prev + a2 + alpha level + u - zd)
+            if (cval && lj == 0) s_out_b[(size_t)t * C + c] = exp2_hw((float)(lam + (double)a2) + u_t);
+            if (((t_hi - 1 - t) & 63) == 63) fold_d();
+          }
+        }
       } else {
         // max over durations; ties go to the smallest duration (lanes hold ascending k)
         double ym = e[0] + dbr[0];
@@ -392,6 +557,22 @@ struct Chunk {
         }
       }
     }
+    if constexpr (MARG) {
+      // rows still in the registers (lane lj, register r: position t_lo+1+lj+16r),
+      // row t_lo (no own starts end there) and the duration sums
+      if (cval) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const int pr = t_lo + 1 + lj + J * r;
+          if (pr <= t_hi - 1 + Kmax && pr <= len) {
+            if (pr < own_hi) e_own_b[(size_t)pr * C + c] = ea[r];
+            else halo_i[(size_t)(pr - t_hi) * C + c] = ea[r];
+          }
+        }
+        if (lj == 0) e_own_b[(size_t)t_lo * C + c] = 0.0f;
+      }
+      fold_d();
+    }
   }
 };
 
@@ -399,6 +580,12 @@ template <int J, int R>
 int launch_fast_jr(const Plan& pl, const ScanParams& p, bool fwd, hipStream_t st) {
   return fwd ? launch_chunk_dir<Chunk<J, R, true, true>>(pl, p, pl.fast_lds, pl.FNT, st)
              : launch_chunk_dir<Chunk<J, R, false, true>>(pl, p, pl.fast_lds, pl.FNT, st);
+}
+
+// Backward log scan with the segment marginals fused (16-lane groups).
+template <int R>
+int launch_fused_r(const Plan& pl, const ScanParams& p, hipStream_t st) {
+  return launch_chunk_dir<Chunk<16, R, false, true, true>>(pl, p, pl.fast_lds, pl.FNT, st);
 }
 
 // Max-semiring forward with backpointers (factorised Viterbi).

@@ -58,6 +58,17 @@ struct ScanParams {
   int G, CL, NQ, xmap;
   unsigned long long* xch;
   int* xabort;
+  // backward scan with fused marginals: forward-side inputs and, per chunk
+  // item (b*P + j), outputs in the chunk's frame (rescaled by the finalize)
+  const float* uval;       // (B, T+1, C) u[t,c] = log2 sum_c' 2^(alpha-hat[t,c'] + trans[c',c] log2(e))
+  const float* aval;       // (B, T+1, C) alpha-hat (log2)
+  const double* alvl;      // (B, T+1) alpha levels
+  const double* mz2;       // (B) log2 partition
+  float* e_own;            // (B, T+1, C) end sums of the rows a chunk owns
+  float* s_out;            // (B, T+1, C) start sums
+  float* halo;             // (B*P, Kmax, C) end sums of rows t_hi .. t_hi+Kmax-1 of chunk j < jl
+  double* db_part;         // (B*P, Kmax, C) duration sums
+  double* mframe;          // (B*P) the chunk's frame estimate fr (log2)
 };
 
 struct MargParams {
@@ -100,6 +111,30 @@ struct FinalParams {
   float* grad_tr;            // (C, C)
   float* grad_db;            // (K, C)
   int trows;                 // grad_tr is (trows, C, C) when > 0
+};
+
+// Row passes of the backward with fused marginals (tsm_fused.hip).
+struct FusedParams {
+  const int64_t* lengths;
+  const float* trans;      // (C, C) natural log units
+  const float* aval;       // (B, T+1, C) alpha-hat
+  float* uval;             // (B, T+1, C) written by the u pass
+  int B, T, C, K, Kmax;
+  int P, Lc;               // backward scan chunks per sequence, chunk length
+  int GNB, GTB;            // transition-gradient row blocks per sequence, rows per block
+  const double* offs;      // (B*P) verified level offsets of the backward chunks
+  double* mframe;          // (B*P) frame estimates; the frame scale pass turns them into factors f_j
+  const float* e_own;      // (B, T+1, C)
+  const float* s_out;      // (B, T+1, C)
+  const float* halo;       // (B*P, Kmax, C)
+  const double* db_part;   // (B*P, Kmax, C)
+  double* tr_part;         // (B*GNB, C, C)
+  const float* grad_output;
+  float* grad_cum;
+  float* grad_ps;
+  float* grad_pe;
+  float* grad_tr;
+  float* grad_db;
 };
 
 struct ViterbiParams {
@@ -155,6 +190,12 @@ struct PrologueParams {
 // launchers (return hipError_t as int)
 int launch_scan_forward(const Plan& pl, const ScanParams& p, int semiring, hipStream_t s);
 int launch_scan_backward(const Plan& pl, const ScanParams& p, int semiring, hipStream_t s);
+// backward log scan with fused marginals (pl.mfused), and its row passes
+int launch_scan_backward_fused(const Plan& pl, const ScanParams& p, hipStream_t s);
+int launch_fused_j16_lo(const Plan& pl, const ScanParams& p, hipStream_t s);
+int launch_fused_j16_hi(const Plan& pl, const ScanParams& p, hipStream_t s);
+int launch_u_rows(const Plan& pl, const FusedParams& f, hipStream_t s);
+int launch_fused_finalize(const Plan& pl, const FusedParams& f, hipStream_t s);
 // verification of speculative chunk boundaries / level offsets (shared by both scan paths)
 int launch_verify(const Plan& pl, const ScanParams& p, bool forward, hipStream_t s);
 int launch_apply_offsets(const Plan& pl, const ScanParams& p, bool forward, hipStream_t s);
@@ -232,6 +273,10 @@ enum KernelId : int {
   kKTransPrep,
   kKGold,
   kKPrologue,
+  kKURows,
+  kKTransGrad,
+  kKFusedRows,
+  kKFusedShared,
   kNumKernels
 };
 

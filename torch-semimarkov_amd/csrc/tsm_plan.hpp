@@ -49,6 +49,10 @@ struct Plan {
   // when members share blockIdx % 8
   int coop, CG, CCL, CR, CNT, CRS, CRL, CNQ, CGRID, cxmap;
   size_t coop_lds;
+  // backward with the marginals fused into the register-resident beta scan
+  // (mfused == 1; needs fast with FJ == 16): GNB transition-gradient row blocks
+  // of GTB starts per sequence
+  int mfused, GNB, GTB;
 };
 
 

@@ -654,6 +654,16 @@ int launch_apply_offsets(const Plan& pl, const ScanParams& p, bool forward, hipS
   return hipGetLastError();
 }
 
+int launch_scan_backward_fused(const Plan& pl, const ScanParams& p, hipStream_t st) {
+  if (!pl.fast || pl.FJ != 16) return (int)hipErrorInvalidValue;
+  ScanParams q = p;
+  q.RS = pl.FRS;
+  q.RL = pl.FRL;
+  q.R = pl.FR;
+  q.KP = 16 * pl.FR;
+  return pl.FR <= 16 ? launch_fused_j16_lo(pl, q, st) : launch_fused_j16_hi(pl, q, st);
+}
+
 int launch_scan_forward(const Plan& pl, const ScanParams& p, int semiring, hipStream_t s) {
   return launch_any(pl, p, semiring, true, s);
 }

@@ -22,7 +22,8 @@ const char* const kNames[kNumKernels] = {
     "bwd_fixup_kernel",  "apply_offsets_kernel", "marginal_kernel",         "finalize_rows_kernel",
     "finalize_shared_kernel", "checkpoints_kernel", "viterbi_kernel",       "backtrace_kernel",
     "retry_kernel",      "dense_prep_kernel",    "gold_kernels",
-    "prologue_kernels",
+    "prologue_kernels",  "u_rows_kernel",        "trans_grad_kernel",       "fused_rows_kernel",
+    "fused_shared_kernel",
 };
 
 struct Pending {

@@ -31,6 +31,7 @@ PLAN_FIELDS = (
     "fast", "FJ", "FR", "FNT", "fast_lds", "mfast", "MR",
     "dense", "DJ", "DNT", "dtrl", "dense_lds", "DG", "DNTM", "DNB", "DTB", "dmarg_lds",
     "coop", "CG", "CCL", "CR", "CNQ", "coop_lds",
+    "mfused", "GNB", "GTB",
 )
 
 _p = ctypes.c_void_p
