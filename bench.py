@@ -390,10 +390,14 @@ def main():
     passes = None if args.no_passes else measure_passes(args, cum.detach(), tr.detach(), db.detach(), L, K, cells,
                                                           ms_step, plan)
     # dominant kernel: the largest total time over the timed steps
-    dom = max((k for k in ktimes if k in KERNEL_OPS), key=lambda k: ktimes[k][0])
+    kops = dict(KERNEL_OPS)
+    if plan.get("mfused"):
+        # the beta scan also accumulates the segment marginals: both passes' ops per cell
+        kops["scan_bwd_kernel"] = tuple(a + b for a, b in zip(KERNEL_OPS["scan_bwd_kernel"], KERNEL_OPS["marginal_kernel"]))
+    dom = max((k for k in ktimes if k in kops), key=lambda k: ktimes[k][0])
     dom_total, dom_launches = ktimes[dom]
     dom_avg_ms = dom_total / dom_launches
-    nv, nt = KERNEL_OPS[dom]
+    nv, nt = kops[dom]
     achieved = cells * (nv + nt * V_PEAK / T_PEAK) / (dom_avg_ms / 1e3) / 1e12
     traffic = profiled_traffic(dom, args.config)
     peak = V_PEAK / 1e12

@@ -451,6 +451,24 @@ def test_fused_backward_vs_fp64_oracle(B, T, K, C, lengths, proj, monkeypatch):
     assert_grads(grads, g64)
 
 
+def test_fused_backward_banded_transitions(monkeypatch):
+    """Transitions of -1000 outside a band of width 3: the transition ranges
+    exceed what the one-pass label mix and the factorised transition gradient
+    accept, so both take their exact forms."""
+    monkeypatch.delenv("TSM_SCAN_PATH", raising=False)
+    monkeypatch.delenv("TSM_MARGINAL_PATH", raising=False)
+    B, T, K, C = 2, 2000, 40, 36
+    _fused_plan(B, T, C, K, False)
+    cum, tr, db, L, _, _ = rand_problem(B, T, K, C, 4242, [2000, 1333])
+    idx = torch.arange(C)
+    tr[(idx[:, None] - idx[None, :]).abs() > 3] = -1000.0
+    g = torch.tensor([1.0, 0.7])
+    p64, g64 = oracle_fp64(cum, tr, db, L, K, g=g)
+    part, grads = run_hip(cum, tr, db, L, K, g=g)
+    np.testing.assert_allclose(part.double().numpy(), p64.numpy(), rtol=RTOL_Z)
+    assert_grads(grads, g64)
+
+
 def _ops_backward(cum, tr, db, L, K, ps=None, pe=None, g=None):
     """forward (storing alpha) + backward through the custom ops: grads and the
     backward's recomputed-chunk counts."""

@@ -390,8 +390,8 @@ int make_plan(int64_t B, int64_t T, int64_t C, int64_t K, int has_ps, int has_pe
   const bool separate = menv != nullptr && strcmp(menv, "separate") == 0;
   if (!separate && p.fast && p.FJ == 16 && p.C * p.C <= 4096) {
     p.mfused = 1;
-    // transition gradient: about two blocks per CU, at least 256 starts each
-    int64_t gnb = cdiv(2 * (int64_t)di.n_cu, (int64_t)p.B);
+    // transition gradient: about eight blocks per CU, at least 256 starts each
+    int64_t gnb = cdiv(8 * (int64_t)di.n_cu, (int64_t)p.B);
     gnb = std::max<int64_t>(1, std::min<int64_t>(gnb, cdiv(T, 256)));
     p.GTB = (int)cdiv(T, gnb);
     p.GNB = (int)cdiv(T, p.GTB);

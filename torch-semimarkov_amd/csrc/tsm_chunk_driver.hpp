@@ -56,6 +56,51 @@ __global__ void __launch_bounds__(CH::kMaxThreads) chunk_retry_kernel(ScanParams
   chunk_scan_body<CH>(p);
 }
 
+// Fast path of the repair: when no speculative chunk of sequence b failed its
+// verification, nothing is recomputed and the frame offsets are a segmented
+// prefix sum over the walk (restarting at 0 at each exact chunk) of the
+// accepted mid-spreads.  Wave 0 scans 64 chunks at a time with shuffles.
+// Returns false (and writes nothing) when some chunk needs a recompute;
+// otherwise F (thread 0) is the offset after the walk.
+template <bool FWD>
+__device__ bool fixup_prefix(const ScanParams& p, int b, int jl, int nch, double& F) {
+  const int n = FWD ? nch - 1 : jl;  // chunks of the walk: FWD 1..nch-1, BWD jl-1..0
+  bool bad = false;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    const int it = b * p.P + (FWD ? 1 + i : jl - 1 - i);
+    bad = bad || (p.status[it] == 1 && !(p.vstat[2 * it] - p.vstat[2 * it + 1] <= (double)p.tol));
+  }
+  if (__syncthreads_or(bad)) return false;
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    double carry = 0.0;
+    for (int i0 = 0; i0 < n; i0 += 64) {
+      const int i = i0 + lane;
+      const int it = b * p.P + (FWD ? 1 + i : jl - 1 - i);
+      double v = 0.0;
+      int rst = 0;
+      if (i < n) {
+        if (p.status[it] == 1) v = 0.5 * (p.vstat[2 * it] + p.vstat[2 * it + 1]);
+        else rst = 1;  // exact chunk: the offset restarts at 0
+      }
+      // inclusive segmented scan: (a, ra) then (v, r) -> (r ? v : a + v, ra | r)
+      for (int d = 1; d < 64; d <<= 1) {
+        const double a = __shfl_up(v, d, 64);
+        const int ra = __shfl_up(rst, d, 64);
+        if (lane >= d) {
+          if (!rst) v += a;
+          rst |= ra;
+        }
+      }
+      const double off = rst ? v : carry + v;
+      if (i < n) p.offs[it] = off;
+      carry = __shfl(off, 63, 64);
+    }
+    F = carry;
+  }
+  return true;
+}
+
 // Sequential verification / repair of one direction: one block per sequence
 // walks its chunks, accepts a speculative chunk's frame offset when the
 // boundary spread is within tolerance, recomputes it exactly otherwise.
@@ -73,6 +118,12 @@ __global__ void __launch_bounds__(CH::kMaxThreads) chunk_fixup_kernel(ScanParams
   const int jl = bwd_last_chunk(p, len);
   const int nch = len == 0 ? 1 : (len + p.Lc - 1) / p.Lc;
   if (threadIdx.x == 0) p.offs[(size_t)b * p.P + (FWD ? 0 : jl)] = 0.0;
+  if (fixup_prefix<FWD>(p, b, jl, nch, F)) {
+    __syncthreads();
+    if (FWD) finish_partition<CH::kLog>(p, b, len, F, 0);
+    else if (threadIdx.x == 0 && p.recomputed != nullptr) p.recomputed[b] = 0;
+    return;
+  }
   for (int j = FWD ? 1 : jl - 1; FWD ? j < nch : j >= 0; j += FWD ? 1 : -1) {
     const int item = b * p.P + j;
     if (p.status[item] != 1) {

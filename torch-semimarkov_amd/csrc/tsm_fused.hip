@@ -14,6 +14,8 @@
 //               block in fp64;
 //   shared      grad_db = sum_j f_j db_part[j], grad_tr = sum of the row blocks,
 //               both weighted by grad_output, in a fixed order.
+#include <algorithm>
+
 #include "tsm_device.hpp"
 #include "tsm_internal.hpp"
 
@@ -59,19 +61,54 @@ __global__ void __launch_bounds__(256) u_rows_kernel(FusedParams f) {
   const int nr = min(kURows, len + 1 - t0);
   float* tr2 = reinterpret_cast<float*>(smem);  // [c_src][c_dst], log2 units
   float* ah = tr2 + C * C;                       // [row][c]
+  float* cmx = ah + kURows * C;                  // [c] max over sources of tr2[., c]
+  float* crg = cmx + C;                          // [c] its range (max - min)
   for (int i = threadIdx.x; i < C * C; i += blockDim.x) tr2[i] = f.trans[i] * kLog2e;
   const float* av = f.aval + ((size_t)b * (T + 1) + t0) * C;
   for (int i = threadIdx.x; i < nr * C; i += blockDim.x) ah[i] = av[i];
+  __syncthreads();
+  for (int c = threadIdx.x; c < C; c += blockDim.x) {
+    float hi = kMinusInf, lo = -kMinusInf;
+    for (int cs = 0; cs < C; ++cs) {
+      hi = fmax2(hi, tr2[cs * C + c]);
+      lo = fmin(lo, tr2[cs * C + c]);
+    }
+    cmx[c] = hi;
+    crg[c] = hi - lo;
+  }
   __syncthreads();
   float* uo = f.uval + ((size_t)b * (T + 1) + t0) * C;
   for (int i = threadIdx.x; i < nr * C; i += blockDim.x) {
     const int r = i / C, c = i % C;
     const float* a = ah + r * C;
-    float m = kMinusInf;
-    for (int cs = 0; cs < C; ++cs) m = fmax2(m, a[cs] + tr2[cs * C + c]);
-    float s = 0.0f;
-    for (int cs = 0; cs < C; ++cs) s += exp2_hw((a[cs] + tr2[cs * C + c]) - m);
-    uo[i] = m + log2_hw(s);
+    const float* tc = tr2 + c;
+    // Shift: alpha-hat <= 0 with an exact 0 at the row's best label, so every
+    // term is <= 2^cmx[c] and the largest is >= 2^(cmx[c] - crg[c]): with a
+    // range of at most 64 the column maximum is a safe shift (one pass);
+    // otherwise the row's own maximum (a first pass).  Four independent chains
+    // per pass (the LDS reads of a chain's next term overlap the others' work).
+    int cs = 0;
+    float m = cmx[c];
+    if (!(crg[c] <= 64.0f)) {
+      float m0 = kMinusInf, m1 = kMinusInf, m2 = kMinusInf, m3 = kMinusInf;
+      for (; cs + 4 <= C; cs += 4) {
+        m0 = fmax2(m0, a[cs] + tc[cs * C]);
+        m1 = fmax2(m1, a[cs + 1] + tc[(cs + 1) * C]);
+        m2 = fmax2(m2, a[cs + 2] + tc[(cs + 2) * C]);
+        m3 = fmax2(m3, a[cs + 3] + tc[(cs + 3) * C]);
+      }
+      for (; cs < C; ++cs) m0 = fmax2(m0, a[cs] + tc[cs * C]);
+      m = fmax2(fmax2(m0, m1), fmax2(m2, m3));
+    }
+    float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+    for (cs = 0; cs + 4 <= C; cs += 4) {
+      s0 += exp2_hw((a[cs] + tc[cs * C]) - m);
+      s1 += exp2_hw((a[cs + 1] + tc[(cs + 1) * C]) - m);
+      s2 += exp2_hw((a[cs + 2] + tc[(cs + 2) * C]) - m);
+      s3 += exp2_hw((a[cs + 3] + tc[(cs + 3) * C]) - m);
+    }
+    for (; cs < C; ++cs) s0 += exp2_hw((a[cs] + tc[cs * C]) - m);
+    uo[i] = m + log2_hw((s0 + s1) + (s2 + s3));
   }
 }
 
@@ -104,23 +141,47 @@ __global__ void fused_rows_kernel(FusedParams f) {
 }
 
 // ---- transitions: one block per (sequence, row block); rows staged kGRows at a time ----
-// Thread i of 256 takes the (source, destination) pairs i, i+256, ... (NPT of them).
-constexpr int kGRows = 128;
+// Thread i of the block takes the (source, destination) pairs i, i+nt, ... (NPT
+// of them); the block has about C*C/NPT threads.
+//
+// With x = alpha-hat[t,c'] + tr[c',c] + log2 S[t,c] - u[t,c] the term is 2^x.
+// When every column's transition range (max - min over sources) is <= 30 the
+// block uses the factorised form 2^x = A[t,c'] * W[t,c] * E[c',c] with
+// A = 2^alpha-hat (<= 1), W = 2^(log2 S - u + cm[c]), E = 2^(tr - cm[c]) (<= 1),
+// cm[c] the column maximum: u >= cm[c] - range, so W <= S * 2^30, and an A that
+// underflows drops a term below 2^-96.  The row loop is then one FMA per pair
+// (the sum over rows of A * W, times E at the end) instead of an exponential.
+constexpr int kGRows = 64;
 
 template <int NPT>
 __global__ void __launch_bounds__(256) trans_grad_kernel(FusedParams f) {
   extern __shared__ __align__(16) char smem[];
   const int C = f.C, T = f.T, Lc = f.Lc;
   const int b = blockIdx.y, blk = blockIdx.x;
+  const int nt = blockDim.x;
   const int len = flen(f.lengths, b, T);
   const int NP = C * C;
-  float* ah = reinterpret_cast<float*>(smem);  // [row][c_src] alpha-hat
-  float* vq = ah + kGRows * C;                 // [row][c_dst] log2 S - u
+  float* ah = reinterpret_cast<float*>(smem);  // [row][c_src] alpha-hat, or A
+  float* vq = ah + kGRows * C;                 // [row][c_dst] log2 S - u, or W
+  float* fs = vq + kGRows * C;                 // [row] chunk factor of the row's start
+  float* cm = fs + kGRows;                     // [c_dst] column maximum of the transitions
+  bool wide = false;
+  for (int c = threadIdx.x; c < C; c += nt) {
+    float hi = kMinusInf, lo = -kMinusInf;
+    for (int cs = 0; cs < C; ++cs) {
+      const float v = f.trans[(size_t)cs * C + c] * kLog2e;
+      hi = fmax2(hi, v);
+      lo = fmin(lo, v);
+    }
+    cm[c] = hi;
+    wide = wide || !(hi - lo <= 30.0f);
+  }
+  const bool fact = !__syncthreads_or(wide);
   float tr2[NPT];
   int cs_[NPT], cd_[NPT];
 #pragma unroll
   for (int i = 0; i < NPT; ++i) {
-    const int pr = threadIdx.x + 256 * i;
+    const int pr = threadIdx.x + nt * i;
     const int pp = pr < NP ? pr : 0;  // surplus slots repeat pair 0 and are not stored
     cs_[i] = pp / C;
     cd_[i] = pp % C;
@@ -139,19 +200,37 @@ __global__ void __launch_bounds__(256) trans_grad_kernel(FusedParams f) {
   for (int tb = lo; tb < hi; tb += kGRows) {
     const int nr = min(kGRows, hi - tb);
     __syncthreads();
-    for (int i = threadIdx.x; i < nr * C; i += blockDim.x) {
-      const int r = i / C, c = i % C, t = tb + r;
-      const size_t o = ((size_t)b * (T + 1) + t) * C + c;
-      ah[i] = f.aval[o];
-      const float S = (float)(fscale(f, b, fchunk(t, len, Lc)) * (double)f.s_out[o]);
-      vq[i] = (S > 0.0f ? log2_hw(S) : kMinusInf) - f.uval[o];
+    if (threadIdx.x < nr) fs[threadIdx.x] = (float)fscale(f, b, fchunk(tb + threadIdx.x, len, Lc));
+    __syncthreads();
+    const size_t o0 = ((size_t)b * (T + 1) + tb) * C;
+    for (int i = threadIdx.x; i < nr * C; i += nt) {
+      const float S = fs[i / C] * f.s_out[o0 + i];
+      const float v = (S > 0.0f ? log2_hw(S) : kMinusInf) - f.uval[o0 + i];
+      if (fact) {
+        ah[i] = exp2_hw(f.aval[o0 + i]);
+        vq[i] = exp2_hw(v + cm[i % C]);
+      } else {
+        ah[i] = f.aval[o0 + i];
+        vq[i] = v;
+      }
     }
     __syncthreads();
-    for (int r = 0; r < nr; ++r) {
-      const float* ar = ah + r * C;
-      const float* vr = vq + r * C;
+    if (fact) {
+#pragma unroll 4
+      for (int r = 0; r < nr; ++r) {
+        const float* ar = ah + r * C;
+        const float* vr = vq + r * C;
 #pragma unroll
-      for (int i = 0; i < NPT; ++i) a32[i] += exp2_hw((ar[cs_[i]] + tr2[i]) + vr[cd_[i]]);
+        for (int i = 0; i < NPT; ++i) a32[i] = fmaf(ar[cs_[i]], vr[cd_[i]], a32[i]);
+      }
+    } else {
+#pragma unroll 4
+      for (int r = 0; r < nr; ++r) {
+        const float* ar = ah + r * C;
+        const float* vr = vq + r * C;
+#pragma unroll
+        for (int i = 0; i < NPT; ++i) a32[i] += exp2_hw((ar[cs_[i]] + tr2[i]) + vr[cd_[i]]);
+      }
     }
 #pragma unroll
     for (int i = 0; i < NPT; ++i) {
@@ -162,7 +241,7 @@ __global__ void __launch_bounds__(256) trans_grad_kernel(FusedParams f) {
   double* out = f.tr_part + ((size_t)b * f.GNB + blk) * NP;
 #pragma unroll
   for (int i = 0; i < NPT; ++i)
-    if (threadIdx.x + 256 * i < NP) out[threadIdx.x + 256 * i] = a64[i];
+    if (threadIdx.x + nt * i < NP) out[threadIdx.x + nt * i] = fact ? a64[i] * exp2((double)(tr2[i] - cm[cd_[i]])) : a64[i];
 }
 
 // ---- shared gradients: one wavefront per output element, fixed summation order ----
@@ -202,7 +281,7 @@ __global__ void __launch_bounds__(256) fused_shared_kernel(FusedParams f) {
 }  // namespace
 
 int launch_u_rows(const Plan& pl, const FusedParams& f, hipStream_t s) {
-  const size_t lds = sizeof(float) * ((size_t)pl.C * pl.C + (size_t)kURows * pl.C);
+  const size_t lds = sizeof(float) * ((size_t)pl.C * pl.C + (size_t)kURows * pl.C + 2 * (size_t)pl.C);
   TimedLaunch tl(kKURows, s);
   hipLaunchKernelGGL(u_rows_kernel, dim3((pl.T + 1 + kURows - 1) / kURows, pl.B), dim3(256), lds, s, f);
   return hipGetLastError();
@@ -210,12 +289,15 @@ int launch_u_rows(const Plan& pl, const FusedParams& f, hipStream_t s) {
 
 template <int NPT>
 void launch_trans_grad(const Plan& pl, const FusedParams& f, hipStream_t s) {
-  const size_t lds = sizeof(float) * 2 * (size_t)kGRows * pl.C;
-  hipLaunchKernelGGL(trans_grad_kernel<NPT>, dim3(pl.GNB, pl.B), dim3(256), lds, s, f);
+  const size_t lds = sizeof(float) * (2 * (size_t)kGRows * pl.C + kGRows + pl.C);
+  const int np = pl.C * pl.C;
+  int nt = (np + NPT - 1) / NPT;
+  nt = std::max(64, std::min(256, (nt + 63) / 64 * 64));
+  hipLaunchKernelGGL(trans_grad_kernel<NPT>, dim3(pl.GNB, pl.B), dim3(nt), lds, s, f);
 }
 
 int launch_fused_finalize(const Plan& pl, const FusedParams& f, hipStream_t s) {
-  const int npt = (pl.C * pl.C + 255) / 256;
+  const int npt = (pl.C * pl.C + 255) / 256;  // pairs per thread with 256 threads
   if (npt > 16) return (int)hipErrorInvalidValue;
   {
     const int n = pl.B * pl.P;
