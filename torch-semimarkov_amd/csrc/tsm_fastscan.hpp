@@ -48,7 +48,6 @@ namespace fastscan {
 using namespace scan_detail;
 
 constexpr double kInvD = -1e30;  // ring value of a position that does not exist
-constexpr int kCJ = 4;           // labels per lane in the label mix (plans keep C <= 4*J)
 constexpr double kLog2eD = 1.4426950408889634;
 
 // Wait for this wave's LDS operations, then barrier.  Global loads in flight
@@ -70,9 +69,12 @@ __device__ __forceinline__ float add_row_ror1(float rot, float a) {
   return r;
 }
 
-template <int J, int R, bool FWD, bool LOGSR, bool MARG = false>
+// CJ source labels per lane in the label mix (C <= CJ * J; the launchers pick 2
+// when C <= 2J, else 4).
+template <int J, int R, bool FWD, bool LOGSR, bool MARG = false, int CJ = 4>
 struct Chunk {
   static_assert(!MARG || (!FWD && LOGSR && J == 16), "fused marginals: backward log scan, 16-lane DPP rows");
+  static constexpr int kCJ = CJ;
   static constexpr bool kFwd = FWD;
   static constexpr bool kLog = LOGSR;
   static constexpr int kMaxThreads = R > 16 ? 512 : 1024;
@@ -487,25 +489,34 @@ struct Chunk {
       }
       const float mx = group_max<J>(ml);
       const double lvl_t = lvl_prev + (double)mx;
-      float mq = kMinusInf;
-      int mqi = 0x7fffffff;
-#pragma unroll
-      for (int i = 0; i < kCJ; ++i)
-        if (lj + J * i < C) {
-          const float q = (rv[i] - mx) + trr[i];
-          if (q > mq) {
-            mq = q;
-            mqi = lj + J * i;
-          }
-        }
       float mixv;
       if constexpr (LOGSR) {
+        // the exponent shift of the mix is the source maximum of rv + trr, which
+        // does not wait for the row maximum (the two group reductions overlap);
+        // the shift only has to be near the largest term and is added back
+        // exactly, the terms keep the form (rv - mx) + trr
+        float mt = kMinusInf;
+#pragma unroll
+        for (int i = 0; i < kCJ; ++i)
+          if (lj + J * i < C) mt = fmax2(mt, rv[i] + trr[i]);
+        const float shift = group_max<J>(mt) - mx;
         float sq = 0.0f;
 #pragma unroll
         for (int i = 0; i < kCJ; ++i)
-          if (lj + J * i < C) sq += exp2_hw(((rv[i] - mx) + trr[i]) - mq);
-        mixv = group_lse2<J>(mq, sq);
+          if (lj + J * i < C) sq += exp2_hw(((rv[i] - mx) + trr[i]) - shift);
+        mixv = shift + log2_hw(group_sum<J>(sq));
       } else {
+        float mq = kMinusInf;
+        int mqi = 0x7fffffff;
+#pragma unroll
+        for (int i = 0; i < kCJ; ++i)
+          if (lj + J * i < C) {
+            const float q = (rv[i] - mx) + trr[i];
+            if (q > mq) {
+              mq = q;
+              mqi = lj + J * i;
+            }
+          }
         // Viterbi: best source label for a segment starting at t (first on ties)
         const ValIdx best = group_argmax_first<J>(ValIdx{mq, mqi});
         mixv = best.v;
@@ -578,22 +589,31 @@ struct Chunk {
   }
 };
 
+// source labels per lane of the label mix: 2 when C <= 2J, else 4 (the plan keeps C <= 4J)
+template <int J>
+inline bool narrow_mix(const ScanParams& p) { return p.C <= 2 * J; }
+
 template <int J, int R>
 int launch_fast_jr(const Plan& pl, const ScanParams& p, bool fwd, hipStream_t st) {
-  return fwd ? launch_chunk_dir<Chunk<J, R, true, true>>(pl, p, pl.fast_lds, pl.FNT, st)
-             : launch_chunk_dir<Chunk<J, R, false, true>>(pl, p, pl.fast_lds, pl.FNT, st);
+  if (narrow_mix<J>(p))
+    return fwd ? launch_chunk_dir<Chunk<J, R, true, true, false, 2>>(pl, p, pl.fast_lds, pl.FNT, st)
+               : launch_chunk_dir<Chunk<J, R, false, true, false, 2>>(pl, p, pl.fast_lds, pl.FNT, st);
+  return fwd ? launch_chunk_dir<Chunk<J, R, true, true, false, 4>>(pl, p, pl.fast_lds, pl.FNT, st)
+             : launch_chunk_dir<Chunk<J, R, false, true, false, 4>>(pl, p, pl.fast_lds, pl.FNT, st);
 }
 
 // Backward log scan with the segment marginals fused (16-lane groups).
 template <int R>
 int launch_fused_r(const Plan& pl, const ScanParams& p, hipStream_t st) {
-  return launch_chunk_dir<Chunk<16, R, false, true, true>>(pl, p, pl.fast_lds, pl.FNT, st);
+  if (narrow_mix<16>(p)) return launch_chunk_dir<Chunk<16, R, false, true, true, 2>>(pl, p, pl.fast_lds, pl.FNT, st);
+  return launch_chunk_dir<Chunk<16, R, false, true, true, 4>>(pl, p, pl.fast_lds, pl.FNT, st);
 }
 
 // Max-semiring forward with backpointers (factorised Viterbi).
 template <int J, int R>
 int launch_fast_max_jr(const Plan& pl, const ScanParams& p, hipStream_t st) {
-  return launch_chunk_dir<Chunk<J, R, true, false>>(pl, p, pl.fast_lds, pl.FNT, st);
+  if (narrow_mix<J>(p)) return launch_chunk_dir<Chunk<J, R, true, false, false, 2>>(pl, p, pl.fast_lds, pl.FNT, st);
+  return launch_chunk_dir<Chunk<J, R, true, false, false, 4>>(pl, p, pl.fast_lds, pl.FNT, st);
 }
 
 }  // namespace fastscan
