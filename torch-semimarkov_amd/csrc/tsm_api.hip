@@ -90,7 +90,10 @@ void plan_fast(Plan& p, const DeviceInfo& di) {
   const char* env = getenv("TSM_SCAN_PATH");
   if (env != nullptr && strcmp(env, "generic") == 0) return;
   double best = 1e300;
+  const char* jenv = getenv("TSM_FAST_J");  // diagnostics: only this lane-group size
+  const int jonly = jenv != nullptr ? atoi(jenv) : 0;
   for (int J : {8, 16, 32, 64}) {
+    if (jonly != 0 && J != jonly) continue;
     if (p.C > 4 * J) continue;  // the label mix handles at most 4 labels per lane
     int R = (p.Kmax + J - 1) / J;
     while (R <= 32 && !fast_instantiated(J, R)) ++R;
@@ -418,6 +421,7 @@ struct ScanWs {
   float *st_spec, *st_end, *fin, *gring;
   double *lv_spec, *lv_end, *offs, *vstat, *fin_lvl, *z2;
   int* status;
+  int* vflag;
   unsigned long long* xch;
   int* xabort;
 };
@@ -432,6 +436,7 @@ ScanWs carve_scan(Carver& cv, const Plan& p) {
   w.offs = cv.take<double>(items);
   w.vstat = cv.take<double>(2 * items);
   w.status = cv.take<int>(items);
+  w.vflag = cv.take<int>(1);
   w.fin = cv.take<float>((size_t)p.B * p.C);
   w.fin_lvl = cv.take<double>(p.B);
   w.z2 = cv.take<double>(p.B);
@@ -470,6 +475,7 @@ tsm::ScanParams scan_params(const Plan& pl, const ScanWs& w, const float* cum, c
   p.offs = w.offs;
   p.vstat = w.vstat;
   p.status = w.status;
+  p.vflag = w.vflag;
   p.fin = w.fin;
   p.fin_lvl = w.fin_lvl;
   p.z2 = w.z2;

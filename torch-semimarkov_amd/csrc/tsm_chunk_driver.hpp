@@ -40,7 +40,10 @@ __device__ __forceinline__ void chunk_scan_body(const ScanParams& p) {
   }
   if (p.retry && retry_skip(p, item)) return;
   const int mode = (FWD ? fwd_spec(p, j) : bwd_spec(p, j, len)) ? 1 : 0;
-  if (threadIdx.x == 0) p.status[item] = mode;
+  if (threadIdx.x == 0) {
+    p.status[item] = mode;
+    if (p.retry) *p.vflag = 1;
+  }
   CH::run(p, smem, b, j, mode, nullptr, nullptr);
 }
 
@@ -190,7 +193,7 @@ int launch_chunk_dir(const Plan& pl, const ScanParams& p, size_t lds, int nthrea
       TimedLaunch tl(kKRetry, st);
       hipLaunchKernelGGL(kr, dim3(pl.B * pl.P), dim3(nthreads), lds, st, retry_params(p));
     }
-    e = (hipError_t)launch_verify(pl, p, fwd, st);
+    e = (hipError_t)launch_verify(pl, p, fwd, st, true);
     if (e != hipSuccess) return e;
   }
   {

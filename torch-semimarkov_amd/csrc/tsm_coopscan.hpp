@@ -409,7 +409,10 @@ __device__ __forceinline__ void coop_scan_body(const ScanParams& p) {
     if (p.retry && !(p.status[item] == 1 && (p.vstat[2 * item] - p.vstat[2 * item + 1] > (double)p.tol))) continue;
     const int mode = (FWD ? fwd_spec(p, j) : bwd_spec(p, j, len)) ? 1 : 0;
     if (!CH::run(p, smem, b, j, mode, nullptr, nullptr, me.m, xb, s)) return;
-    if (lead && threadIdx.x == 0) p.status[item] = mode;
+    if (lead && threadIdx.x == 0) {
+      p.status[item] = mode;
+      if (p.retry) *p.vflag = 1;
+    }
     __syncthreads();
   }
 }
@@ -546,7 +549,7 @@ int launch_coop_dir(const Plan& pl, const ScanParams& p, hipStream_t st) {
       e = launch_coop(kr, pl, retry_params(p), 0, st);
     }
     if (e != hipSuccess) return e;
-    e = (hipError_t)launch_verify(pl, p, fwd, st);
+    e = (hipError_t)launch_verify(pl, p, fwd, st, true);
     if (e != hipSuccess) return e;
   }
   {

@@ -49,8 +49,17 @@ __global__ void frame_scale_kernel(FusedParams f) {
 }
 
 // ---- u pass: 64 rows per block, transitions and the rows' alpha-hat in LDS ----
+// When every column's transition range is <= 30, u is a dot product:
+// u[t,c] = cm[c] + log2 sum_c' 2^alpha-hat[t,c'] * 2^(tr[c',c] - cm[c]), both
+// factors <= 1 and the largest term >= 2^-30 (alpha-hat has an exact 0 at the
+// row's best label), so an underflowed 2^alpha-hat drops a term below 2^-96.
+// A thread then keeps its column's factors in registers (CP >= C of them) and
+// reads the rows' 2^alpha-hat as float4s: one FMA per pair, no exponential.
+// Otherwise each pair takes an exponential (with a first pass for the row
+// maximum when the range exceeds 64).
 constexpr int kURows = 64;
 
+template <int CP>
 __global__ void __launch_bounds__(256) u_rows_kernel(FusedParams f) {
   extern __shared__ __align__(16) char smem[];
   const int C = f.C, T = f.T;
@@ -60,13 +69,12 @@ __global__ void __launch_bounds__(256) u_rows_kernel(FusedParams f) {
   if (t0 > len) return;
   const int nr = min(kURows, len + 1 - t0);
   float* tr2 = reinterpret_cast<float*>(smem);  // [c_src][c_dst], log2 units
-  float* ah = tr2 + C * C;                       // [row][c]
-  float* cmx = ah + kURows * C;                  // [c] max over sources of tr2[., c]
+  float* ah = tr2 + C * C;                       // [row][c], row stride CP
+  float* cmx = ah + kURows * CP;                 // [c] max over sources of tr2[., c]
   float* crg = cmx + C;                          // [c] its range (max - min)
   for (int i = threadIdx.x; i < C * C; i += blockDim.x) tr2[i] = f.trans[i] * kLog2e;
-  const float* av = f.aval + ((size_t)b * (T + 1) + t0) * C;
-  for (int i = threadIdx.x; i < nr * C; i += blockDim.x) ah[i] = av[i];
   __syncthreads();
+  bool wide = false;
   for (int c = threadIdx.x; c < C; c += blockDim.x) {
     float hi = kMinusInf, lo = -kMinusInf;
     for (int cs = 0; cs < C; ++cs) {
@@ -75,12 +83,42 @@ __global__ void __launch_bounds__(256) u_rows_kernel(FusedParams f) {
     }
     cmx[c] = hi;
     crg[c] = hi - lo;
+    wide = wide || !(hi - lo <= 30.0f);
+  }
+  const bool fact = !__syncthreads_or(wide);
+  const float* av = f.aval + ((size_t)b * (T + 1) + t0) * C;
+  for (int i = threadIdx.x; i < nr * CP; i += blockDim.x) {
+    const int r = i / CP, cs = i % CP;
+    const float a = cs < C ? av[(size_t)r * C + cs] : kMinusInf;
+    ah[i] = fact ? exp2_hw(a) : a;
   }
   __syncthreads();
   float* uo = f.uval + ((size_t)b * (T + 1) + t0) * C;
+  if (fact) {
+    const int RG = blockDim.x / C;  // row groups
+    const int c = threadIdx.x % C, rg = threadIdx.x / C;
+    if (rg >= RG) return;
+    float er[CP];
+#pragma unroll
+    for (int cs = 0; cs < CP; ++cs) er[cs] = cs < C ? exp2_hw(tr2[cs * C + c] - cmx[c]) : 0.0f;
+    for (int r = rg; r < nr; r += RG) {
+      const float4* a4 = reinterpret_cast<const float4*>(ah + r * CP);
+      float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+      for (int q = 0; q < CP / 4; ++q) {
+        const float4 a = a4[q];
+        s0 = fmaf(a.x, er[4 * q], s0);
+        s1 = fmaf(a.y, er[4 * q + 1], s1);
+        s0 = fmaf(a.z, er[4 * q + 2], s0);
+        s1 = fmaf(a.w, er[4 * q + 3], s1);
+      }
+      uo[(size_t)r * C + c] = cmx[c] + log2_hw(s0 + s1);
+    }
+    return;
+  }
   for (int i = threadIdx.x; i < nr * C; i += blockDim.x) {
     const int r = i / C, c = i % C;
-    const float* a = ah + r * C;
+    const float* a = ah + r * CP;
     const float* tc = tr2 + c;
     // Shift: alpha-hat <= 0 with an exact 0 at the row's best label, so every
     // term is <= 2^cmx[c] and the largest is >= 2^(cmx[c] - crg[c]): with a
@@ -281,9 +319,17 @@ __global__ void __launch_bounds__(256) fused_shared_kernel(FusedParams f) {
 }  // namespace
 
 int launch_u_rows(const Plan& pl, const FusedParams& f, hipStream_t s) {
-  const size_t lds = sizeof(float) * ((size_t)pl.C * pl.C + (size_t)kURows * pl.C + 2 * (size_t)pl.C);
+  const int CP = pl.C <= 8 ? 8 : pl.C <= 16 ? 16 : pl.C <= 32 ? 32 : 64;
+  if (pl.C > 64) return (int)hipErrorInvalidValue;
+  const size_t lds = sizeof(float) * ((size_t)pl.C * pl.C + (size_t)kURows * CP + 2 * (size_t)pl.C);
+  const dim3 grid((pl.T + 1 + kURows - 1) / kURows, pl.B);
   TimedLaunch tl(kKURows, s);
-  hipLaunchKernelGGL(u_rows_kernel, dim3((pl.T + 1 + kURows - 1) / kURows, pl.B), dim3(256), lds, s, f);
+  switch (CP) {
+    case 8: hipLaunchKernelGGL(u_rows_kernel<8>, grid, dim3(256), lds, s, f); break;
+    case 16: hipLaunchKernelGGL(u_rows_kernel<16>, grid, dim3(256), lds, s, f); break;
+    case 32: hipLaunchKernelGGL(u_rows_kernel<32>, grid, dim3(256), lds, s, f); break;
+    default: hipLaunchKernelGGL(u_rows_kernel<64>, grid, dim3(256), lds, s, f); break;
+  }
   return hipGetLastError();
 }
 

@@ -35,6 +35,7 @@ struct ScanParams {
   double* offs;            // (B*P) frame offsets (log2 units)
   double* vstat;           // (B*P, 2) max / min of exact - speculative boundary state
   int* status;             // (B*P) 0 exact, 1 speculative+verified, 2 recomputed
+  int* vflag;              // set when the retry pass reran a chunk (the second verification is skipped otherwise)
   int32_t* recomputed;     // (B) number of recomputed chunks, or null
   // forward only: final row at position len, partition
   float* fin;              // (B, C)
@@ -197,7 +198,8 @@ int launch_fused_j16_hi(const Plan& pl, const ScanParams& p, hipStream_t s);
 int launch_u_rows(const Plan& pl, const FusedParams& f, hipStream_t s);
 int launch_fused_finalize(const Plan& pl, const FusedParams& f, hipStream_t s);
 // verification of speculative chunk boundaries / level offsets (shared by both scan paths)
-int launch_verify(const Plan& pl, const ScanParams& p, bool forward, hipStream_t s);
+// after_retry: the verification that follows the retry pass (nothing to do unless it reran a chunk)
+int launch_verify(const Plan& pl, const ScanParams& p, bool forward, hipStream_t s, bool after_retry = false);
 int launch_apply_offsets(const Plan& pl, const ScanParams& p, bool forward, hipStream_t s);
 // register-resident log-semiring scan, one entry per lane-group size (pl.FJ)
 int launch_fast_j8(const Plan& pl, const ScanParams& p, bool forward, hipStream_t s);

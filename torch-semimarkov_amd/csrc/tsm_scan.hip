@@ -516,8 +516,13 @@ struct GenericChunk {
 // where "exact" is the neighbouring chunk's end state (forward: chunk j-1,
 // backward: chunk j+1).  Entries unreachable in both (< -1e8 in log2 units) are
 // skipped: they add exactly nothing to any later sum.
-__global__ void __launch_bounds__(256) verify_kernel(ScanParams p, int forward) {
+__global__ void __launch_bounds__(256) verify_kernel(ScanParams p, int forward, int after_retry) {
   __shared__ double red[64];
+  if (after_retry) {
+    if (*p.vflag == 0) return;  // the retry pass reran nothing: the first verification stands
+  } else if (blockIdx.x == 0 && threadIdx.x == 0) {
+    *p.vflag = 0;  // the retry pass sets it when it reruns a chunk
+  }
   const int b = blockIdx.x / p.P, j = blockIdx.x % p.P;
   const int len = seq_len(p, b);
   const int item = b * p.P + j;
@@ -635,10 +640,10 @@ int launch_scan_viterbi(const Plan& pl, const ScanParams& p, hipStream_t st) {
   }
 }
 
-int launch_verify(const Plan& pl, const ScanParams& p, bool forward, hipStream_t st) {
+int launch_verify(const Plan& pl, const ScanParams& p, bool forward, hipStream_t st, bool after_retry) {
   if (pl.P > 1) {
     TimedLaunch tl(kKVerify, st);
-    hipLaunchKernelGGL(verify_kernel, dim3(pl.B * pl.P), dim3(256), 0, st, p, forward ? 1 : 0);
+    hipLaunchKernelGGL(verify_kernel, dim3(pl.B * pl.P), dim3(256), 0, st, p, forward ? 1 : 0, after_retry ? 1 : 0);
   }
   return hipGetLastError();
 }
