@@ -387,11 +387,13 @@ int make_plan(int64_t B, int64_t T, int64_t C, int64_t K, int has_ps, int has_pe
     }
   }
   // marginals fused into the backward scan: the register-resident scan with
-  // 16-lane groups (TSM_MARGINAL_PATH=separate keeps the separate kernel)
+  // 16-lane groups (TSM_MARGINAL_PATH=separate keeps the separate kernel).  (The
+  // same fusion in the cooperative scan was measured slower at cfg5: one wave
+  // per SIMD there, so the extra per-term work lands on the step's critical path.)
   p.mfused = 0;
   const char* menv = getenv("TSM_MARGINAL_PATH");
   const bool separate = menv != nullptr && strcmp(menv, "separate") == 0;
-  if (!separate && p.fast && p.FJ == 16 && p.C * p.C <= 4096) {
+  if (!separate && p.fast && p.FJ == 16) {
     p.mfused = 1;
     // transition gradient: about eight blocks per CU, at least 256 starts each
     int64_t gnb = cdiv(8 * (int64_t)di.n_cu, (int64_t)p.B);

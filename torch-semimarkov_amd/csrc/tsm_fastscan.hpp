@@ -58,19 +58,6 @@ __device__ __forceinline__ void lds_barrier() { __asm__ volatile("s_waitcnt lgkm
 // of the same words by other lanes (LDS executes a wave's operations in order).
 __device__ __forceinline__ void wave_lds_order() { __asm__ volatile("" ::: "memory"); }
 
-// a + (lane (i-1) mod 16 of the row of `rot`), one v_add_f32 with a DPP source
-// (row_ror:1).  The s_nop gives the two wait states a DPP read needs after a
-// VALU write, which the compiler does not track across inline asm.  All lanes
-// are active.
-__device__ __forceinline__ float add_row_ror1(float rot, float a) {
-  float r;
-  asm("s_nop 1\n\tv_add_f32_dpp %0, %1, %2 row_ror:1 row_mask:0xf bank_mask:0xf bound_ctrl:1"
-      : "=v"(r) : "v"(rot), "v"(a));
-  return r;
-}
-
-// CJ source labels per lane in the label mix (C <= CJ * J; the launchers pick 2
-// when C <= 2J, else 4).
 template <int J, int R, bool FWD, bool LOGSR, bool MARG = false, int CJ = 4>
 struct Chunk {
   static_assert(!MARG || (!FWD && LOGSR && J == 16), "fused marginals: backward log scan, 16-lane DPP rows");

@@ -192,7 +192,7 @@ __global__ void fused_rows_kernel(FusedParams f) {
 constexpr int kGRows = 64;
 
 template <int NPT>
-__global__ void __launch_bounds__(256) trans_grad_kernel(FusedParams f) {
+__global__ void __launch_bounds__(1024) trans_grad_kernel(FusedParams f) {
   extern __shared__ __align__(16) char smem[];
   const int C = f.C, T = f.T, Lc = f.Lc;
   const int b = blockIdx.y, blk = blockIdx.x;
@@ -318,33 +318,52 @@ __global__ void __launch_bounds__(256) fused_shared_kernel(FusedParams f) {
 
 }  // namespace
 
+template <int CP>
+int launch_u_cp(const FusedParams& f, dim3 grid, size_t lds, hipStream_t s) {
+  const hipError_t e = hipFuncSetAttribute((const void*)u_rows_kernel<CP>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(u_rows_kernel<CP>, grid, dim3(256), lds, s, f);
+  return hipSuccess;
+}
+
 int launch_u_rows(const Plan& pl, const FusedParams& f, hipStream_t s) {
-  const int CP = pl.C <= 8 ? 8 : pl.C <= 16 ? 16 : pl.C <= 32 ? 32 : 64;
-  if (pl.C > 64) return (int)hipErrorInvalidValue;
+  const int CP = pl.C <= 8 ? 8 : pl.C <= 16 ? 16 : pl.C <= 32 ? 32 : pl.C <= 64 ? 64 : 128;
+  if (pl.C > 128) return (int)hipErrorInvalidValue;
   const size_t lds = sizeof(float) * ((size_t)pl.C * pl.C + (size_t)kURows * CP + 2 * (size_t)pl.C);
   const dim3 grid((pl.T + 1 + kURows - 1) / kURows, pl.B);
   TimedLaunch tl(kKURows, s);
+  int e;
   switch (CP) {
-    case 8: hipLaunchKernelGGL(u_rows_kernel<8>, grid, dim3(256), lds, s, f); break;
-    case 16: hipLaunchKernelGGL(u_rows_kernel<16>, grid, dim3(256), lds, s, f); break;
-    case 32: hipLaunchKernelGGL(u_rows_kernel<32>, grid, dim3(256), lds, s, f); break;
-    default: hipLaunchKernelGGL(u_rows_kernel<64>, grid, dim3(256), lds, s, f); break;
+    case 8: e = launch_u_cp<8>(f, grid, lds, s); break;
+    case 16: e = launch_u_cp<16>(f, grid, lds, s); break;
+    case 32: e = launch_u_cp<32>(f, grid, lds, s); break;
+    case 64: e = launch_u_cp<64>(f, grid, lds, s); break;
+    default: e = launch_u_cp<128>(f, grid, lds, s); break;
   }
+  if (e != hipSuccess) return e;
   return hipGetLastError();
 }
 
 template <int NPT>
-void launch_trans_grad(const Plan& pl, const FusedParams& f, hipStream_t s) {
+int launch_trans_grad(const Plan& pl, const FusedParams& f, hipStream_t s) {
   const size_t lds = sizeof(float) * (2 * (size_t)kGRows * pl.C + kGRows + pl.C);
+  const hipError_t e = hipFuncSetAttribute((const void*)trans_grad_kernel<NPT>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (e != hipSuccess) return e;
   const int np = pl.C * pl.C;
   int nt = (np + NPT - 1) / NPT;
-  nt = std::max(64, std::min(256, (nt + 63) / 64 * 64));
+  nt = std::max(64, std::min(1024, (nt + 63) / 64 * 64));
   hipLaunchKernelGGL(trans_grad_kernel<NPT>, dim3(pl.GNB, pl.B), dim3(nt), lds, s, f);
+  return hipSuccess;
 }
 
 int launch_fused_finalize(const Plan& pl, const FusedParams& f, hipStream_t s) {
-  const int npt = (pl.C * pl.C + 255) / 256;  // pairs per thread with 256 threads
-  if (npt > 16) return (int)hipErrorInvalidValue;
+  // pairs per thread: with 256 threads up to 16; above C*C = 4096 (C <= 128) 16 pairs
+  // per thread on up to 1024 threads
+  const int np = pl.C * pl.C;
+  const int npt = np <= 4096 ? (np + 255) / 256 : 16;
+  if (np > 16 * 1024) return (int)hipErrorInvalidValue;
   {
     const int n = pl.B * pl.P;
     hipLaunchKernelGGL(frame_scale_kernel, dim3((n + 255) / 256), dim3(256), 0, s, f);
@@ -357,12 +376,14 @@ int launch_fused_finalize(const Plan& pl, const FusedParams& f, hipStream_t s) {
   }
   {
     TimedLaunch tl(kKTransGrad, s);
-    if (npt <= 1) launch_trans_grad<1>(pl, f, s);
-    else if (npt <= 2) launch_trans_grad<2>(pl, f, s);
-    else if (npt <= 3) launch_trans_grad<3>(pl, f, s);
-    else if (npt <= 4) launch_trans_grad<4>(pl, f, s);
-    else if (npt <= 8) launch_trans_grad<8>(pl, f, s);
-    else launch_trans_grad<16>(pl, f, s);
+    int e;
+    if (npt <= 1) e = launch_trans_grad<1>(pl, f, s);
+    else if (npt <= 2) e = launch_trans_grad<2>(pl, f, s);
+    else if (npt <= 3) e = launch_trans_grad<3>(pl, f, s);
+    else if (npt <= 4) e = launch_trans_grad<4>(pl, f, s);
+    else if (npt <= 8) e = launch_trans_grad<8>(pl, f, s);
+    else e = launch_trans_grad<16>(pl, f, s);
+    if (e != hipSuccess) return e;
   }
   {
     TimedLaunch tl(kKFusedShared, s);
