@@ -225,12 +225,16 @@ def bench_viterbi(args):
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    N.timing_enable(True)  # per-kernel HIP events on the launch stream
     t0 = time.perf_counter()
     for _ in range(args.steps):
         out = step()
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    # per-kernel HIP events on the launch stream, over the same steps again (outside the timed region)
+    N.timing_enable(True)
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
     ktimes = N.timing_read()
     N.timing_enable(False)
     cells_sum = int(lengths.sum()) * K * C * C
@@ -372,13 +376,19 @@ def main():
     for _ in range(args.warmup):
         step(False)
     torch.cuda.synchronize()
-    # per-kernel HIP events, recorded by the library on the stream each kernel runs on
-    N.timing_enable(True)
+    # the timed region (value): K steps, without the library's per-kernel events
     t0 = time.perf_counter()
     for _ in range(args.steps):
         part = step(True)
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
+    # the same K steps again with per-kernel HIP events, recorded by the library on
+    # the stream each kernel runs on (kernel_avg_ms, roofline); the events add about
+    # 1 % to the step, so they stay out of the timed region above
+    N.timing_enable(True)
+    for _ in range(args.steps):
+        step(False)
+    torch.cuda.synchronize()
     ktimes = N.timing_read()
     N.timing_enable(False)
     ms_step = dt * 1e3 / args.steps

@@ -429,6 +429,8 @@ FUSED_CASES = [
     (2, 6000, 280, 12, [6000, 4117], True),        # long durations, few labels, projections
     (1, 1800, 64, 64, None, False),                # 64 labels: 4096 transition pairs
     (2, 2080, 33, 48, [2080, 1040], False),        # lengths that are multiples of the chunk length
+    (2, 700, 1, 40, [700, 333], False),            # one duration: every position is a boundary
+    (1, 900, 2, 36, None, True),                   # K = 2 (one register per lane, 15 padded lanes)
 ]
 
 
