@@ -63,7 +63,8 @@ const char* tsm_last_error(void);
  * `n` int64 host values: J, NT, RS, P, Lc, W, global_rings, scan_lds, NB, TB,
  * CB, NCB, JM, NTM, marg_lds, Kmax, n_cu, R, KP, RMAX, fast, FJ, FR, FNT,
  * fast_lds, mfast, MR, dense, DJ, DNT, dtrl, dense_lds, DG, DNTM, DNB, DTB,
- * dmarg_lds, coop, CG, CCL, CR, CNQ, coop_lds, mfused, GNB, GTB (fast = 1: log-semiring scans use
+ * dmarg_lds, coop, CG, CCL, CR, CNQ, coop_lds, mfused, GNB, GTB, P2, Lc2, FRL2, fast_lds2,
+ * dualF, dualB, dualV, regsF, regsB, regsV (fast = 1: log-semiring scans use
  * the register-resident kernels with
  * FJ lanes per label and FR durations per lane; mfast = 1: the marginals use
  * the register-resident kernel with MR durations per lane; the environment
@@ -74,7 +75,12 @@ const char* tsm_last_error(void);
  * with CCL labels each and CR durations per lane, CNQ co-resident groups;
  * mfused = 1: the log-semiring backward computes the segment marginals inside
  * the register-resident beta scan, transition gradient in GNB row blocks of GTB
- * starts per sequence; TSM_MARGINAL_PATH=separate turns it off).
+ * starts per sequence; TSM_MARGINAL_PATH=separate turns it off; dualF / dualB /
+ * dualV = 1: the log forward / the log backward with separate marginals / the
+ * factorised Viterbi forward run two chunks per CU, P2 chunks of Lc2 positions
+ * with rings of FRL2 entries (fast_lds2 bytes), because their kernels use
+ * regsF / regsB / regsV VGPRs, few enough for two workgroups per CU; -1 = not
+ * queried).
  */
 int tsm_plan_info(int64_t B, int64_t T, int64_t C, int64_t K, int64_t trans_rows, int has_proj_start,
                   int has_proj_end, int64_t* out, int n);

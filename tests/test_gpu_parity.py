@@ -509,6 +509,65 @@ def test_fused_backward_recomputes_non_mixing_chunks(monkeypatch):
     assert_grads(grads, g64)
 
 
+@pytest.mark.parametrize("marginals", ["fused", "separate"])
+def test_two_chunks_per_cu_vs_fp64_oracle(marginals, monkeypatch):
+    """Scan directions whose kernels leave registers for a second workgroup on
+    every SIMD run two chunks per CU, with shorter rings (compacted every 96
+    steps here) and a chunk count of their own; the fused backward keeps one
+    chunk per CU.  TSM_SCAN_CHUNKS=dual takes that chunking on a problem the
+    oracle can check, with the headline's lane layout (C=24, 19 durations per
+    lane): the forward in two chunks and, with separate marginals, the beta scan
+    too."""
+    monkeypatch.delenv("TSM_SCAN_PATH", raising=False)
+    monkeypatch.setenv("TSM_SCAN_CHUNKS", "dual")
+    if marginals == "separate":
+        monkeypatch.setenv("TSM_MARGINAL_PATH", "separate")
+    else:
+        monkeypatch.delenv("TSM_MARGINAL_PATH", raising=False)
+    B, T, K, C = 2, 2400, 300, 24
+    info = N.plan_info(B, T, C, K)
+    assert info["dualF"] == 1 and info["P2"] == 2 * info["P"], info
+    assert 0 < info["regsF"] <= 128 and 2 * info["fast_lds2"] <= 160 * 1024, info
+    if marginals == "separate":
+        assert info["mfused"] == 0 and info["dualB"] == 1, info
+    else:
+        assert info["mfused"] == 1 and info["dualB"] == 0, info
+    cum, tr, db, L, _, _ = rand_problem(B, T, K, C, 4242, [2400, 1333])
+    g = torch.tensor([0.75, 1.5])
+    p64, g64 = oracle_fp64(cum, tr, db, L, K, "log", None, None, g)
+    part, grads = run_hip(cum, tr, db, L, K, "log", None, None, g)
+    np.testing.assert_allclose(part.double().numpy(), p64.numpy(), rtol=RTOL_Z)
+    assert_grads(grads, g64)
+
+
+def test_two_chunks_per_cu_full_size_config3(monkeypatch):
+    """At the headline size (B=1, T=10^6, C=24, K=300) the log forward runs two
+    chunks per CU (its kernel fits in 128 VGPRs); its partition and alpha
+    table match the plan with one chunk per CU (TSM_SCAN_CHUNKS=single) up to
+    the speculative chunks' verification tolerance (2e-4 in log2 units)."""
+    monkeypatch.delenv("TSM_SCAN_PATH", raising=False)
+    monkeypatch.delenv("TSM_SCAN_CHUNKS", raising=False)
+    B, T, C, K = 1, 1_000_000, 24, 300
+    info = N.plan_info(B, T, C, K)
+    assert info["dualF"] == 1 and info["P2"] == 2 * info["P"] and 0 < info["regsF"] <= 128, info
+    g = torch.Generator().manual_seed(20261203)
+    em = torch.randn(B, T, C, generator=g)
+    tr = 0.1 * torch.randn(C, C, generator=g)
+    db = 0.1 * torch.randn(K, C, generator=g)
+    cum = torch.zeros(B, T + 1, C)
+    cum[:, 1:] = torch.cumsum(em, dim=1)
+    L = torch.full((B,), T, dtype=torch.long)
+    args = [x.to(DEV) for x in (cum, tr, db, L)]
+    with torch.no_grad():
+        _, z2, ah, al, _ = ops.scan_forward(*args, K, 0, None, None, True)
+        monkeypatch.setenv("TSM_SCAN_CHUNKS", "single")
+        assert N.plan_info(B, T, C, K)["dualF"] == 0
+        _, z1, bh, bl, _ = ops.scan_forward(*args, K, 0, None, None, True)
+        np.testing.assert_allclose(z2.cpu().numpy(), z1.cpu().numpy(), rtol=RTOL_Z)
+        d = ((ah.double() + al.unsqueeze(-1)) - (bh.double() + bl.unsqueeze(-1))).abs().max().item()
+    assert d <= 1e-3, d
+
+
 def test_fused_backward_full_size_config3(monkeypatch):
     """The headline configuration (B=1, T=10^6, C=24, K=300): the fused backward
     against the separate marginal kernel (itself checked against the oracle

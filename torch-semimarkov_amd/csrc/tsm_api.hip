@@ -104,20 +104,23 @@ void plan_fast(Plan& p, const DeviceInfo& di) {
     const int RS = p.Kmax + 2;  // levels of the positions a step reads (pos % RS)
     // linear ring of RL > KP entries, compacted every RL - KP steps: about 2*KP+1
     // entries, fewer when LDS is short (at least 32 steps between compactions).
-    // (Shrinking it further so that two long chunks share a CU was measured at
-    // cfg3: the same steps per CU per second and twice the warm-up share.)
     // RL % 32 == J % 32 puts the label rows of a half-wave on distinct banks.
     auto ring_fits = [&](int rl, int per) { return (size_t)per * tsm::fast_lds_layout(p.C, rl, RS).total <= (size_t)di.max_lds; };
     auto bank_down = [&](int rl) { while (rl > 0 && rl % 32 != J % 32) --rl; return rl; };
-    int RL = bank_down(2 * KP + 1 + 31);
-    if (!ring_fits(RL, 1)) {
-      int hi = RL;
-      while (hi > KP && !ring_fits(hi, 1)) --hi;
-      hi = bank_down(hi);
-      if (hi < KP + 33) continue;
-      RL = hi;
-    }
+    // the longest ring (<= 2*KP+1 entries) of which `per` fit one CU, 0 if none does
+    auto ring_for = [&](int per) {
+      int rl = bank_down(2 * KP + 1 + 31);
+      if (ring_fits(rl, per)) return rl;
+      while (rl > KP && !ring_fits(rl, per)) --rl;
+      rl = bank_down(rl);
+      return rl < KP + 33 ? 0 : rl;
+    };
+    const int RL = ring_for(1);
+    if (RL == 0) continue;
     const size_t lds = tsm::fast_lds_layout(p.C, RL, RS).total;
+    // rings for two chunks per CU (used when the compiled kernel also leaves
+    // registers for a second workgroup)
+    const int RL2 = ring_for(2);
     const double cost = (double)((NT / 64 + 3) / 4) * (R + 12);  // waves per SIMD x work per wave
     if (cost < best) {
       best = cost;
@@ -128,6 +131,8 @@ void plan_fast(Plan& p, const DeviceInfo& di) {
       p.FRS = RS;
       p.FRL = RL;
       p.fast_lds = lds;
+      p.FRL2 = RL2;
+      p.fast_lds2 = RL2 > 0 ? tsm::fast_lds_layout(p.C, RL2, RS).total : 0;
     }
   }
 }
@@ -401,8 +406,57 @@ int make_plan(int64_t B, int64_t T, int64_t C, int64_t K, int has_ps, int has_pe
     p.GTB = (int)cdiv(T, gnb);
     p.GNB = (int)cdiv(T, p.GTB);
   }
+  // Two chunks per CU with the smaller rings, for each fast scan direction whose
+  // kernel allows it.  A second workgroup is placed on a CU only when every SIMD
+  // has registers for the waves the workgroup puts on it (a six-wave workgroup
+  // puts two on a SIMD, so at most 128 VGPRs); otherwise the two would run one
+  // after the other, with twice the warm-up.  TSM_SCAN_CHUNKS=single turns this
+  // off; =dual (tests) takes twice the chunks of the plan whenever the sequence
+  // has room for them, so that small problems exercise the same path.
+  p.regsF = p.regsB = p.regsV = -1;
+  const char* cenv = getenv("TSM_SCAN_CHUNKS");
+  const bool single = cenv != nullptr && strcmp(cenv, "single") == 0;
+  const bool force = cenv != nullptr && strcmp(cenv, "dual") == 0;
+  if (p.fast && p.FRL2 > 0 && !single) {
+    const int64_t min_lc = std::max<int64_t>(4 * (int64_t)p.W, 128);
+    int64_t P2 = cdiv(2 * (int64_t)di.n_cu, B);
+    P2 = std::max<int64_t>(1, std::min<int64_t>(P2, std::max<int64_t>(1, T / min_lc)));
+    if (force) P2 = std::min<int64_t>(2 * (int64_t)p.P, std::max<int64_t>(1, T / (2 * (int64_t)p.Kmax)));
+    if (P2 > p.P) {
+      Plan q = p;
+      q.FRL = p.FRL2;
+      q.fast_lds = p.fast_lds2;
+      auto pair_fits = [&](int regs) {
+        if (regs <= 0) return 0;
+        const int alloc = (regs + 7) / 8 * 8;
+        const int per_simd = (p.FNT / 64 + 3) / 4;
+        return 2 * per_simd * alloc <= 512 ? 1 : 0;
+      };
+      p.regsF = tsm::fast_scan_regs(q, 0);
+      p.regsB = tsm::fast_scan_regs(q, 1);
+      p.regsV = tsm::fast_scan_regs(q, 2);
+      p.dualF = pair_fits(p.regsF);
+      p.dualB = p.mfused ? 0 : pair_fits(p.regsB);
+      p.dualV = pair_fits(p.regsV);
+      if (p.dualF || p.dualB || p.dualV) {
+        p.P2 = (int)P2;
+        p.Lc2 = (int)cdiv(T, P2);
+      }
+    }
+  }
+  if (p.P2 == 0) p.dualF = p.dualB = p.dualV = 0;
   *out = p;
   return TSM_OK;
+}
+
+// The plan of a fast scan direction that runs two chunks per CU.
+Plan dual_plan(const Plan& pl) {
+  Plan q = pl;
+  q.P = pl.P2;
+  q.Lc = pl.Lc2;
+  q.FRL = pl.FRL2;
+  q.fast_lds = pl.fast_lds2;
+  return q;
 }
 
 // Bump allocator over the caller's workspace (256-byte aligned pieces).
@@ -428,9 +482,10 @@ struct ScanWs {
   int* xabort;
 };
 
+// (Sized for the larger of the plan's two chunkings, so that either fits.)
 ScanWs carve_scan(Carver& cv, const Plan& p) {
   ScanWs w;
-  const size_t items = (size_t)p.B * p.P;
+  const size_t items = (size_t)p.B * std::max(p.P, p.P2);
   w.st_spec = cv.take<float>(items * p.Kmax * p.C);
   w.st_end = cv.take<float>(items * p.Kmax * p.C);
   w.lv_spec = cv.take<double>(items * p.Kmax);
@@ -676,7 +731,8 @@ int tsm_plan_info(int64_t B, int64_t T, int64_t C, int64_t K, int64_t trans_rows
                           p.fast, p.FJ, p.FR, p.FNT, (int64_t)p.fast_lds, p.mfast, p.MR,
                           p.dense, p.DJ, p.DNT, p.dtrl, (int64_t)p.dense_lds, p.DG, p.DNTM, p.DNB, p.DTB,
                           (int64_t)p.dmarg_lds, p.coop, p.CG, p.CCL, p.CR, p.CNQ, (int64_t)p.coop_lds,
-                          p.mfused, p.GNB, p.GTB};
+                          p.mfused, p.GNB, p.GTB, p.P2, p.Lc2, p.FRL2, (int64_t)p.fast_lds2, p.dualF, p.dualB,
+                          p.dualV, p.regsF, p.regsB, p.regsV};
   const int m = (int)(sizeof(vals) / sizeof(vals[0]));
   for (int i = 0; i < n && i < m; ++i) out[i] = vals[i];
   return TSM_OK;
@@ -708,6 +764,7 @@ int tsm_forward(const float* cum, const float* tr, const float* db, const int64_
   const size_t need = forward_ws_bytes(pl);
   if (!workspace || ws_bytes < need)
     return fail(TSM_ERR_WORKSPACE, "forward workspace too small: %zu < %zu bytes", ws_bytes, need);
+  if (semiring == TSM_SEMIRING_LOG && pl.dualF) pl = dual_plan(pl);
   Carver cv(workspace);
   ScanWs w = carve_scan(cv, pl);
   const DenseTr dt = carve_dense(cv, pl);
@@ -758,6 +815,7 @@ int tsm_backward(const float* cum, const float* tr, const float* db, const int64
     return fail(TSM_ERR_WORKSPACE, "backward workspace too small: %zu < %zu bytes", ws_bytes, need);
   hipStream_t st = (hipStream_t)stream;
   if (semiring != TSM_SEMIRING_LOG) pl.mfused = 0;  // max semiring: the separate marginals
+  if (semiring == TSM_SEMIRING_LOG && !pl.mfused && pl.dualB) pl = dual_plan(pl);
   Carver cv(workspace);
   const BwdWs bw = carve_backward(cv, pl);
   const ScanWs& w = bw.scan;
@@ -924,6 +982,7 @@ int tsm_viterbi(const float* cum, const float* tr, const float* db, const int64_
     const size_t need = viterbi_ws_bytes(pl, with_tb);
     if (!workspace || ws_bytes < need)
       return fail(TSM_ERR_WORKSPACE, "viterbi workspace too small: %zu < %zu bytes", ws_bytes, need);
+    if (pl.dualV) pl = dual_plan(pl);
     Carver cv(workspace);
     int32_t* bp = with_tb ? cv.take<int32_t>((size_t)pl.B * (pl.T + 1) * pl.C) : nullptr;
     cv.take<int32_t>(pl.B);

@@ -175,6 +175,13 @@ int launch_chunk_dir(const Plan& pl, const ScanParams& p, size_t lds, int nthrea
   auto k = chunk_scan_kernel<CH>;
   auto kr = chunk_retry_kernel<CH>;
   auto kf = chunk_fixup_kernel<CH>;
+  if (p.query_regs != nullptr) {
+    hipFuncAttributes a;
+    const hipError_t qe = hipFuncGetAttributes(&a, (const void*)k);
+    *p.query_regs = qe == hipSuccess ? a.numRegs : -1;
+    (void)hipGetLastError();
+    return hipSuccess;
+  }
   hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return e;
   e = hipFuncSetAttribute((const void*)kr, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);

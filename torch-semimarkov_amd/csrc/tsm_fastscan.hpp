@@ -111,12 +111,13 @@ struct Chunk {
     }
 
     // ---- per-lane constants ----
-    double dbr[R];
+    // duration bias in log2 units: fp32 products, widened to fp64 where they are used
+    float dbr[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int k = 1 + lj + J * r;
       const int di = k < K - 1 ? k : K - 1;
-      dbr[r] = (k <= Kmax) ? (double)(p.db[(size_t)di * C + c] * kLog2e) : kInvD;
+      dbr[r] = (k <= Kmax) ? p.db[(size_t)di * C + c] * kLog2e : (float)kInvD;
     }
     float trr[kCJ];
 #pragma unroll
@@ -134,7 +135,7 @@ struct Chunk {
     bool lane_exact = false;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const double d = dbr[r] - dbr[0];
+      const double d = (double)dbr[r] - (double)dbr[0];
       edb[r] = exp2_hw((float)d);
       lane_exact = lane_exact || (d > 64.0);
     }
@@ -367,7 +368,7 @@ struct Chunk {
       float a2;
       int kbest = 0;
       if constexpr (LOGSR) {
-        double y0 = e[0] + dbr[0];
+        double y0 = e[0] + (double)dbr[0];
         float s0 = 1.0f, s1 = 0.0f;
         float tm[MARG ? R : 1];  // MARG: the lane's terms 2^(x + db - y0)
         if constexpr (MARG) tm[0] = 1.0f;
@@ -386,14 +387,23 @@ struct Chunk {
         float s = s0 + s1;
         // overflow (inf, or inf * 0 = NaN on a padded duration) or extreme factors
         if (__ballot(!(s <= FLT_MAX) || lane_exact)) {
-          // a later term exceeds the first by more than the fp32 exponent range
+          // a later term exceeds the first by more than the fp32 exponent range.
+          // The fp64 biases are widened here from opaque copies: widened outside the
+          // step loop they would hold 2R registers throughout.
+          double ey[R];
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            float dv = dbr[r];
+            __asm__ volatile("" : "+v"(dv));
+            ey[r] = e[r] + (double)dv;
+          }
           double m = y0;
 #pragma unroll
-          for (int r = 1; r < R; ++r) m = fmax(m, e[r] + dbr[r]);
+          for (int r = 1; r < R; ++r) m = fmax(m, ey[r]);
           s = 0.0f;
 #pragma unroll
           for (int r = 0; r < R; ++r) {
-            const float q = exp2_hw((float)((e[r] + dbr[r]) - m));
+            const float q = exp2_hw((float)(ey[r] - m));
             if constexpr (MARG) tm[r] = q;
             s += q;
           }
@@ -447,11 +457,11 @@ struct Chunk {
         }
       } else {
         // max over durations; ties go to the smallest duration (lanes hold ascending k)
-        double ym = e[0] + dbr[0];
+        double ym = e[0] + (double)dbr[0];
         int km = 1 + lj;
 #pragma unroll
         for (int r = 1; r < R; ++r) {
-          const double y = e[r] + dbr[r];
+          const double y = e[r] + (double)dbr[r];
           if (y > ym) {
             ym = y;
             km = 1 + lj + J * r;

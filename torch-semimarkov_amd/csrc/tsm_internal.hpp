@@ -36,6 +36,7 @@ struct ScanParams {
   double* vstat;           // (B*P, 2) max / min of exact - speculative boundary state
   int* status;             // (B*P) 0 exact, 1 speculative+verified, 2 recomputed
   int* vflag;              // set when the retry pass reran a chunk (the second verification is skipped otherwise)
+  int* query_regs;         // plan time: the launch stores its scan kernel's VGPR count here and launches nothing
   int32_t* recomputed;     // (B) number of recomputed chunks, or null
   // forward only: final row at position len, partition
   float* fin;              // (B, C)
@@ -191,6 +192,10 @@ struct PrologueParams {
 // launchers (return hipError_t as int)
 int launch_scan_forward(const Plan& pl, const ScanParams& p, int semiring, hipStream_t s);
 int launch_scan_backward(const Plan& pl, const ScanParams& p, int semiring, hipStream_t s);
+// VGPRs of the register-resident scan kernel a launch with this plan would use
+// (kind 0: log forward, 1: log backward with separate marginals, 2: Viterbi
+// forward), -1 when unknown
+int fast_scan_regs(const Plan& pl, int kind);
 // backward log scan with fused marginals (pl.mfused), and its row passes
 int launch_scan_backward_fused(const Plan& pl, const ScanParams& p, hipStream_t s);
 int launch_fused_j16_lo(const Plan& pl, const ScanParams& p, hipStream_t s);

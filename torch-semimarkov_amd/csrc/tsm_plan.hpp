@@ -30,6 +30,13 @@ struct Plan {
   // FRS level slots, FRL ring length per label (fp64 entries), fast_lds bytes
   int fast, FJ, FR, FNT, FRS, FRL;
   size_t fast_lds;
+  // Two chunks per CU for a fast scan direction whose compiled instance leaves
+  // room for a second workgroup on every SIMD: P2 chunks of Lc2 positions per
+  // sequence, rings of FRL2 entries (fast_lds2 bytes).  dualF / dualB / dualV: the
+  // log forward, the log backward with separate marginals and the Viterbi
+  // forward run with them; regsF / regsB / regsV: those instances' VGPRs.
+  int P2, Lc2, FRL2, dualF, dualB, dualV, regsF, regsB, regsV;
+  size_t fast_lds2;
   // register-resident marginal kernel (mfast == 1): 16 lanes per label, MR
   // durations per lane, one wavefront of 4 labels per workgroup, ring slots /
   // row length.  NB, TB, CB, NCB and marg_lds above then describe its blocking.

@@ -669,6 +669,19 @@ int launch_scan_backward_fused(const Plan& pl, const ScanParams& p, hipStream_t 
   return pl.FR <= 16 ? launch_fused_j16_lo(pl, q, st) : launch_fused_j16_hi(pl, q, st);
 }
 
+int fast_scan_regs(const Plan& pl, int kind) {
+  int regs = -1;
+  ScanParams q{};
+  q.B = pl.B;
+  q.T = pl.T;
+  q.C = pl.C;
+  q.K = pl.K;
+  q.Kmax = pl.Kmax;
+  q.query_regs = &regs;
+  const int e = kind == 2 ? launch_scan_viterbi(pl, q, nullptr) : launch_fast(pl, q, kind == 0, nullptr);
+  return e == hipSuccess ? regs : -1;
+}
+
 int launch_scan_forward(const Plan& pl, const ScanParams& p, int semiring, hipStream_t s) {
   return launch_any(pl, p, semiring, true, s);
 }

@@ -32,6 +32,7 @@ PLAN_FIELDS = (
     "dense", "DJ", "DNT", "dtrl", "dense_lds", "DG", "DNTM", "DNB", "DTB", "dmarg_lds",
     "coop", "CG", "CCL", "CR", "CNQ", "coop_lds",
     "mfused", "GNB", "GTB",
+    "P2", "Lc2", "FRL2", "fast_lds2", "dualF", "dualB", "dualV", "regsF", "regsB", "regsV",
 )
 
 _p = ctypes.c_void_p
