@@ -647,6 +647,22 @@ def test_viterbi_factorised_vs_fp64_optimum(B, T, K, C, lengths, tie_free):
     permuted at equal total), so the segmentation itself is compared bit-exactly
     on tie-free inputs, where self-transitions are penalised out of every optimum.
     The multi-chunk case exercises speculation in the max semiring."""
+    _viterbi_factorised_check(B, T, K, C, lengths, tie_free)
+
+
+def test_viterbi_factorised_two_chunks_per_cu(monkeypatch):
+    """The factorised Viterbi forward with two chunks per CU (shorter rings, its
+    own chunk count; TSM_SCAN_CHUNKS=dual on a problem the oracle can check,
+    with the headline's lane layout: C=24, 19 durations per lane): the same
+    checks as above on tie-free inputs."""
+    monkeypatch.setenv("TSM_SCAN_CHUNKS", "dual")
+    B, T, K, C = 2, 2400, 300, 24
+    info = N.plan_info(B, T, C, K)
+    assert info["dualV"] == 1 and info["P2"] == 2 * info["P"] and 0 < info["regsV"] <= 128, info
+    _viterbi_factorised_check(B, T, K, C, [2400, 1333], True)
+
+
+def _viterbi_factorised_check(B, T, K, C, lengths, tie_free):
     cum, tr, db, L, _, _ = rand_problem(B, T, K, C, 57 + C, lengths, tscale=0.5, dscale=0.5)
     if tie_free:
         tr = tr - 30.0 * torch.eye(C)

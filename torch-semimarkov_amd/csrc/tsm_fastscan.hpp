@@ -456,12 +456,16 @@ struct Chunk {
           }
         }
       } else {
-        // max over durations; ties go to the smallest duration (lanes hold ascending k)
+        // max over durations; ties go to the smallest duration (lanes hold ascending k).
+        // The fp64 biases are widened here from opaque copies (one conversion per
+        // term): widened outside the step loop they would hold 2R registers.
         double ym = e[0] + (double)dbr[0];
         int km = 1 + lj;
 #pragma unroll
         for (int r = 1; r < R; ++r) {
-          const double y = e[r] + (double)dbr[r];
+          float dv = dbr[r];
+          __asm__ volatile("" : "+v"(dv));
+          const double y = e[r] + (double)dv;
           if (y > ym) {
             ym = y;
             km = 1 + lj + J * r;
