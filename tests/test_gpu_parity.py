@@ -526,7 +526,7 @@ def test_two_chunks_per_cu_vs_fp64_oracle(marginals, monkeypatch):
         monkeypatch.delenv("TSM_MARGINAL_PATH", raising=False)
     B, T, K, C = 2, 2400, 300, 24
     info = N.plan_info(B, T, C, K)
-    assert info["dualF"] == 1 and info["P2"] == 2 * info["P"], info
+    assert info["dualF"] == 1 and info["P2"] > info["P"], info
     assert 0 < info["regsF"] <= 128 and 2 * info["fast_lds2"] <= 160 * 1024, info
     if marginals == "separate":
         assert info["mfused"] == 0 and info["dualB"] == 1, info
@@ -658,7 +658,7 @@ def test_viterbi_factorised_two_chunks_per_cu(monkeypatch):
     monkeypatch.setenv("TSM_SCAN_CHUNKS", "dual")
     B, T, K, C = 2, 2400, 300, 24
     info = N.plan_info(B, T, C, K)
-    assert info["dualV"] == 1 and info["P2"] == 2 * info["P"] and 0 < info["regsV"] <= 128, info
+    assert info["dualV"] == 1 and info["P2"] > info["P"] and 0 < info["regsV"] <= 128, info
     _viterbi_factorised_check(B, T, K, C, [2400, 1333], True)
 
 

@@ -52,8 +52,11 @@ def test_plan_and_workspace_queries_without_gpu():
     assert p["RS"] >= p["Kmax"] + 2 and p["RS"] % 32 == 16
     assert p["P"] > 1 and p["Lc"] * p["P"] >= 1_000_000 and p["Lc"] >= 4 * p["W"]
     assert p["TB"] >= p["Kmax"] and p["NB"] * p["TB"] >= 1_000_000
-    # small problems run exactly in one chunk
-    assert N.plan_info(4, 1000, 24, 100)["P"] == 1
+    # few short sequences leave most CUs idle: chunks of about one warm-up each
+    s = N.plan_info(4, 1000, 24, 100)
+    assert s["P"] == 1000 // s["W"] and s["Lc"] >= s["W"], s
+    # a sequence shorter than two warm-ups runs in one chunk
+    assert N.plan_info(4, 300, 24, 100)["P"] == 1
     # large label spaces split the marginal kernel into label blocks
     q = N.plan_info(8, 50_000, 128, 500)
     assert q["CB"] * q["NCB"] >= 128 and q["marg_lds"] <= 160 * 1024

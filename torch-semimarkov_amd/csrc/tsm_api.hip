@@ -284,11 +284,17 @@ int make_plan(int64_t B, int64_t T, int64_t C, int64_t K, int has_ps, int has_pe
   p.RMAX = (!p.global_rings && p.R <= 32) ? 32 : 0;
   p.scan_lds = lds;
   // chunking: about one work item per CU; chunks long enough that the warm-up
-  // (W steps) costs at most ~25%.
+  // (W steps) costs at most ~25%.  When that leaves most CUs idle (few, short
+  // sequences), a chunk's step count is the time: chunks down to one warm-up
+  // long, about 2W steps each instead of up to T.
   p.W = p.Kmax + 64;
   const int64_t min_lc = std::max<int64_t>(4 * (int64_t)p.W, 128);
   int64_t P = cdiv(di.n_cu, B);
   P = std::min<int64_t>(P, std::max<int64_t>(1, T / min_lc));
+  if (B * P * 2 <= di.n_cu) {
+    const int64_t short_lc = std::max<int64_t>(p.W, 128);
+    P = std::min<int64_t>(cdiv(di.n_cu, B), std::max<int64_t>(1, T / short_lc));
+  }
   P = std::max<int64_t>(P, 1);
   p.P = (int)P;
   p.Lc = (int)cdiv(T, P);
@@ -411,8 +417,8 @@ int make_plan(int64_t B, int64_t T, int64_t C, int64_t K, int has_ps, int has_pe
   // has registers for the waves the workgroup puts on it (a six-wave workgroup
   // puts two on a SIMD, so at most 128 VGPRs); otherwise the two would run one
   // after the other, with twice the warm-up.  TSM_SCAN_CHUNKS=single turns this
-  // off; =dual (tests) takes twice the chunks of the plan whenever the sequence
-  // has room for them, so that small problems exercise the same path.
+  // off; =dual (tests) takes up to twice the chunks of the plan, each at least
+  // Kmax+1 positions long, so that small problems exercise the same path.
   p.regsF = p.regsB = p.regsV = -1;
   const char* cenv = getenv("TSM_SCAN_CHUNKS");
   const bool single = cenv != nullptr && strcmp(cenv, "single") == 0;
@@ -421,7 +427,7 @@ int make_plan(int64_t B, int64_t T, int64_t C, int64_t K, int has_ps, int has_pe
     const int64_t min_lc = std::max<int64_t>(4 * (int64_t)p.W, 128);
     int64_t P2 = cdiv(2 * (int64_t)di.n_cu, B);
     P2 = std::max<int64_t>(1, std::min<int64_t>(P2, std::max<int64_t>(1, T / min_lc)));
-    if (force) P2 = std::min<int64_t>(2 * (int64_t)p.P, std::max<int64_t>(1, T / (2 * (int64_t)p.Kmax)));
+    if (force) P2 = std::min<int64_t>(2 * (int64_t)p.P, std::max<int64_t>(1, T / ((int64_t)p.Kmax + 1)));
     if (P2 > p.P) {
       Plan q = p;
       q.FRL = p.FRL2;

@@ -26,6 +26,10 @@
 // handles durations k = 1+j, 1+j+J, ...  Rings are laid out [c][slot] so the J
 // lanes of a label read consecutive LDS words.
 
+#include <map>
+#include <mutex>
+#include <tuple>
+
 #include "tsm_device.hpp"
 #include "tsm_internal.hpp"
 #include "tsm_chunk_driver.hpp"
@@ -670,6 +674,15 @@ int launch_scan_backward_fused(const Plan& pl, const ScanParams& p, hipStream_t 
 }
 
 int fast_scan_regs(const Plan& pl, int kind) {
+  // one query per instance (kind, lanes per label, durations per lane, mix width)
+  static std::mutex mu;
+  static std::map<std::tuple<int, int, int, int>, int> cache;
+  const auto key = std::make_tuple(kind, pl.FJ, pl.FR, pl.C <= 2 * pl.FJ ? 2 : 4);
+  {
+    std::lock_guard<std::mutex> lk(mu);
+    const auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+  }
   int regs = -1;
   ScanParams q{};
   q.B = pl.B;
@@ -679,7 +692,10 @@ int fast_scan_regs(const Plan& pl, int kind) {
   q.Kmax = pl.Kmax;
   q.query_regs = &regs;
   const int e = kind == 2 ? launch_scan_viterbi(pl, q, nullptr) : launch_fast(pl, q, kind == 0, nullptr);
-  return e == hipSuccess ? regs : -1;
+  if (e != hipSuccess || regs <= 0) return -1;  // not cached: no device yet
+  std::lock_guard<std::mutex> lk(mu);
+  cache[key] = regs;
+  return regs;
 }
 
 int launch_scan_forward(const Plan& pl, const ScanParams& p, int semiring, hipStream_t s) {
