@@ -131,15 +131,13 @@ __device__ __forceinline__ float group_lse2(float m, float s) {
   return M + log2_hw(t);
 }
 
-// a + (lane (i-1) mod 16 of the row of `rot`), one v_add_f32 with a DPP source
-// (row_ror:1): the end-sum slide of the fused marginals.  The s_nop gives the two wait states a DPP read needs after a
-// VALU write, which the compiler does not track across inline asm.  All lanes
-// are active.
+// a + (lane (i-1) mod 16 of the row of `rot`): the end-sum slide of the fused
+// marginals.  A DPP move (row_ror:1) that the compiler folds into the add
+// (one v_add_f32 with a DPP source), so it also places the wait states a DPP
+// read needs after a VALU write only where the schedule needs them.  All
+// lanes are active.
 __device__ __forceinline__ float add_row_ror1(float rot, float a) {
-  float r;
-  asm("s_nop 1\n\tv_add_f32_dpp %0, %1, %2 row_ror:1 row_mask:0xf bank_mask:0xf bound_ctrl:1"
-      : "=v"(r) : "v"(rot), "v"(a));
-  return r;
+  return a + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(rot), 0x121, 0xf, 0xf, true));
 }
 
 // CJ source labels per lane in the label mix (C <= CJ * J; the launchers pick 2
