@@ -132,9 +132,9 @@ __device__ __forceinline__ float group_lse2(float m, float s) {
 }
 
 // a + (lane (i-1) mod 16 of the row of `rot`): the end-sum slide of the fused
-// marginals.  A DPP move (row_ror:1) that the compiler folds into the add
-// (one v_add_f32 with a DPP source), so it also places the wait states a DPP
-// read needs after a VALU write only where the schedule needs them.  All
+// marginals.  A DPP move (row_ror:1) left to the compiler, so it schedules the
+// wait states a DPP read needs after a VALU write (only where the schedule
+// needs them) and fuses a product added here into an FMA after the move.  All
 // lanes are active.
 __device__ __forceinline__ float add_row_ror1(float rot, float a) {
   return a + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(rot), 0x121, 0xf, 0xf, true));
