@@ -369,8 +369,10 @@ int make_plan(int64_t B, int64_t T, int64_t C, int64_t K, int has_ps, int has_pe
     const int J = 16, MR = p.C > 64 ? ((p.Kmax + 15) / 16 + 3) / 4 * 4 : (p.Kmax + 15) / 16, KP = J * MR;
     const int CBm = 64 / J;
     const int RSm = std::max(p.Kmax + 2, KP + J);
-    int RLm = RSm + KP;
-    while (RLm % 32 != J % 32) ++RLm;
+    // linear ring of KP + 2 or 3 batches of 16 entries (moved every few batches),
+    // RL % 32 == 16 so the four label rows of a wave fall on distinct banks
+    int RLm = KP + 2 * J;
+    if (RLm % 32 != 16) RLm += J;
     const size_t lds = tsm::margfast_lds_layout(CBm, RLm, J, p.C).total;
     if (lds <= (size_t)di.max_lds) {
       p.mfast = 1;

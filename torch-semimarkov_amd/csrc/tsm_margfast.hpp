@@ -15,10 +15,10 @@
 //
 // One wavefront serves 4 labels of one position block: a 16-lane group (one
 // DPP row) per label, lane j owning durations k = 1 + j + 16*r (r < R, the
-// compile-time mapping of the scans).  x lives in an LDS ring per label
-// (mirrored so the KP = 16*R terms of a step are read without wrap-around),
-// staged 16 positions at a time, together with the per-step operands, from
-// loads issued one batch earlier.  E lives in registers: lane j's register r
+// compile-time mapping of the scans).  x lives in a linear LDS ring per label
+// (the KP = 16*R terms of a step are contiguous; every few batches the live
+// KP entries move to the front), staged 16 positions at a time, together with
+// the per-step operands, from loads issued one batch earlier.  E lives in registers: lane j's register r
 // holds the running end sum of position t+1+j+16r, so after each step the
 // sums slide one lane down the row (DPP row rotate; lane 0 first takes its
 // next register) and position t+1, complete, leaves from lane 0.  D and G
@@ -81,7 +81,7 @@ __global__ void __launch_bounds__(64) margfast_kernel(MargParams q) {
   if (pb >= q.B * q.NB) return;
   const int blk = pb % q.NB;
   const int b = pb / q.NB;
-  const int C = q.C, Kmax = q.Kmax, K = q.K, T = q.T, RS = q.RS, RL = q.RL;
+  const int C = q.C, Kmax = q.Kmax, K = q.K, T = q.T, RL = q.RL;
   const int lane = threadIdx.x, g = lane / J, lj = lane % J;
   const int c_raw = cbk * CB + g;
   const bool cval = c_raw < C;
@@ -142,15 +142,16 @@ __global__ void __launch_bounds__(64) margfast_kernel(MargParams q) {
   auto clampT = [&](int e) { return e > T ? T : e; };
 
   // ---- initial ring: x for positions t0+1 .. t0+KP ----
+  // The ring is linear: position p sits at index p - ofs (wave-uniform), each
+  // batch appends J positions, and when the next batch would run past RL
+  // entries the KP live positions move to the front.
+  int ofs = t0 + 1;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int e = t0 + 1 + lj + J * r;
     const int ec = clampT(e);
     const float pe = (has_pe && ec >= 1) ? pe_b[(size_t)(ec - 1) * C + c] * kLog2e : 0.0f;
-    const double x = x_of(e, bv_b[(size_t)ec * C + c], bl_b[ec], cum_b[(size_t)ec * C + c], pe);
-    const int a = e % RS;
-    xr[a] = x;
-    if (a < KP) xr[a + RS] = x;
+    xr[e - ofs] = x_of(e, bv_b[(size_t)ec * C + c], bl_b[ec], cum_b[(size_t)ec * C + c], pe);
   }
   // Batches of J steps.  At a batch start tb the registers loaded one batch
   // earlier are written to LDS -- x for positions tb+KP+1 .. tb+KP+J and the
@@ -207,10 +208,16 @@ __global__ void __launch_bounds__(64) margfast_kernel(MargParams q) {
   for (int t = t0; t < t1; ++t) {
     const int ib = (t - t0) % J;  // step within the batch
     if (ib == 0) {
-      const double x = x_of(e_n, sb_bv, sb_bl, sb_cm, sb_pe);
-      const int a = e_n % RS;
-      xr[a] = x;
-      if (a < KP) xr[a + RS] = x;
+      if (t + KP + J - ofs >= RL) {  // the batch's last index t+KP+J-ofs must stay below RL
+        // positions t+1 .. t+KP to indices 0 .. KP-1, ascending: each lane moves
+        // only its own entries, and overwrites only ones it has already moved
+        const int sh = t + 1 - ofs;
+#pragma unroll
+        for (int r = 0; r < R; ++r) xr[lj + J * r] = xr[sh + lj + J * r];
+        ofs = t + 1;
+        wave_lds_order();
+      }
+      xr[e_n - ofs] = x_of(e_n, sb_bv, sb_bl, sb_cm, sb_pe);
 #pragma unroll
       for (int i = 0; i < kRowLoads; ++i)
         if (lane + 64 * i < J * C) arow[lane + 64 * i] = ra[i];
@@ -246,7 +253,7 @@ __global__ void __launch_bounds__(64) margfast_kernel(MargParams q) {
     const double At = ((al + (double)(u2 + ps_t * kLog2e)) - (double)cm * kLog2eD) - z2;
 
     // ---- segment marginals over the lane's durations ----
-    const double* xb = xr + (t % RS + 1 + lj);
+    const double* xb = xr + (t + 1 - ofs + lj);
     double xv[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) xv[r] = xb[J * r];

@@ -38,8 +38,9 @@ struct Plan {
   int P2, Lc2, FRL2, dualF, dualB, dualV, regsF, regsB, regsV;
   size_t fast_lds2;
   // register-resident marginal kernel (mfast == 1): 16 lanes per label, MR
-  // durations per lane, one wavefront of 4 labels per workgroup, ring slots /
-  // row length.  NB, TB, CB, NCB and marg_lds above then describe its blocking.
+  // durations per lane, one wavefront of 4 labels per workgroup, MRS level
+  // slots of the generic layout, MRL linear ring length.  NB, TB, CB, NCB and
+  // marg_lds above then describe its blocking.
   int mfast, MR, MRS, MRL;
   // duration-dependent (trows, C, C) transitions (trows > 0): dense scans with DJ
   // lanes per label and DNT threads, DRS ring slots, dense_lds bytes, transition
