@@ -22,8 +22,11 @@
 // holds the running end sum of position t+1+j+16r, so after each step the
 // sums slide one lane down the row (DPP row rotate; lane 0 first takes its
 // next register) and position t+1, complete, leaves from lane 0.  D and G
-// accumulate in registers (fp32, folded into fp64 every 64 steps).  Waves
-// never synchronise with each other.
+// accumulate in fp32 registers; every 64 steps they are folded into the
+// block's fp64 partials in global memory with non-returning atomic adds (each
+// lane owns its entries), so no fp64 accumulators hold registers.  The
+// duration biases stay fp32 and are added after the fp64 sum x + A, whose
+// large parts cancel.  Waves never synchronise with each other.
 // Outputs follow the blocked layout of the generic marginal kernel (e_own /
 // halo / s_out rows, fp64 per-block partials), so the same finalize kernels
 // produce the gradients.
@@ -102,6 +105,11 @@ __global__ void __launch_bounds__(64) margfast_kernel(MargParams q) {
     return;
   }
   const int t1 = min(t0 + q.TB, len);
+  if (cval) {
+    for (int k = lj; k < Kmax; k += J) dbp[(size_t)k * C + c] = 0.0;
+    for (int cs = lj; cs < C; cs += J) trp[(size_t)cs * C + c] = 0.0;
+  }
+  __threadfence();  // the zeros before the first atomic add
   const bool has_ps = q.ps != nullptr, has_pe = q.pe != nullptr;
   const float* cum_b = q.cum + (size_t)b * (T + 1) * C;
   const float* ps_b = has_ps ? q.ps + (size_t)b * T * C : nullptr;
@@ -121,12 +129,12 @@ __global__ void __launch_bounds__(64) margfast_kernel(MargParams q) {
   float* psv = reinterpret_cast<float*>(smem + L.psv);    // [CB][J] proj_start of own labels
 
   // ---- constants ----
-  double dbr[R];
+  float dbr[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int k = 1 + lj + J * r;
     const int di = k < K - 1 ? k : K - 1;
-    dbr[r] = (k <= Kmax) ? (double)(q.db[(size_t)di * C + c] * kLog2e) : kInvD;
+    dbr[r] = (k <= Kmax) ? q.db[(size_t)di * C + c] * kLog2e : (float)kInvD;
   }
   float trr[kCJ];
 #pragma unroll
@@ -168,9 +176,13 @@ __global__ void __launch_bounds__(64) margfast_kernel(MargParams q) {
     sb_bl = bl_b[ec];
     sb_cm = cum_b[(size_t)ec * C + c];
     sb_pe = (has_pe && ec >= 1) ? pe_b[(size_t)(ec - 1) * C + c] * kLog2e : 0.0f;
+    // row indices from an opaque copy of the lane index: otherwise the 2 * kRowLoads
+    // quotients and remainders are hoisted out of the step loop into registers
+    int lno = lane;
+    __asm__ volatile("" : "+v"(lno));
 #pragma unroll
     for (int i = 0; i < kRowLoads; ++i) {
-      const int idx = lane + 64 * i;
+      const int idx = lno + 64 * i;
       ra[i] = (idx < J * C) ? av_b[(size_t)clampT(tb + idx / C) * C + idx % C] : 0.0f;
     }
     ral = al_b[clampT(tb + (lane % J))];
@@ -183,22 +195,37 @@ __global__ void __launch_bounds__(64) margfast_kernel(MargParams q) {
   wave_lds_order();
 
   float d32[R];
-  double d64[R];
   float ea[R];  // running end sums of positions t+1+lj+16r (this block's starts)
   const int lane0 = (lj == 0) ? -1 : 0;  // all bits set on the row's lane 0
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     d32[r] = 0.0f;
-    d64[r] = 0.0;
     ea[r] = 0.0f;
   }
   float g32[kCJ];
-  double g64[kCJ];
 #pragma unroll
-  for (int i = 0; i < kCJ; ++i) {
-    g32[i] = 0.0f;
-    g64[i] = 0.0;
-  }
+  for (int i = 0; i < kCJ; ++i) g32[i] = 0.0f;
+  // D and G partials: fp32 sums since the last fold added into the zeroed fp64
+  // block partials.  Addresses and masks come from an opaque copy of the lane
+  // index: otherwise they are hoisted out of the step loop into registers.
+  auto fold = [&]() {
+    int ljo = lj;
+    __asm__ volatile("" : "+v"(ljo));
+    double* a = dbp + (size_t)ljo * C + c;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (cval && 1 + ljo + J * r <= Kmax) unsafeAtomicAdd(a, (double)d32[r]);
+      a += (size_t)J * C;
+      d32[r] = 0.0f;
+    }
+    double* tg = trp + (size_t)ljo * C + c;
+#pragma unroll
+    for (int i = 0; i < kCJ; ++i) {
+      if (cval && ljo + J * i < C) unsafeAtomicAdd(tg, (double)g32[i]);
+      tg += (size_t)J * C;
+      g32[i] = 0.0f;
+    }
+  };
   float* s_out_b = q.s_out + (size_t)b * (T + 1) * C;
   float* halo_b = q.halo + ((size_t)b * q.NB + blk) * Kmax * C;
   // end rows [t0, own_hi) are this block's own; rows own_hi .. own_hi+Kmax-1 go to the
@@ -253,31 +280,23 @@ __global__ void __launch_bounds__(64) margfast_kernel(MargParams q) {
     const double At = ((al + (double)(u2 + ps_t * kLog2e)) - (double)cm * kLog2eD) - z2;
 
     // ---- segment marginals over the lane's durations ----
-    const double* xb = xr + (t + 1 - ofs + lj);
-    double xv[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) xv[r] = xb[J * r];
-    float sp0 = 0.0f, sp1 = 0.0f;
-    float pr[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const float P = exp2_hw((float)((xv[r] + dbr[r]) + At));
-      pr[r] = P;
-      d32[r] += P;
-      if (r & 1) sp1 += P;
-      else sp0 += P;
-    }
-    // the previous step's end sums slide to positions t+1+lj+16r: lane 0 takes its
+    // The previous step's end sums slide to positions t+1+lj+16r: lane 0 takes its
     // next register (dropping the row it flushed), then the row rotates one lane
     // down (lane j takes lane j+1), fused with the accumulation.  Ascending r
     // reads ea[r+1] before it is updated.
+    const double* xb = xr + (t + 1 - ofs + lj);
+    float sp0 = 0.0f, sp1 = 0.0f;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
+      const float P = exp2_hw((float)(xb[J * r] + At) + dbr[r]);
+      d32[r] += P;
+      if (r & 1) sp1 += P;
+      else sp0 += P;
       // a bitwise merge: a select between ea[r + 1] and ea[r] would be turned
       // into one register-array read at a lane-dependent index
       const float nxt = (r + 1 < R) ? ea[r + 1] : 0.0f;
       const float sl = __int_as_float((__float_as_int(nxt) & lane0) | (__float_as_int(ea[r]) & ~lane0));
-      ea[r] = add_row_ror15(sl, pr[r]);
+      ea[r] = add_row_ror15(sl, P);
     }
     const float St = group_sum<J>(sp0 + sp1);
     // ---- transition gradient: softmax weight of each source label times S[t,c] ----
@@ -291,18 +310,7 @@ __global__ void __launch_bounds__(64) margfast_kernel(MargParams q) {
       if (p < own_hi) e_own_b[(size_t)p * C + c] = ea[0];
       else halo_b[(size_t)(p - own_hi) * C + c] = ea[0];
     }
-    if (((t - t0) & 63) == 63) {
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        d64[r] += (double)d32[r];
-        d32[r] = 0.0f;
-      }
-#pragma unroll
-      for (int i = 0; i < kCJ; ++i) {
-        g64[i] += (double)g32[i];
-        g32[i] = 0.0f;
-      }
-    }
+    if (((t - t0) & 63) == 63) fold();
   }
   // ---- pending end rows t1+1 .. t1+Kmax-1 (partial sums from this block's starts) ----
 #pragma unroll
@@ -320,19 +328,8 @@ __global__ void __launch_bounds__(64) margfast_kernel(MargParams q) {
       }
     }
   }
-  // ---- block partials ----
-  if (cval) {
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int k = 1 + lj + J * r;
-      if (k <= Kmax) dbp[(size_t)(k - 1) * C + c] = d64[r] + (double)d32[r];
-    }
-#pragma unroll
-    for (int i = 0; i < kCJ; ++i) {
-      const int ci = lj + J * i;
-      if (ci < C) trp[(size_t)ci * C + c] = g64[i] + (double)g32[i];
-    }
-  }
+  // ---- block partials: the sums since the last fold ----
+  fold();
 }
 
 template <int J, int R, int CJ = 4>
