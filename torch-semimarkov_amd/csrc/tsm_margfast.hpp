@@ -18,7 +18,9 @@
 // compile-time mapping of the scans).  x lives in a linear LDS ring per label
 // (the KP = 16*R terms of a step are contiguous; every few batches the live
 // KP entries move to the front), staged 16 positions at a time, together with
-// the per-step operands, from loads issued one batch earlier.  E lives in registers: lane j's register r
+// the per-step operands, from loads issued one batch earlier.  The alpha-hat
+// row of a step (the label mix's sources) goes straight from global memory to
+// registers, loaded one step ahead.  E lives in registers: lane j's register r
 // holds the running end sum of position t+1+j+16r, so after each step the
 // sums slide one lane down the row (DPP row rotate; lane 0 first takes its
 // next register) and position t+1, complete, leaves from lane 0.  D and G
@@ -64,13 +66,11 @@ __device__ __forceinline__ float add_row_ror15(float rot, float a) {
   return r;
 }
 
-// CJ source labels per lane in the label mix (C <= CJ * J); the batch's alpha-hat
-// rows (J * C floats) are staged with 4 * CJ loads per lane.
+// CJ source labels per lane in the label mix (C <= CJ * J).
 template <int J, int R, int CJ>
 __global__ void __launch_bounds__(64) margfast_kernel(MargParams q) {
   static_assert(J == 16, "end sums slide along one 16-lane DPP row");
   constexpr int kCJ = CJ;
-  constexpr int kRowLoads = 4 * CJ;
   extern __shared__ __align__(16) char smem[];
   constexpr int KP = J * R;
   constexpr int CB = 64 / J;
@@ -123,7 +123,6 @@ __global__ void __launch_bounds__(64) margfast_kernel(MargParams q) {
   const MargFastLds L = margfast_lds_layout(CB, RL, J, C);
   double* xr = reinterpret_cast<double*>(smem + L.xring) + (size_t)g * RL;
   // per-step operands of the current batch of J positions [tb, tb+J)
-  float* arow = reinterpret_cast<float*>(smem + L.arow);  // [J][C] alpha-hat rows
   double* alv = reinterpret_cast<double*>(smem + L.alv);  // [J]    alpha levels
   float* cmv = reinterpret_cast<float*>(smem + L.cmv);    // [CB][J] cum of own labels
   float* psv = reinterpret_cast<float*>(smem + L.psv);    // [CB][J] proj_start of own labels
@@ -167,7 +166,6 @@ __global__ void __launch_bounds__(64) margfast_kernel(MargParams q) {
   int e_n = t0 + KP + 1 + lj;  // x position this lane stages at the next batch start
   float sb_bv, sb_cm, sb_pe;
   double sb_bl;
-  float ra[kRowLoads];
   double ral;
   float rcm, rps;
   auto load_batch = [&](int tb, int e) {
@@ -176,21 +174,21 @@ __global__ void __launch_bounds__(64) margfast_kernel(MargParams q) {
     sb_bl = bl_b[ec];
     sb_cm = cum_b[(size_t)ec * C + c];
     sb_pe = (has_pe && ec >= 1) ? pe_b[(size_t)(ec - 1) * C + c] * kLog2e : 0.0f;
-    // row indices from an opaque copy of the lane index: otherwise the 2 * kRowLoads
-    // quotients and remainders are hoisted out of the step loop into registers
-    int lno = lane;
-    __asm__ volatile("" : "+v"(lno));
-#pragma unroll
-    for (int i = 0; i < kRowLoads; ++i) {
-      const int idx = lno + 64 * i;
-      ra[i] = (idx < J * C) ? av_b[(size_t)clampT(tb + idx / C) * C + idx % C] : 0.0f;
-    }
     ral = al_b[clampT(tb + (lane % J))];
     const int tp = clampT(tb + lj);
     rcm = cum_b[(size_t)tp * C + c];
     rps = has_ps ? ps_b[(size_t)min(tp, T - 1) * C + c] : 0.0f;
   };
   load_batch(t0, e_n);
+  // alpha-hat row of step tp: this lane's CJ source labels (clamped into the row;
+  // the label mix masks the clamped ones)
+  float rvn[kCJ];
+  auto load_row = [&](int tp) {
+    const float* rowp = av_b + (size_t)clampT(tp) * C;
+#pragma unroll
+    for (int i = 0; i < kCJ; ++i) rvn[i] = rowp[min(lj + J * i, C - 1)];
+  };
+  load_row(t0);
   if (cval && lj == 0) e_own_b[(size_t)t0 * C + c] = 0.0f;
   wave_lds_order();
 
@@ -245,9 +243,6 @@ __global__ void __launch_bounds__(64) margfast_kernel(MargParams q) {
         wave_lds_order();
       }
       xr[e_n - ofs] = x_of(e_n, sb_bv, sb_bl, sb_cm, sb_pe);
-#pragma unroll
-      for (int i = 0; i < kRowLoads; ++i)
-        if (lane + 64 * i < J * C) arow[lane + 64 * i] = ra[i];
       if (lane < J) alv[lane] = ral;
       cmv[g * J + lj] = rcm;
       psv[g * J + lj] = rps;
@@ -258,7 +253,8 @@ __global__ void __launch_bounds__(64) margfast_kernel(MargParams q) {
     // ---- this step's operands ----
     float rv[kCJ];
 #pragma unroll
-    for (int i = 0; i < kCJ; ++i) rv[i] = arow[ib * C + min(lj + J * i, C - 1)];
+    for (int i = 0; i < kCJ; ++i) rv[i] = rvn[i];
+    load_row(t + 1);
     const double al = alv[ib];
     const float cm = cmv[g * J + ib];
     const float ps_t = psv[g * J + ib];

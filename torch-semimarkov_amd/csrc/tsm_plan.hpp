@@ -72,7 +72,6 @@ __host__ __device__ inline size_t align16(size_t x) { return (x + 15) & ~size_t(
 // of one batch of J positions.
 struct MargFastLds {
   size_t xring;  // double[CB*RL]
-  size_t arow;   // float[J*C]   alpha-hat rows
   size_t alv;    // double[J]    alpha levels
   size_t cmv;    // float[CB*J]  cumulative scores of the own labels
   size_t psv;    // float[CB*J]  proj_start of the own labels
@@ -83,7 +82,6 @@ __host__ __device__ inline MargFastLds margfast_lds_layout(int CB, int RL, int J
   MargFastLds L;
   size_t o = 0;
   L.xring = o; o = align16(o + 8 * (size_t)CB * RL);
-  L.arow = o; o = align16(o + 4 * (size_t)J * C);
   L.alv = o; o = align16(o + 8 * (size_t)J);
   L.cmv = o; o = align16(o + 4 * (size_t)CB * J);
   L.psv = o; o = align16(o + 4 * (size_t)CB * J);
