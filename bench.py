@@ -44,6 +44,21 @@ V_PEAK_NONPACKED = 39.3e12
 # build stores alpha instead of recomputing it.
 OPS = {"fwd_log": (5, 1), "bwd_log": (14, 3), "fwdbwd_log": (19, 4), "max": (3, 0)}
 KERNEL_OPS = {"scan_fwd_kernel": (5, 1), "scan_bwd_kernel": (4, 1), "marginal_kernel": (5, 1)}
+# What the kernels EXECUTE: the exact label factorisation.  Per position and
+# sequence a pass evaluates max(K-1, 1)*C duration terms (t, k, c) and C^2
+# label-mix terms (t, c', c) instead of K*C^2 cells.  Each term is priced with
+# the ops of the pass it belongs to, (VALU lane-ops, transcendentals):
+#   log forward     duration (5, 1) [edge add, + u, max, sub, exp+sum],  mix (5, 1)
+#   beta scan       duration (4, 1),                                     mix (4, 1)
+#   fused beta scan duration (9, 2) [beta (4, 1) + marginal (5, 1)],     mix (4, 1) [beta only;
+#                   the transition gradient runs in its own kernel]
+#   marginals       duration (5, 1),                                     mix (5, 1) [transition grad]
+EXEC_OPS = {
+    "scan_fwd_kernel": ((5, 1), (5, 1)),
+    "scan_bwd_kernel": ((4, 1), (4, 1)),
+    "scan_bwd_kernel_fused": ((9, 2), (4, 1)),
+    "marginal_kernel": ((5, 1), (5, 1)),
+}
 PROFILES = os.path.join(ROOT, "profiles")
 
 
@@ -55,6 +70,16 @@ def roofline_cells_per_s(kind):
 def valu_equiv_ops_per_cell(kind):
     nv, nt = OPS[kind]
     return nv + nt * (V_PEAK / T_PEAK)
+
+
+def executed_valu_ops(kernel, B, T, C, K):
+    """VALU-equivalent lane-ops (transcendentals weighted by V_peak/T_peak) one
+    launch of `kernel` executes on the factorised recursion: B*T positions times
+    (duration terms * their ops + label-mix terms * theirs)."""
+    (dv, dt), (mv, mt) = EXEC_OPS[kernel]
+    w = V_PEAK / T_PEAK
+    per_pos = max(K - 1, 1) * C * (dv + dt * w) + C * C * (mv + mt * w)
+    return B * T * per_pos
 
 
 def profiled_traffic(kernel, workload):
@@ -121,17 +146,31 @@ def copy_calibration(mib=256, reps=3):
 
 
 CONFIGS = {
+    "cfg1": dict(B=4, T=1000, C=24, K=100, H=512, seed=20261201),
     "cfg2": dict(B=32, T=10_000, C=8, K=1, seed=20261202),
     "cfg3": dict(B=1, T=1_000_000, C=24, K=300, seed=20261203),
+    "cfg4": dict(B=64, T=8192, C=32, K=64, seed=20261204),
     "cfg5": dict(B=8, T=50_000, C=128, K=500, seed=20261205),
 }
 
 
 def make_inputs(name):
+    """Host (CPU, fp32) inputs of a scan workload, drawn in the documented order
+    with torch.Generator().manual_seed(seed): returns (cfg, cum (B,T+1,C),
+    transition (C,C), duration_bias (K,C), lengths (B,) int64).  Also used by
+    tests/golden/make_config_fixtures.py and the full-size parity tests, so the
+    draws live in one place."""
     cfg = CONFIGS[name]
     B, T, C, K = cfg["B"], cfg["T"], cfg["C"], cfg["K"]
     g = torch.Generator().manual_seed(cfg["seed"])
-    em = torch.randn(B, T, C, generator=g)
+    if name == "cfg4":
+        L = torch.randint(4096, 8193, (B,), generator=g)
+        em = torch.randn(B, T, C, generator=g)
+        tr = 0.1 * torch.randn(C, C, generator=g)
+        db = 0.1 * torch.randn(K, C, generator=g)
+    else:
+        em = torch.randn(B, T, C, generator=g)
+        L = torch.full((B,), T, dtype=torch.long)
     if name == "cfg5":
         tr = 0.05 * torch.randn(C, C, generator=g)
         k = torch.arange(1, K, dtype=torch.float64)
@@ -142,32 +181,41 @@ def make_inputs(name):
     elif name == "cfg2":
         tr = 0.1 * torch.randn(C, C, generator=g)
         db = 0.1 * torch.randn(1, C, generator=g)
-    else:
+    elif name == "cfg3":
         tr = 0.1 * torch.randn(C, C, generator=g)
         db = torch.zeros(K, C)
         db[1:] = -0.01 * torch.arange(1, K, dtype=torch.float32).unsqueeze(1) + 0.05 * torch.randn(K - 1, C, generator=g)
     cum = torch.zeros(B, T + 1, C)
     cum[:, 1:] = torch.cumsum(em, dim=1)
-    L = torch.full((B,), T, dtype=torch.long)
     return cfg, cum, tr, db, L
 
 
-def bench_head(args):
-    """cfg1: SemiMarkovCRFHead(24, 100, 512) on h ~ N(0,1) (4, 1000, 512), random labels:
-    one step = compute_loss + backward, then decode_with_traceback; latency-bound."""
+def make_head_inputs():
+    """cfg1: SemiMarkovCRFHead(24, 100, 512) built right after torch.manual_seed(seed)
+    (the reference's parameter order: transition, duration bias, projection), then
+    h ~ N(0,1) (4, 1000, 512) and labels uniform in [0, 24) from
+    torch.Generator().manual_seed(seed); lengths all 1000.  Host tensors."""
     import torch_semimarkov_amd as tsa
 
-    seed = 20261201
-    B, T, H, C, K = 4, 1000, 512, 24, 100
+    cfg = CONFIGS["cfg1"]
+    B, T, C, K, H, seed = cfg["B"], cfg["T"], cfg["C"], cfg["K"], cfg["H"], cfg["seed"]
     torch.manual_seed(seed)
     head = tsa.SemiMarkovCRFHead(C, K, hidden_dim=H)
     g = torch.Generator().manual_seed(seed)
     h = torch.randn(B, T, H, generator=g)
     labels = torch.randint(0, C, (B, T), generator=g)
+    L = torch.full((B,), T, dtype=torch.long)
+    return cfg, head, h, L, labels
+
+
+def bench_head(args):
+    """cfg1: SemiMarkovCRFHead(24, 100, 512) on h ~ N(0,1) (4, 1000, 512), random labels:
+    one step = compute_loss + backward, then decode_with_traceback; latency-bound."""
+    cfg, head, h, L, labels = make_head_inputs()
+    B, T, H, C, K, seed = cfg["B"], cfg["T"], cfg["H"], cfg["C"], cfg["K"], cfg["seed"]
     dev = torch.device("cuda", 0)
     head = head.to(dev)
-    h, labels = h.to(dev), labels.to(dev)
-    L = torch.full((B,), T, dtype=torch.long, device=dev)
+    h, labels, L = h.to(dev), labels.to(dev), L.to(dev)
 
     def train_step():
         head.zero_grad(set_to_none=True)
@@ -203,19 +251,11 @@ def bench_head(args):
 
 def bench_viterbi(args):
     """cfg4: Viterbi with backtrace (max semiring), 64 ragged sequences."""
-    import torch_semimarkov_amd as tsa
     from torch_semimarkov_amd import _native as N
     from torch_semimarkov_amd.streaming import ops
 
-    seed = 20261204
-    B, T, C, K = 64, 8192, 32, 64
-    g = torch.Generator().manual_seed(seed)
-    lengths = torch.randint(4096, 8193, (B,), generator=g)
-    em = torch.randn(B, T, C, generator=g)
-    tr = 0.1 * torch.randn(C, C, generator=g)
-    db = 0.1 * torch.randn(K, C, generator=g)
-    cum = torch.zeros(B, T + 1, C)
-    cum[:, 1:] = torch.cumsum(em, dim=1)
+    cfg, cum, tr, db, lengths = make_inputs("cfg4")
+    B, T, C, K, seed = cfg["B"], cfg["T"], cfg["C"], cfg["K"], cfg["seed"]
     dev = torch.device("cuda", 0)
     cum, tr, db, L = cum.to(dev), tr.to(dev), db.to(dev), lengths.to(dev)
 
@@ -249,39 +289,77 @@ def bench_viterbi(args):
     }))
 
 
-def cpu_baseline(name, cum, tr, db, K, t_sample):
-    """The oracle (fp32 PyTorch-CPU restatement of the reference streaming path)
-    on the first t_sample positions of the same workload, forward + backward."""
-    from oracle import streaming_ref as R
-
-    threads = min(os.cpu_count() or 1, 16)
-    torch.set_num_threads(threads)
-    B = cum.shape[0]
-    c = cum[:, : t_sample + 1].contiguous()
-    L = torch.full((B,), t_sample, dtype=torch.long)
-    t0 = time.perf_counter()
-    part, ck, S = R.forward(c, tr, db, L, K, "log")
-    R.backward(c, tr, db, L, K, part, ck, S, "log")
-    dt = time.perf_counter() - t0
-    C = cum.shape[2]
-    cells = B * t_sample * K * C * C
-    model = ""
+def host_facts():
+    """Host CPU facts for the baseline: model name, physical cores, logical CPUs,
+    and the CPUs this process may run on."""
+    model, phys = "", set()
     try:
+        cur = {}
         with open("/proc/cpuinfo") as f:
             for ln in f:
-                if ln.startswith("model name"):
-                    model = ln.split(":", 1)[1].strip()
-                    break
+                if ":" not in ln:
+                    if "physical id" in cur and "core id" in cur:
+                        phys.add((cur["physical id"], cur["core id"]))
+                    cur = {}
+                    continue
+                k, v = (x.strip() for x in ln.split(":", 1))
+                cur[k] = v
+                if k == "model name" and not model:
+                    model = v
+        if "physical id" in cur and "core id" in cur:
+            phys.add((cur["physical id"], cur["core id"]))
     except OSError:
         model = platform.processor()
+    try:
+        allowed = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        allowed = os.cpu_count() or 1
+    return {"model": model or "unknown", "physical_cores": len(phys) or None, "logical_cpus": os.cpu_count(),
+            "cpus_allowed": allowed}
+
+
+def cpu_baseline(name, cum, tr, db, K, t_sample):
+    """The oracle (fp32 PyTorch-CPU restatement of the reference's CPU streaming
+    path, its arithmetic order kept) timed on this host: forward + backward on
+    prefixes of the same workload of t_sample/2 and t_sample positions, median
+    of 3 after one warm-up, extrapolated linearly in T to the full length (exact
+    for T >> K: every position past K costs the same).  About 10-30 s of CPU."""
+    from oracle import streaming_ref as R
+
+    facts = host_facts()
+    threads = max(1, min(facts["cpus_allowed"], 16))
+    torch.set_num_threads(threads)
+    B, Tp1, C = cum.shape
+    T_full = Tp1 - 1
+    t2 = min(t_sample, T_full)
+    t1 = max(1, t2 // 2)
+
+    def run(t):
+        c = cum[:, : t + 1].contiguous()
+        L = torch.full((B,), t, dtype=torch.long)
+        t0 = time.perf_counter()
+        part, ck, S = R.forward(c, tr, db, L, K, "log")
+        R.backward(c, tr, db, L, K, part, ck, S, "log")
+        return time.perf_counter() - t0
+
+    run(max(1, min(t1, K + 16)))  # warm-up
+    m1 = statistics.median(run(t1) for _ in range(3))
+    m2 = statistics.median(run(t2) for _ in range(3))
+    slope = (m2 - m1) / (t2 - t1) if t2 > t1 else m2 / t2
+    full_s = m2 + slope * (T_full - t2)
+    cells = B * T_full * K * C * C
     return {
-        "value": cells / dt,
+        "value": cells / full_s,
         "unit": "cells/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"{name} inputs truncated to T={t_sample} (B={B}, C={C}, K={K}), oracle fp32 forward+backward "
-                  f"once, {dt:.1f} s on {model or 'host CPU'}",
-        "seconds": dt,
+        "sample": f"{name}: oracle fp32 forward+backward on prefixes T={t1} and T={t2} (B={B}, C={C}, K={K}), "
+                  f"median of 3 after a warm-up: {m1:.2f} s and {m2:.2f} s; extrapolated linearly to "
+                  f"T={T_full}: {full_s:.0f} s (extrapolated)",
+        "extrapolated_seconds_full": full_s,
+        "median_seconds": {str(t1): m1, str(t2): m2},
+        "host": facts,
+        "torch_threads": torch.get_num_threads(),
     }
 
 
@@ -323,7 +401,7 @@ def main():
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--config", default="cfg3", choices=sorted(list(CONFIGS) + ["cfg1", "cfg4"]))
-    ap.add_argument("--cpu-sample", type=int, default=4000)
+    ap.add_argument("--cpu-sample", type=int, default=1200)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-passes", action="store_true",
                     help="skip the per-pass timings (forward only, Viterbi), e.g. under a profiler")
@@ -376,12 +454,15 @@ def main():
     for _ in range(args.warmup):
         step(False)
     torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats(dev)
     # the timed region (value): K steps, without the library's per-kernel events
     t0 = time.perf_counter()
     for _ in range(args.steps):
         part = step(True)
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
+    # peak device memory of a step (inputs, outputs, saved tables, workspaces)
+    peak_mem = torch.cuda.max_memory_allocated(dev)
     # the same K steps again with per-kernel HIP events, recorded by the library on
     # the stream each kernel runs on (kernel_avg_ms, roofline); the events add about
     # 1 % to the step, so they stay out of the timed region above
@@ -401,14 +482,19 @@ def main():
                                                           ms_step, plan)
     # dominant kernel: the largest total time over the timed steps
     kops = dict(KERNEL_OPS)
-    if plan.get("mfused"):
+    fused = bool(plan.get("mfused"))
+    if fused:
         # the beta scan also accumulates the segment marginals: both passes' ops per cell
         kops["scan_bwd_kernel"] = tuple(a + b for a, b in zip(KERNEL_OPS["scan_bwd_kernel"], KERNEL_OPS["marginal_kernel"]))
     dom = max((k for k in ktimes if k in kops), key=lambda k: ktimes[k][0])
     dom_total, dom_launches = ktimes[dom]
     dom_avg_ms = dom_total / dom_launches
     nv, nt = kops[dom]
-    achieved = cells * (nv + nt * V_PEAK / T_PEAK) / (dom_avg_ms / 1e3) / 1e12
+    # roofline on the executed (factorised) work, and the survey's nominal pricing beside it
+    exec_key = "scan_bwd_kernel_fused" if (dom == "scan_bwd_kernel" and fused) else dom
+    exec_ops = executed_valu_ops(exec_key, B, T, C, K)
+    achieved = exec_ops / (dom_avg_ms / 1e3) / 1e12
+    nominal_achieved = cells * (nv + nt * V_PEAK / T_PEAK) / (dom_avg_ms / 1e3) / 1e12
     traffic = profiled_traffic(dom, args.config)
     peak = V_PEAK / 1e12
     out = {
@@ -436,6 +522,20 @@ def main():
             "unit": "TFLOP/s",
             "frac": achieved / peak,
             "traffic": traffic,
+            # what `achieved` counts: the factorised terms the kernel executes per launch
+            "work": {
+                "executed_terms_per_position": max(K - 1, 1) * C + C * C,
+                "nominal_cells_per_position": K * C * C,
+                "work_ratio": K * C * C / (max(K - 1, 1) * C + C * C),
+                "ops_per_duration_term": dict(zip(("valu", "transcendental"), EXEC_OPS[exec_key][0])),
+                "ops_per_mix_term": dict(zip(("valu", "transcendental"), EXEC_OPS[exec_key][1])),
+                "valu_equiv_ops_per_launch": exec_ops,
+                "formula": "B*T*(max(K-1,1)*C*(dv+dt*V/T) + C^2*(mv+mt*V/T)) / avg_launch_s / V_peak",
+            },
+            # the survey's nominal pricing: every B*T*K*C^2 cell of the direct recursion at the
+            # pass's (VALU, transcendental) ops; above 1 because the factorisation skips most cells
+            "nominal_frac": nominal_achieved / peak,
+            "nominal_ops_per_cell": {"valu": nv, "transcendental": nt},
             # achieved HBM rate of the dominant kernel (profiled bytes / launch time) and of its
             # emission stream alone (the (B, T+1, C) fp32 cumulative scores, read once per pass)
             "hbm_gb_per_s": traffic / (dom_avg_ms / 1e3) / 1e9 if traffic else None,
@@ -443,11 +543,8 @@ def main():
             "hbm_peak_gb_per_s": 8000.0,
             "executed": profiled_executed(dom, args.config),
             "avg_launch_ms": dom_avg_ms,
-            "ops_per_cell": {"valu": nv, "transcendental": nt},
-            "note": "NOMINAL: VALU-equivalent lane-ops (transcendental weighted by V_peak/T_peak) of the "
-                    "direct recursion per cell B*T*K*C^2; the kernels execute the exact label factorisation "
-                    "(K*C + C^2 instead of K*C^2 terms per position), so frac can exceed 1",
         },
+        "max_memory_allocated_bytes": peak_mem,
         "nominal_roofline_frac_fwdbwd": value / roofline_cells_per_s("fwdbwd_log"),
         "passes": passes,
         "fwd_ms": fwd_ms,

@@ -98,7 +98,11 @@ int tsm_plan_info(int64_t B, int64_t T, int64_t C, int64_t K, int64_t trans_rows
  *   alpha_level     (B, T+1)    fp64 per-position level (base 2) or NULL
  *   alpha = (alpha_hat + alpha_level) * ln 2.  Pass both non-NULL to keep the
  *   state a later tsm_backward() call needs; pass both NULL for inference.
- *   recomputed      (B,) int32  chunks recomputed by the verifier, or NULL
+ *   recomputed      (B,) int32  chunks recomputed by the verifier, or NULL; -1 marks a
+ *                               sequence whose cooperative scan (label sets too large for
+ *                               one CU) gave up its bounded wait for a partner block: its
+ *                               results are NaN (the call still returns TSM_OK, the kernels
+ *                               having exited normally)
  * ------------------------------------------------------------------------- */
 int tsm_forward_workspace(int64_t B, int64_t T, int64_t C, int64_t K, int64_t trans_rows, int semiring,
                           int has_proj_start, int has_proj_end, size_t* bytes);

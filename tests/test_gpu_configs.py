@@ -1,0 +1,293 @@
+"""GPU parity at the benchmark configurations themselves (cfg1..cfg5 of the
+benchmark set), through the same entry points a user calls.
+
+Inputs are drawn again from their seeds by ``bench.make_inputs`` /
+``bench.make_head_inputs`` and checked against the checksum stored with the
+fixture (``tests/golden/config_cfg*.npz``, written by
+``tests/golden/make_config_fixtures.py`` from the fp64 C restatement of the
+reference recursions and the fp32 restatement of its Viterbi).
+
+Tolerances (the path's parity bar): log Z within 1e-5 relative; gradients
+within 1e-5 relative + 1e-4 absolute of the fp64 oracle; Viterbi scores within
+1e-5 relative of the fp64 optimum; segmentations of the exact Viterbi kernel
+bit-identical to the reference's fp32 recursion on the same inputs.
+
+Segmentations and ties.  A run of one label cut into several segments scores
+exactly the same for every order of its segment durations (the content
+telescopes; the duration and transition terms commute), so such "structural"
+ties are compared in canonical form (runs with sorted durations).  Beyond
+them, cfg4's fp64 optimum has decisions whose runner-up is within 1e-6 (the
+smallest nonzero gap over 64 sequences is 2.4e-7), below the fp32 reference's
+own drift at |score| ~ 10^4, so no redraw of 64 sequences of ~6000 decisions
+is tie-free at the 1e-3 level: the fp32 reference's segmentation is then fixed
+by its rounding, and only an fp32 kernel with its operation order reproduces
+it.  The tests therefore check (a) the exact kernel bit-for-bit against the
+fp32 restatement, and (b) the default (factorised) path against the fp64
+optimum: score, an fp64 rescoring of its path, and canonical segment equality
+on every sequence whose decisions are all separated by more than the
+kernel's decision error.
+"""
+
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import gpu_available, load_golden
+from golden.make_config_fixtures import canonical_hash, input_checksum, seg_hash
+
+import bench
+from oracle import brute as BR
+from oracle import cref
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda", 0) if gpu_available() else None
+
+import torch_semimarkov_amd as tsa  # noqa: E402
+from torch_semimarkov_amd import _native as N  # noqa: E402
+from torch_semimarkov_amd.streaming import ops  # noqa: E402
+
+RTOL_Z = 1e-5
+GRAD_TOL = dict(rtol=1e-5, atol=1e-4)
+# canonical segment equality with the fp64 optimum is required where every
+# decision of the fp64 path beats its runner-up by more than this (the
+# factorised kernel compares candidates in an fp64-level / fp32-offset frame)
+FACT_GAP = 1e-4
+
+
+def _check_inputs(z, *arrays):
+    np.testing.assert_allclose(input_checksum(*arrays), z["checksum"], rtol=1e-10, atol=1e-6)
+
+
+def _segments_of(cnt, segs, b):
+    """GPU rows (last segment first) -> list of (start, end, label, prev), first first."""
+    n = int(cnt[b])
+    return [tuple(int(v) for v in segs[b, i]) for i in range(n - 1, -1, -1)]
+
+
+def _path_total_fp64(cum_b, tr, db, K, n, segs):
+    """fp64 score of a segmentation after checking it tiles [0, n) with durations
+    1..max(K-1, 1) and chained labels."""
+    pos, total, prev = 0, 0.0, None
+    for (s, e, c, cp) in segs:
+        assert s == pos and s <= e and e - s + 1 <= max(K - 1, 1)
+        if prev is not None:
+            assert cp == prev
+        d = min(e - s + 1, K - 1)
+        total += (cum_b[e + 1, c] - cum_b[s, c]) + db[d, c] + tr[cp, c]
+        pos, prev = e + 1, c
+    assert pos == n
+    return total
+
+
+def _identities(gc, gt, gd, L):
+    """Size-independent identities of the log-partition gradients (grad_output = 1)."""
+    gc = gc.double()
+    for b in range(gc.shape[0]):
+        n = int(L[b])
+        col = gc[b].sum(0)  # every segment has one start and one end
+        assert col.abs().max() <= 1e-4 + 1e-6 * gc[b].abs().sum(0).max(), (b, col.abs().max())
+        assert abs(gc[b, n].sum() - 1.0) <= 1e-4 and abs(gc[b, 0].sum() + 1.0) <= 1e-4
+    n_seg = gd.double().sum()
+    assert abs(gt.double().sum() - n_seg) <= 1e-5 * n_seg
+    assert torch.isfinite(gc).all() and torch.isfinite(gt).all() and torch.isfinite(gd).all()
+
+
+def _scan_config(name, monkeypatch):
+    monkeypatch.delenv("TSM_SCAN_PATH", raising=False)
+    monkeypatch.delenv("TSM_MARGINAL_PATH", raising=False)
+    monkeypatch.delenv("TSM_SCAN_CHUNKS", raising=False)
+    z = load_golden(f"config_{name}")
+    cfg, cum, tr, db, L = bench.make_inputs(name)
+    _check_inputs(z, cum, tr, db, L)
+    K = cfg["K"]
+    c, t, d = (x.to(DEV).requires_grad_(True) for x in (cum, tr, db))
+    part = tsa.semi_crf_streaming_forward(c, t, d, L.to(DEV), K)
+    part.sum().backward()
+    return z, cfg, (cum, tr, db, L), part.detach().cpu(), (c.grad.cpu(), t.grad.cpu(), d.grad.cpu())
+
+
+def _compare_scan(z, part, grads, L):
+    gc, gt, gd = grads
+    np.testing.assert_allclose(part.double().numpy(), z["logZ"], rtol=RTOL_Z)
+    np.testing.assert_allclose(gt.double().numpy(), z["grad_transition"], **GRAD_TOL)
+    np.testing.assert_allclose(gd.double().numpy(), z["grad_duration_bias"], **GRAD_TOL)
+    idx = z["grad_cum_rows_idx"]
+    rows = np.stack([gc[b, idx[b]].double().numpy() for b in range(gc.shape[0])])
+    np.testing.assert_allclose(rows, z["grad_cum_rows"].astype(np.float64), **GRAD_TOL)
+    _identities(gc, gt, gd, L)
+
+
+# --------------------------------------------------------------------------- cfg3 (headline)
+def test_cfg3_full_size_vs_fp64_fixture(monkeypatch):
+    """B=1, T=10^6, C=24, K=300 (the headline workload): log Z, grad_transition,
+    grad_duration_bias and 4102 sampled grad_cum rows against the fp64 oracle,
+    the gradient identities on the whole table, and the Viterbi score of the
+    default path against the fp64 max-semiring optimum."""
+    z, cfg, (cum, tr, db, L), part, grads = _scan_config("cfg3", monkeypatch)
+    _compare_scan(z, part, grads, L)
+    with torch.no_grad():
+        score = ops.viterbi(cum.to(DEV), tr.to(DEV), db.to(DEV), L.to(DEV), cfg["K"], None, None, False)[0]
+    np.testing.assert_allclose(score.cpu().double().numpy(), z["max_score"], rtol=1e-5)
+
+
+# --------------------------------------------------------------------------- cfg5 (large label set)
+def test_cfg5_full_size_vs_fp64_fixture(monkeypatch):
+    """B=8, T=5*10^4, C=128, K=500 (cooperative scans, wide marginals): the
+    full 500-entry rings and durations up to 499 are exercised.  log Z,
+    shared gradients and 68 sampled grad_cum rows per sequence against the
+    fp64 oracle, plus the identities on the whole table."""
+    info = N.plan_info(8, 50_000, 128, 500)
+    assert info["coop"] == 1 and info["mfast"] == 1 and info["NB"] >= 2, info
+    z, cfg, (cum, tr, db, L), part, grads = _scan_config("cfg5", monkeypatch)
+    _compare_scan(z, part, grads, L)
+
+
+# --------------------------------------------------------------------------- cfg2 (K = 1)
+def test_cfg2_full_size_vs_hmm(monkeypatch):
+    """B=32, T=10^4, C=8, K=1 against a probability-space HMM (fp64) on every
+    sequence: log Z, grad_cum (state posteriors), grad_transition (expected
+    transition counts, the virtual start label included) and
+    grad_duration_bias (row 0 counts every position)."""
+    monkeypatch.delenv("TSM_SCAN_PATH", raising=False)
+    cfg, cum, tr, db, L = bench.make_inputs("cfg2")
+    B, T, C = cfg["B"], cfg["T"], cfg["C"]
+    c, t, d = (x.to(DEV).requires_grad_(True) for x in (cum, tr, db))
+    part = tsa.semi_crf_streaming_forward(c, t, d, L.to(DEV), 1)
+    part.sum().backward()
+    part = part.detach().cpu()
+    gc, gt, gd = c.grad.cpu().double().numpy(), t.grad.cpu().double().numpy(), d.grad.cpu().double().numpy()
+    cum64, tr64, db64 = cum.double().numpy(), tr.double().numpy(), db.double().numpy()
+    tr_counts = np.zeros((C, C))
+    db_counts = np.zeros((1, C))
+    for b in range(B):
+        logZ, state_post, trans_counts, _ = BR.hmm_forward_backward(cum64[b], tr64, db64[0], T)
+        assert abs(part[b].item() - logZ) <= RTOL_Z * abs(logZ), b
+        want = np.zeros((T + 1, C))
+        want[1:] += state_post
+        want[:-1] -= state_post
+        np.testing.assert_allclose(gc[b], want, **GRAD_TOL)
+        tr_counts += trans_counts
+        db_counts[0] += state_post.sum(0)
+    np.testing.assert_allclose(gt, tr_counts, **GRAD_TOL)
+    np.testing.assert_allclose(gd, db_counts, **GRAD_TOL)
+
+
+# --------------------------------------------------------------------------- cfg4 (ragged Viterbi)
+def _cfg4():
+    z = load_golden("config_cfg4")
+    cfg, cum, tr, db, L = bench.make_inputs("cfg4")
+    _check_inputs(z, cum, tr, db, L)
+    return z, cfg, cum, tr, db, L
+
+
+def test_cfg4_exact_viterbi_bit_identical_to_reference_fp32():
+    """The exact kernel on the 64 ragged sequences: every score and every
+    segmentation bit-identical to the fp32 restatement of the reference's
+    recursion (``nn.py:444-531``)."""
+    z, cfg, cum, tr, db, L = _cfg4()
+    with torch.no_grad():
+        score, cnt, segs = ops.viterbi(cum.to(DEV), tr.to(DEV), db.to(DEV), L.to(DEV), cfg["K"], None, None, True,
+                                       N.TSM_VITERBI_EXACT)
+    score, cnt, segs = score.cpu(), cnt.cpu(), segs.cpu().numpy()
+    np.testing.assert_array_equal(score.numpy(), z["f32_score"].astype(np.float32))
+    np.testing.assert_array_equal(cnt.numpy(), z["f32_nseg"])
+    for b in range(cfg["B"]):
+        got = _segments_of(cnt, segs, b)
+        assert seg_hash(got) == bytes(z["f32_hash"][b]), b
+
+
+def test_cfg4_default_viterbi_vs_fp64_optimum():
+    """The default path (AUTO: the factorised, chunked kernel at this size) on
+    the 64 ragged sequences: scores within 1e-5 of the fp64 optimum; every
+    returned path tiles its sequence and rescores in fp64 to the optimum; the
+    segmentation equals the fp64 optimum's (canonical form) on every sequence
+    whose decisions are separated by more than FACT_GAP."""
+    z, cfg, cum, tr, db, L = _cfg4()
+    K = cfg["K"]
+    info = N.plan_info(cfg["B"], cfg["T"], cfg["C"], K)
+    assert info["fast"] == 1, info
+    with torch.no_grad():
+        score, cnt, segs = ops.viterbi(cum.to(DEV), tr.to(DEV), db.to(DEV), L.to(DEV), K, None, None, True)
+    score, cnt, segs = score.cpu(), cnt.cpu(), segs.cpu().numpy()
+    want = z["f64_score"]
+    np.testing.assert_allclose(score.double().numpy(), want, rtol=1e-5)
+    cum64, tr64, db64 = cum.double().numpy(), tr.double().numpy(), db.double().numpy()
+    checked = 0
+    worst = 0.0
+    for b in range(cfg["B"]):
+        got = _segments_of(cnt, segs, b)
+        total = _path_total_fp64(cum64[b], tr64, db64, K, int(L[b]), got)
+        worst = max(worst, float(want[b] - total))
+        assert total >= want[b] - 1e-6 * abs(want[b]), (b, total, want[b])
+        if z["f64_min_gap"][b] > FACT_GAP:
+            assert canonical_hash(got) == bytes(z["f64_canonical_hash"][b]), b
+            checked += 1
+    assert checked >= 16, checked
+    print(f"cfg4: {checked} sequences compared segment for segment; worst fp64 shortfall {worst:.3e}")
+
+
+# --------------------------------------------------------------------------- cfg1 (head)
+def test_cfg1_head_full_size_vs_fp64_fixture():
+    """SemiMarkovCRFHead(24, 100, 512), B=4, T=1000, random init from the seed:
+    the loss (``compute_loss``, mean) and its gradients w.r.t. every parameter
+    (transition, duration bias, projection weight and bias) against the fp64
+    oracle (fp64 projection, cumsum, partition and gold score), ``forward``'s
+    partition, and ``decode``'s Viterbi score."""
+    z = load_golden("config_cfg1")
+    cfg, head, h, L, labels = bench.make_head_inputs()
+    _check_inputs(z, h, labels, head.transition, head.duration_bias, head.projection.weight, head.projection.bias)
+    head = head.to(DEV)
+    h, L, labels = h.to(DEV), L.to(DEV), labels.to(DEV)
+    loss = head.compute_loss(h, L, labels)
+    loss.backward()
+    assert abs(loss.item() - float(z["loss"])) <= RTOL_Z * abs(float(z["loss"]))
+    for got, key in ((head.transition.grad, "grad_transition"),
+                     (head.duration_dist.duration_bias.grad, "grad_duration_bias"),
+                     (head.projection.weight.grad, "grad_proj_weight")):
+        np.testing.assert_allclose(got.cpu().double().numpy(), z[key], **GRAD_TOL, err_msg=key)
+    # The bias gradient of label c is (expected - gold occupancy of c) / B: a value of
+    # 1..20 that is the difference of two sums of about T/C = 42.  Rounding the exact
+    # grad_cum to fp32 (the type the scan returns) already moves it by up to 7e-5
+    # (measured on the fp64 oracle's gradient), beyond the absolute part of the bar
+    # for small entries; so the relative part applies to the occupancy it is a
+    # difference of: |err| <= 1e-4 + 1e-5 * max(|grad|, occupancy).
+    gb = head.projection.bias.grad.cpu().double().numpy()
+    tol = 1e-4 + 1e-5 * np.maximum(np.abs(z["grad_proj_bias"]), np.abs(z["proj_bias_scale"]))
+    assert np.all(np.abs(gb - z["grad_proj_bias"]) <= tol), (np.abs(gb - z["grad_proj_bias"]) / tol).max()
+    with torch.no_grad():
+        part = head(h, L)["partition"]
+        vit = head.decode(h, L)
+    np.testing.assert_allclose(part.cpu().double().numpy(), z["logZ"], rtol=RTOL_Z)
+    np.testing.assert_allclose(vit.cpu().double().numpy(), z["viterbi_score"], rtol=1e-5)
+
+
+def test_cfg1_decode_with_traceback_full_size():
+    """``decode_with_traceback`` at cfg1: (a) scores and segments bit-identical
+    to the fp32 restatement of the reference's traceback run on the same
+    cumulative scores (the head's own, read back from the GPU); (b) scores
+    within 1e-5 of the fp64 optimum, and every path rescored in fp64 (fp64
+    projection and cumsum) within 1e-5 of it."""
+    z = load_golden("config_cfg1")
+    cfg, head, h, L, labels = bench.make_head_inputs()
+    K = cfg["K"]
+    W, bl = head.projection.weight.detach().double(), head.projection.bias.detach().double()
+    tr64, db64 = head.transition.detach().double(), head.duration_bias.detach().double()
+    cum64 = torch.zeros(cfg["B"], cfg["T"] + 1, cfg["C"], dtype=torch.float64)
+    cum64[:, 1:] = torch.cumsum(h.double() @ W.T + bl, dim=1)
+    head = head.to(DEV)
+    hd, Ld = h.to(DEV), L.to(DEV)
+    with torch.no_grad():
+        res = head.decode_with_traceback(hd, Ld)
+        cum32 = head._cum_scores(hd).cpu()
+    ref = cref.viterbi(cum32, head.transition.detach().cpu(), head.duration_bias.detach().cpu(), L, K,
+                       dtype=np.float32)
+    np.testing.assert_array_equal(res.scores.cpu().numpy(), ref["score"].astype(np.float32))
+    np.testing.assert_allclose(res.scores.cpu().double().numpy(), z["viterbi_score"], rtol=1e-5)
+    for b in range(cfg["B"]):
+        got = [(s.start, s.end, s.label) for s in res.segments[b]]
+        assert got == [s[:3] for s in ref["segments"][b]], b
+        total = _path_total_fp64(cum64[b].numpy(), tr64.numpy(), db64.numpy(), K, int(L[b]),
+                                 [tuple(s) for s in ref["segments"][b]])
+        assert abs(total - z["viterbi_score"][b]) <= 1e-5 * abs(z["viterbi_score"][b]), b

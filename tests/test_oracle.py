@@ -247,3 +247,121 @@ def test_oracle_traceback_matches_reference_golden(name):
     part_log, _, _ = R.forward(cum, tr, db, L, K, "log")
     gold = R.score_gold(cum, torch.from_numpy(z["labels"]), L, tr, db, K)
     np.testing.assert_allclose((part_log - gold).numpy(), z["loss"], rtol=1e-5, atol=1e-4)
+
+
+# --------------------------------------------------------------------------- the C restatement (oracle/cref.py)
+CREF_CASES = [
+    (2, 30, 5, 4, None, False), (3, 40, 6, 3, [40, 17, 0], True), (2, 20, 1, 3, [20, 9], False),
+    (1, 60, 8, 24, None, False), (2, 25, 30, 5, [25, 3], True), (1, 1, 4, 3, None, True),
+]
+
+
+@pytest.mark.parametrize("B,T,K,C,lengths,proj", CREF_CASES)
+def test_cref_forward_backward_match_streaming_ref(B, T, K, C, lengths, proj):
+    """The label-factorised C restatement against the direct K*C^2 recursion of
+    oracle/streaming_ref.py (fp64): partition in both semirings and every
+    gradient, with projections, ragged and zero lengths, K=1 and T=1."""
+    from oracle import cref
+
+    cum, tr, db, L, ps, pe = rand_problem(B, T, K, C, 101 + T + K, lengths=lengths)
+    a, b = (ps, pe) if proj else (None, None)
+    for sr in ("log", "max"):
+        got = cref.forward(cum, tr, db, L, K, sr, a, b)
+        want, _, _ = R.forward(cum, tr, db, L, K, sr, a, b)
+        np.testing.assert_allclose(got, want.numpy(), rtol=1e-12, atol=1e-9)
+    res = cref.backward(cum, tr, db, L, K, a, b)
+    part, ck, S = R.forward(cum, tr, db, L, K, "log", a, b)
+    br = R.backward(cum, tr, db, L, K, part, ck, S, "log", a, b)
+    pairs = [("grad_cum", br.grad_cum), ("grad_transition", br.grad_transition),
+             ("grad_duration_bias", br.grad_duration_bias)]
+    if proj:
+        pairs += [("grad_proj_start", br.grad_proj_start), ("grad_proj_end", br.grad_proj_end)]
+    for key, want in pairs:
+        np.testing.assert_allclose(res[key], want.numpy(), rtol=1e-10, atol=1e-11, err_msg=key)
+
+
+def test_cref_backward_matches_enumeration_and_identities():
+    """Exact marginals by enumeration (tiny problem) and the identities on a
+    medium one: every segment has one start, one end, one duration and one
+    incoming transition."""
+    from oracle import cref
+
+    cum, tr, db, L, ps, pe = rand_problem(2, 6, 4, 3, 5, lengths=[6, 4])
+    ins = [x.clone().requires_grad_(True) for x in (cum, tr, db)]
+    z = BR.brute_log_partition(ins[0], ins[1], ins[2], L, 4, "log")
+    want = torch.autograd.grad(z.sum(), ins)
+    res = cref.backward(cum, tr, db, L, 4)
+    np.testing.assert_allclose(res["grad_cum"], want[0].numpy(), atol=1e-12)
+    np.testing.assert_allclose(res["grad_transition"].sum(0), want[1].numpy(), atol=1e-12)
+    np.testing.assert_allclose(res["grad_duration_bias"].sum(0), want[2].numpy(), atol=1e-12)
+    cum, tr, db, L, _, _ = rand_problem(2, 700, 40, 7, 6, lengths=[700, 333])
+    res = cref.backward(cum, tr, db, L, 40)
+    gc = res["grad_cum"]
+    for b in range(2):
+        n = int(L[b])
+        np.testing.assert_allclose(gc[b].sum(0), 0.0, atol=1e-9)
+        assert abs(gc[b, n].sum() - 1) < 1e-10 and abs(gc[b, 0].sum() + 1) < 1e-10
+        assert np.all(gc[b, n + 1:] == 0)
+        n_seg = res["grad_duration_bias"][b].sum()
+        assert abs(res["grad_transition"][b].sum() - n_seg) < 1e-9 * n_seg
+
+
+@pytest.mark.parametrize("B,T,K,C,lengths", [(2, 30, 5, 4, None), (2, 20, 1, 3, [20, 9]), (1, 60, 8, 24, None),
+                                             (3, 45, 12, 5, [45, 0, 7])])
+def test_cref_viterbi_matches_traceback_restatement(B, T, K, C, lengths):
+    """The C Viterbi against ``viterbi_traceback_single`` (itself pinned by the
+    reference's fixtures and by brute force): fp32 tables bit-identical
+    (scores and segments), fp64 segments and scores equal."""
+    from oracle import cref
+
+    cum, tr, db, L, _, _ = rand_problem(B, T, K, C, 211 + C, lengths=lengths)
+    for dt, tdt in ((np.float32, torch.float32), (np.float64, torch.float64)):
+        v = cref.viterbi(cum, tr, db, L, K, dtype=dt)
+        for b in range(B):
+            n = int(L[b])
+            if n == 0:
+                assert v["segments"][b] == []
+                continue
+            segs, sc = R.viterbi_traceback_single(cum[b].to(tdt), tr.to(tdt), db.to(tdt), K, n)
+            assert v["segments"][b] == [tuple(s) for s in segs], (dt, b)
+            assert v["score"][b] == sc, (dt, b)
+
+
+def test_cref_viterbi_gaps_and_exact_ties():
+    """The tie bookkeeping of the fp64 Viterbi.  (1) min_gap equals the
+    smallest nonzero best-minus-runner-up gap over the backtrace's decisions,
+    recomputed here from the restatement's fp64 alpha table.  (2) A run of one
+    label cut into two segments of different durations has an exact twin (the
+    durations swapped): it is counted as a tie, not as a small gap."""
+    from oracle import cref
+
+    cum, tr, db, L, _, _ = rand_problem(1, 40, 6, 3, 17)
+    v = cref.viterbi(cum, tr, db, L, 6, dtype=np.float64, close_thr=0.5)
+    _, _, _, alpha = R.forward(cum, tr, db, L, 6, "max", return_alpha=True)
+    alpha = alpha[0].numpy()
+    c64, t64, d64 = cum[0].numpy(), tr.numpy(), db.numpy()
+    gaps = []
+    fin = np.sort(alpha[40])[::-1]
+    gaps.append(fin[0] - fin[fin < fin[0]].max())
+    for (s, e, c, cp) in v["segments"][0]:
+        t = e + 1
+        cands = [alpha[t - k, q] + ((c64[t, c] - c64[t - k, c]) + d64[min(k, 5), c]) + t64[q, c]
+                 for k in range(1, min(5, t) + 1) for q in range(3)]
+        cands = np.sort(np.array(cands))[::-1]
+        lower = cands[cands < cands[0]]
+        if lower.size:
+            gaps.append(cands[0] - lower[0])
+    assert abs(v["min_gap"][0] - min(gaps)) < 1e-12
+    assert v["n_close"][0] == sum(g < 0.5 for g in gaps)
+    # exact twin: label 0 is the only good label and a self-transition bonus
+    # makes two segments (durations 2 and 3) beat one of duration 5
+    T, K, C = 5, 6, 2
+    cum = torch.zeros(1, T + 1, C, dtype=torch.float64)
+    cum[0, 1:, 0] = torch.arange(1, T + 1, dtype=torch.float64)
+    cum[0, 1:, 1] = -10.0 * torch.arange(1, T + 1, dtype=torch.float64)
+    tr = torch.tensor([[1.0, -5.0], [-5.0, -5.0]], dtype=torch.float64)
+    db = torch.zeros(K, C, dtype=torch.float64)
+    db[1] = db[4] = db[5] = -3.0
+    v = cref.viterbi(cum.float(), tr.float(), db.float(), torch.tensor([T]), K, dtype=np.float64)
+    durs = sorted(e - s + 1 for (s, e, c, cp) in v["segments"][0])
+    assert durs == [2, 3] and v["n_ties"][0] >= 1

@@ -11,6 +11,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 #include <string>
 
 #include "../../include/tsm_hip.h"
@@ -25,6 +26,13 @@ namespace {
 using tsm::Plan;
 
 thread_local std::string g_err;
+
+// Default acceptance threshold of speculative chunks (log2 units); see spec_tolerance().
+constexpr float kSpecTol = 4.0e-6f;
+
+// Sequences at least this long get the separate marginals' coverage pass (block
+// scales); shorter ones drift far below the gradient tolerance.
+constexpr int kCoverageMinT = 65536;
 
 int fail(int code, const char* fmt, ...) {
   char buf[512];
@@ -491,7 +499,10 @@ struct ScanWs {
 };
 
 // (Sized for the larger of the plan's two chunkings, so that either fits.)
-ScanWs carve_scan(Carver& cv, const Plan& p) {
+// generic_rings: the generic scan kernels may run (the max semiring, or a log
+// plan without the register-resident or cooperative scans); only they keep
+// rings in the workspace when LDS is too small.
+ScanWs carve_scan(Carver& cv, const Plan& p, bool generic_rings = true) {
   ScanWs w;
   const size_t items = (size_t)p.B * std::max(p.P, p.P2);
   w.st_spec = cv.take<float>(items * p.Kmax * p.C);
@@ -505,10 +516,24 @@ ScanWs carve_scan(Carver& cv, const Plan& p) {
   w.fin = cv.take<float>((size_t)p.B * p.C);
   w.fin_lvl = cv.take<double>(p.B);
   w.z2 = cv.take<double>(p.B);
-  w.gring = p.global_rings ? cv.take<float>(items * tsm::scan_gring_floats(p.C, p.KP, p.RL)) : nullptr;
+  w.gring = (p.global_rings && generic_rings && !p.dense)
+                ? cv.take<float>(items * tsm::scan_gring_floats(p.C, p.KP, p.RL))
+                : nullptr;
   w.xch = p.coop ? cv.take<unsigned long long>((size_t)p.CNQ * 2 * p.C) : nullptr;
   w.xabort = p.coop ? cv.take<int>(1) : nullptr;
   return w;
+}
+
+// Acceptance threshold of a speculative chunk: the spread (max - min, log2
+// units) of exact minus speculative boundary state.  TSM_SPEC_TOL overrides it
+// (diagnostics and tests).
+float spec_tolerance() {
+  const char* e = getenv("TSM_SPEC_TOL");
+  if (e != nullptr && *e != '\0') {
+    const float v = (float)atof(e);
+    if (v > 0.0f) return v;
+  }
+  return kSpecTol;
 }
 
 tsm::ScanParams scan_params(const Plan& pl, const ScanWs& w, const float* cum, const float* tr, const float* db,
@@ -532,7 +557,7 @@ tsm::ScanParams scan_params(const Plan& pl, const ScanWs& w, const float* cum, c
   p.P = pl.P;
   p.Lc = pl.Lc;
   p.W = pl.W;
-  p.tol = 2.0e-4f;
+  p.tol = spec_tolerance();
   p.st_spec = w.st_spec;
   p.st_end = w.st_end;
   p.lv_spec = w.lv_spec;
@@ -581,9 +606,15 @@ size_t tr_part_len(const Plan& p) {
   return (size_t)p.B * marg_nb(p) * (p.dense ? (size_t)p.Kmax : 1) * p.C * p.C;
 }
 
-size_t forward_ws_bytes(const Plan& pl) {
+// The forward runs a generic scan kernel unless a register-resident or
+// cooperative plan covers its semiring.
+bool forward_generic(const Plan& pl, int semiring) {
+  return semiring != TSM_SEMIRING_LOG || (!pl.fast && !pl.coop);
+}
+
+size_t forward_ws_bytes(const Plan& pl, int semiring) {
   Carver cv(nullptr);
-  carve_scan(cv, pl);
+  carve_scan(cv, pl, forward_generic(pl, semiring));
   carve_dense(cv, pl);
   return cv.off + 256;
 }
@@ -594,7 +625,7 @@ size_t forward_ws_bytes(const Plan& pl) {
 // halo rows, duration sums and frame estimate; transition partials per row block.
 struct BwdWs {
   float *bval = nullptr, *uval = nullptr, *e_own, *s_out, *halo;
-  double *blvl = nullptr, *db_part, *tr_part, *mframe = nullptr;
+  double *blvl = nullptr, *db_part, *tr_part, *mframe = nullptr, *bscale = nullptr;
   ScanWs scan;
   DenseTr dt;
 };
@@ -621,6 +652,7 @@ BwdWs carve_backward(Carver& cv, const Plan& pl) {
     w.halo = cv.take<float>((size_t)pl.B * marg_nb(pl) * pl.Kmax * pl.C);
     w.db_part = cv.take<double>((size_t)pl.B * marg_nb(pl) * pl.Kmax * pl.C);
     w.tr_part = cv.take<double>(tr_part_len(pl));
+    w.bscale = cv.take<double>((size_t)pl.B * marg_nb(pl));
   }
   w.dt = carve_dense(cv, pl);
   return w;
@@ -649,7 +681,7 @@ size_t viterbi_ws_bytes(const Plan& pl, int with_tb) {
   if (with_tb) cv.take<int32_t>((size_t)pl.B * (pl.T + 1) * pl.C);
   cv.take<int32_t>(pl.B);
   if (pl.fast) {
-    carve_scan(cv, pl);
+    carve_scan(cv, pl, false);
     if (with_tb) cv.take<int32_t>((size_t)pl.B * (pl.T + 1) * pl.C);  // factorised backpointers, exact format
   }
   if (with_tb) cv.take<char>(tsm::backtrace_ws_bytes(tsm::backtrace_plan(pl.B, pl.T, pl.C, pl.Kmax), pl.B));
@@ -753,14 +785,19 @@ int tsm_forward_workspace(int64_t B, int64_t T, int64_t C, int64_t K, int64_t tr
   Plan p;
   int rc = make_plan(B, T, C, K, has_ps, has_pe, trans_rows, &p);
   if (rc) return rc;
-  *bytes = forward_ws_bytes(p);
+  *bytes = forward_ws_bytes(p, semiring);
   return TSM_OK;
 }
 
-int tsm_forward(const float* cum, const float* tr, const float* db, const int64_t* len, const float* ps,
-                const float* pe, int64_t B, int64_t T, int64_t C, int64_t K, int64_t trans_rows, int semiring,
-                float* partition, double* log2_partition, float* alpha_hat, double* alpha_level, int32_t* recomputed,
-                void* workspace, size_t ws_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// tsm_forward's work on a given workspace.
+int forward_impl(const float* cum, const float* tr, const float* db, const int64_t* len, const float* ps,
+                 const float* pe, int64_t B, int64_t T, int64_t C, int64_t K, int64_t trans_rows, int semiring,
+                 float* partition, double* log2_partition, float* alpha_hat, double* alpha_level,
+                 int32_t* recomputed, void* workspace, size_t ws_bytes, void* stream, const char* what) {
   int rc = check_common(cum, tr, db, len, semiring);
   if (rc) return rc;
   if (!partition) return fail(TSM_ERR_INVALID, "partition output is required");
@@ -769,12 +806,12 @@ int tsm_forward(const float* cum, const float* tr, const float* db, const int64_
   Plan pl;
   rc = make_plan(B, T, C, K, ps != nullptr, pe != nullptr, trans_rows, &pl);
   if (rc) return rc;
-  const size_t need = forward_ws_bytes(pl);
+  const size_t need = forward_ws_bytes(pl, semiring);
   if (!workspace || ws_bytes < need)
-    return fail(TSM_ERR_WORKSPACE, "forward workspace too small: %zu < %zu bytes", ws_bytes, need);
+    return fail(TSM_ERR_WORKSPACE, "%s: workspace too small: %zu < %zu bytes", what, ws_bytes, need);
   if (semiring == TSM_SEMIRING_LOG && pl.dualF) pl = dual_plan(pl);
   Carver cv(workspace);
-  ScanWs w = carve_scan(cv, pl);
+  ScanWs w = carve_scan(cv, pl, forward_generic(pl, semiring));
   const DenseTr dt = carve_dense(cv, pl);
   tsm::ScanParams p = scan_params(pl, w, cum, tr, db, len, ps, pe);
   if (pl.dense) {
@@ -789,8 +826,20 @@ int tsm_forward(const float* cum, const float* tr, const float* db, const int64_
   p.zout = partition;
   p.recomputed = recomputed;
   const int e = tsm::launch_scan_forward(pl, p, semiring, (hipStream_t)stream);
-  if (e != hipSuccess) return hip_fail(e, "tsm_forward");
+  if (e != hipSuccess) return hip_fail(e, what);
   return TSM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tsm_forward(const float* cum, const float* tr, const float* db, const int64_t* len, const float* ps,
+                const float* pe, int64_t B, int64_t T, int64_t C, int64_t K, int64_t trans_rows, int semiring,
+                float* partition, double* log2_partition, float* alpha_hat, double* alpha_level, int32_t* recomputed,
+                void* workspace, size_t ws_bytes, void* stream) {
+  return forward_impl(cum, tr, db, len, ps, pe, B, T, C, K, trans_rows, semiring, partition, log2_partition,
+                      alpha_hat, alpha_level, recomputed, workspace, ws_bytes, stream, "tsm_forward");
 }
 
 int tsm_backward_workspace(int64_t B, int64_t T, int64_t C, int64_t K, int64_t trans_rows, int has_ps, int has_pe,
@@ -854,6 +903,13 @@ int tsm_backward(const float* cum, const float* tr, const float* db, const int64
     f.GTB = pl.GTB;
     f.offs = w.offs;
     f.mframe = bw.mframe;
+    f.cum = cum;
+    f.db = db;
+    f.ps = ps;
+    f.alvl = alpha_level;
+    f.z2 = log2_partition;
+    f.st_end = w.st_end;
+    f.lv_end = w.lv_end;
     f.e_own = e_own;
     f.s_out = s_out;
     f.halo = halo;
@@ -931,6 +987,15 @@ int tsm_backward(const float* cum, const float* tr, const float* db, const int64
   q.tr_part = tr_part;
   e = tsm::launch_marginals(pl, q, st);
   if (e != hipSuccess) return hip_fail(e, "tsm_backward (marginals)");
+  // coverage pass (block scales): long sequences, where the level chains' rounding
+  // drift reaches the gradient tolerance; log semiring, static transitions
+  const char* cenv = getenv("TSM_COVERAGE");  // diagnostics: =0 skips it
+  const bool coverage = semiring == TSM_SEMIRING_LOG && !pl.dense && pl.T >= kCoverageMinT &&
+                        (cenv == nullptr || strcmp(cenv, "0") != 0);
+  if (coverage) {
+    e = tsm::launch_block_coverage(pl, q, bw.bscale, st);
+    if (e != hipSuccess) return hip_fail(e, "tsm_backward (coverage)");
+  }
 
   tsm::FinalParams f{};
   f.lengths = len;
@@ -953,6 +1018,7 @@ int tsm_backward(const float* cum, const float* tr, const float* db, const int64
   f.grad_pe = grad_pe;
   f.grad_tr = grad_tr;
   f.grad_db = grad_db;
+  f.bscale = coverage ? bw.bscale : nullptr;
   e = tsm::launch_finalize(pl, f, st);
   if (e != hipSuccess) return hip_fail(e, "tsm_backward (finalize)");
   return TSM_OK;
@@ -994,7 +1060,7 @@ int tsm_viterbi(const float* cum, const float* tr, const float* db, const int64_
     Carver cv(workspace);
     int32_t* bp = with_tb ? cv.take<int32_t>((size_t)pl.B * (pl.T + 1) * pl.C) : nullptr;
     cv.take<int32_t>(pl.B);
-    ScanWs w = carve_scan(cv, pl);
+    ScanWs w = carve_scan(cv, pl, false);
     int32_t* bp_exact = with_tb ? cv.take<int32_t>((size_t)pl.B * (pl.T + 1) * pl.C) : nullptr;
     const tsm::BtPlan btp = tsm::backtrace_plan(pl.B, pl.T, pl.C, pl.Kmax);
     void* bt_ws = with_tb ? cv.take<char>(tsm::backtrace_ws_bytes(btp, pl.B)) : nullptr;

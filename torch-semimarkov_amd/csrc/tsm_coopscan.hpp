@@ -499,6 +499,8 @@ __global__ void __launch_bounds__(CH::kMaxThreads) coop_fixup_kernel(ScanParams 
       } else if (threadIdx.x == 0 && p.recomputed != nullptr) {
         p.recomputed[b] = n_re;
       }
+      // a group that gave up leaves NaN results: mark the sequence for the caller
+      if (threadIdx.x == 0 && p.recomputed != nullptr && aborted(p)) p.recomputed[b] = -1;
     }
     __syncthreads();
   }

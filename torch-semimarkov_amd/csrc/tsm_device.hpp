@@ -19,9 +19,22 @@ constexpr float kLog2e = 1.4426950408889634f;         // log2(e)
 constexpr double kLn2 = 0.6931471805599453;           // ln(2)
 constexpr float kMinusInf = -__builtin_inff();
 
-// Hardware base-2 exponential / logarithm (v_exp_f32 / v_log_f32, ~1 ulp).
+// Hardware base-2 exponential (v_exp_f32).  Measured on MI355X against fp64:
+// mean relative error -3.4e-9, rms 2.6e-8 over [-20, 0].
 __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
-__device__ __forceinline__ float log2_hw(float x) { return __builtin_amdgcn_logf(x); }
+
+// Base-2 logarithm.  v_log_f32 alone is biased, and more so for larger
+// arguments (measured mean error against fp64: -8e-9 on [0.5, 1), -1.8e-7 on
+// [4, 32), -3.4e-7 on [1, 512)).  The scans take two logarithms of sums of up
+// to a few hundred terms per step, so that bias accumulated along the level
+// chains (about -1e-7 log2 units per step).  Here x = m * 2^e is split exactly
+// (v_frexp_mant / v_frexp_exp, m in [0.5, 1)) and only m goes through v_log_f32;
+// e is added exactly, with the sum rounded to nearest.  x = 0 gives -inf (m = 0),
+// x = +inf gives +inf, NaN stays NaN.
+__device__ __forceinline__ float log2_hw(float x) {
+  const float e = (float)__builtin_amdgcn_frexp_expf(x);
+  return e + __builtin_amdgcn_logf(__builtin_amdgcn_frexp_mantf(x));
+}
 
 __device__ __forceinline__ float fmax2(float a, float b) { return __builtin_fmaxf(a, b); }
 

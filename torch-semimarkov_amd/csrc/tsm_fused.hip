@@ -12,8 +12,16 @@
 //   transitions G[c',c] = sum_t 2^(alpha-hat[t,c'] + trans[c',c] log2 e - u[t,c]) S[t,c]
 //               (the softmax weight of source c' times the start sum), per row
 //               block in fp64;
+//   coverage    every position lies in exactly one segment: the marginals of the
+//               segments covering one position of each chunk sum to 1; the pass
+//               measures that sum and divides the chunk's factor by it, which
+//               removes the slowly varying scale error that rounding in the long
+//               alpha / beta level chains leaves (see coverage_kernel);
 //   shared      grad_db = sum_j f_j db_part[j], grad_tr = sum of the row blocks,
 //               both weighted by grad_output, in a fixed order.
+#include <stdlib.h>
+#include <string.h>
+
 #include <algorithm>
 
 #include "tsm_device.hpp"
@@ -148,6 +156,104 @@ __global__ void __launch_bounds__(256) u_rows_kernel(FusedParams f) {
     for (; cs < C; ++cs) s0 += exp2_hw((a[cs] + tc[cs * C]) - m);
     uo[i] = m + log2_hw((s0 + s1) + (s2 + s3));
   }
+}
+
+// ---- coverage: every position lies in exactly one segment ----
+// One block per backward chunk j >= 1 evaluates, at t_ref = t_lo - 1 (t_lo = j*Lc),
+// cov_j = sum over the segments [s, s+k) covering t_ref (t_ref-Kmax < s <= t_ref < s+k,
+// s+k <= len) and labels c of 2^(A[s,c] + seg(s,k,c) + beta_j[s+k,c] + offs_j - log2 Z)
+// with A = alpha level + u (+ proj_start) and beta_j the chunk's own beta state at
+// positions t_lo .. t_lo+Kmax-1, recorded for verification (st_end / lv_end).  In
+// exact arithmetic cov_j = 1.  Rounding in the fp32 per-step results of the alpha /
+// beta level chains (summed over up to 10^6 steps) leaves the marginals off by a
+// slowly varying factor (measured up to ~5e-5 at T = 10^6); the chunk's marginals
+// and this window share it, so the chunk factor f_j is divided by cov_j.  Chunk 0
+// uses position 0, covered by the segments starting there (its start sums).  A
+// value far from 1 (not a rounding drift) is left alone.
+// LDS of coverage_kernel: ew (Kmax, C) fp32, the window's levels (Kmax) fp64, and,
+// when they fit, the log2-scaled duration biases of durations 1..Kmax (Kmax, C).
+inline size_t coverage_lds(int C, int Kmax, bool dbl) {
+  return (size_t)Kmax * 8 + (size_t)Kmax * C * 4 * (dbl ? 2 : 1);
+}
+
+template <bool DBL>
+__global__ void __launch_bounds__(1024) coverage_kernel(FusedParams f) {
+  extern __shared__ __align__(16) char csm[];
+  __shared__ double red[1024 / 64];
+  const int b = blockIdx.y, j = blockIdx.x;
+  const int C = f.C, T = f.T, Lc = f.Lc, K = f.K, Kmax = f.Kmax;
+  const int len = flen(f.lengths, b, T);
+  const int jl = len > 0 ? (len - 1) / Lc : 0;
+  if (len == 0 || j > jl) return;
+  double acc = 0.0;
+  if (j == 0) {
+    for (int c = threadIdx.x; c < C; c += blockDim.x) acc += (double)f.s_out[(size_t)b * (T + 1) * C + c];
+  } else {
+    // lvs[i]: the chunk's level at t_lo + i; ew[i, c]: its beta state there plus the
+    // content (cum[t_lo+i,c] - cum[t_ref,c]) log2 e (fp32: the level is kept apart);
+    // dbl[k-1, c] = duration_bias[min(k, K-1), c] log2 e
+    double* lvs = reinterpret_cast<double*>(csm);
+    float* ew = reinterpret_cast<float*>(csm + (size_t)Kmax * 8);
+    float* dbl = ew + (size_t)Kmax * C;
+    const int t_lo = j * Lc, t_ref = t_lo - 1;
+    const int s0 = max(0, t_ref - Kmax + 1);
+    const size_t item = (size_t)b * f.P + j;
+    const float* st = f.st_end + item * Kmax * C;
+    const float* cum_b = f.cum + (size_t)b * (T + 1) * C;
+    const float* cref = cum_b + (size_t)t_ref * C;
+    const int ni = min(Kmax, len - t_lo + 1);  // positions t_lo .. min(len, t_lo+Kmax-1)
+    for (int i = threadIdx.x; i < ni; i += blockDim.x) lvs[i] = f.lv_end[item * Kmax + i];
+    for (int idx = threadIdx.x; idx < ni * C; idx += blockDim.x) {
+      const int i = idx / C, c = idx % C;
+      ew[idx] = st[idx] + (cum_b[(size_t)(t_lo + i) * C + c] - cref[c]) * kLog2e;
+    }
+    if constexpr (DBL) {
+      for (int idx = threadIdx.x; idx < Kmax * C; idx += blockDim.x) {
+        const int k = 1 + idx / C, c = idx % C;
+        dbl[idx] = f.db[(size_t)(K == 1 ? 0 : min(k, K - 1)) * C + c] * kLog2e;
+      }
+    }
+    __syncthreads();
+    const double base = f.offs[item] - f.z2[b];
+    const int n = (t_ref - s0 + 1) * C;
+    for (int w = threadIdx.x; w < n; w += blockDim.x) {
+      const int s = s0 + w / C, c = w % C;
+      const double al = f.alvl[(size_t)b * (T + 1) + s] + base;
+      float a = f.uval[((size_t)b * (T + 1) + s) * C + c] - (cum_b[(size_t)s * C + c] - cref[c]) * kLog2e;
+      if (f.ps != nullptr) a += f.ps[((size_t)b * T + s) * C + c] * kLog2e;
+      const int k0 = t_ref - s + 1, k1 = min(Kmax, len - s);
+      float sk0 = 0.0f, sk1 = 0.0f;
+#pragma unroll 4
+      for (int k = k0; k <= k1; ++k) {
+        const int i = s + k - t_lo;
+        const float dk = DBL ? dbl[(k - 1) * C + c] : f.db[(size_t)(K == 1 ? 0 : min(k, K - 1)) * C + c] * kLog2e;
+        const float y = (float)(al + lvs[i]) + ((a + ew[i * C + c]) + dk);
+        if (k & 1) sk1 += exp2_hw(y);
+        else sk0 += exp2_hw(y);
+      }
+      acc += (double)(sk0 + sk1);
+    }
+  }
+  for (int m = 32; m >= 1; m >>= 1) acc += __shfl_xor(acc, m, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double cov = 0.0;
+    for (int i = 0; i < (int)(blockDim.x >> 6); ++i) cov += red[i];
+    double* fj = f.mframe + (size_t)b * f.P + j;
+    if (j == 0) cov *= *fj;  // start sums are in the chunk frame
+    if (cov > 0.5 && cov < 2.0) *fj /= cov;
+  }
+}
+
+template <bool DBL>
+hipError_t launch_coverage(const Plan& pl, const FusedParams& f, hipStream_t s) {
+  const size_t lds = coverage_lds(pl.C, pl.Kmax, DBL);
+  const hipError_t e =
+      hipFuncSetAttribute((const void*)coverage_kernel<DBL>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(coverage_kernel<DBL>, dim3(pl.P, pl.B), dim3(1024), lds, s, f);
+  return hipSuccess;
 }
 
 // ---- rows: grad_cum / projections ----
@@ -367,6 +473,14 @@ int launch_fused_finalize(const Plan& pl, const FusedParams& f, hipStream_t s) {
   {
     const int n = pl.B * pl.P;
     hipLaunchKernelGGL(frame_scale_kernel, dim3((n + 255) / 256), dim3(256), 0, s, f);
+  }
+  const char* cenv = getenv("TSM_COVERAGE");  // diagnostics: =0 skips the coverage correction
+  if (cenv == nullptr || strcmp(cenv, "0") != 0) {
+    TimedLaunch tl(kKCoverage, s);
+    // fused plans have C <= 64 and Kmax <= 512: ew and the levels always fit LDS
+    const hipError_t e = coverage_lds(pl.C, pl.Kmax, true) <= 160 * 1024 ? launch_coverage<true>(pl, f, s)
+                                                                           : launch_coverage<false>(pl, f, s);
+    if (e != hipSuccess) return e;
   }
   int gx = (int)(((size_t)(pl.T + 1) * pl.C + 255) / 256);
   if (gx > 4096) gx = 4096;

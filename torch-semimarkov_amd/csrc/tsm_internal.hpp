@@ -113,6 +113,7 @@ struct FinalParams {
   float* grad_tr;            // (C, C)
   float* grad_db;            // (K, C)
   int trows;                 // grad_tr is (trows, C, C) when > 0
+  const double* bscale;      // (B, NB) block scales of the coverage pass, or null (1)
 };
 
 // Row passes of the backward with fused marginals (tsm_fused.hip).
@@ -131,6 +132,15 @@ struct FusedParams {
   const float* halo;       // (B*P, Kmax, C)
   const double* db_part;   // (B*P, Kmax, C)
   double* tr_part;         // (B*GNB, C, C)
+  // coverage pass: inputs, the forward's levels and log2 Z, the backward chunks'
+  // recorded beta states (positions t_lo .. t_lo+Kmax-1 of chunk j >= 1)
+  const float* cum;        // (B, T+1, C)
+  const float* db;         // (K, C)
+  const float* ps;         // (B, T, C) or null
+  const double* alvl;      // (B, T+1)
+  const double* z2;        // (B)
+  const float* st_end;     // (B*P, Kmax, C)
+  const double* lv_end;    // (B*P, Kmax)
   const float* grad_output;
   float* grad_cum;
   float* grad_ps;
@@ -247,6 +257,7 @@ int launch_margfast_j16_hi(const Plan& pl, const MargParams& q, hipStream_t s);
 int launch_margfast_j16_wide(const Plan& pl, const MargParams& q, hipStream_t s);  // 64 < C <= 128
 int launch_marginals(const Plan& pl, const MargParams& q, hipStream_t s);
 int launch_finalize(const Plan& pl, const FinalParams& f, hipStream_t s);
+int launch_block_coverage(const Plan& pl, const MargParams& q, double* bscale, hipStream_t s);
 int launch_viterbi(const Plan& pl, const ViterbiParams& v, hipStream_t s);
 // duration-dependent transitions: log2-scaled tables of both directions
 // (trf [k-1][c_dst][c_src], trb [k-1][c_src][c_dst]), dense scans and marginals
@@ -284,6 +295,7 @@ enum KernelId : int {
   kKTransGrad,
   kKFusedRows,
   kKFusedShared,
+  kKCoverage,
   kNumKernels
 };
 

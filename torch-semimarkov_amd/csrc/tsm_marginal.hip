@@ -22,6 +22,8 @@
 namespace tsm {
 namespace {
 
+constexpr double kLog2eM = 1.4426950408889634;  // log2(e) in fp64
+
 constexpr int kTRegMax = 8;  // register accumulators per lane for the transition gradient
 
 __device__ inline int mlen(const int64_t* lengths, int b, int T) {
@@ -233,6 +235,65 @@ __global__ void __launch_bounds__(512) marginal_kernel(MargParams q) {
 }
 
 // grad_cum / proj grads from the end and start sums, scaled by grad_output.
+// Per-block scale of the separate marginals.  Every position lies in exactly one
+// segment, so the marginals of the segments covering one position sum to 1.
+// Rounding in the fp32 per-step results of the long alpha / beta level chains
+// leaves the marginals off by a slowly varying factor; block nb >= 1 measures it
+// at t_ref = nb*TB - 1 from the stored alpha and beta tables (every segment
+// [s, s+k) with t_ref - Kmax < s <= t_ref < s+k <= len, all labels) and the
+// finalize divides the block's sums by it.  Block 0 uses position 0, covered by
+// the segments starting there (its start sums).  A value far from 1 (not a
+// rounding drift) leaves the block alone (scale 1).  Static transitions, log
+// semiring only (the launcher decides).
+__global__ void __launch_bounds__(1024) block_coverage_kernel(MargParams q, double* bscale) {
+  __shared__ double red[1024 / 64];
+  const int b = blockIdx.y, nb = blockIdx.x;
+  const int C = q.C, T = q.T, K = q.K, Kmax = q.Kmax;
+  const int len = mlen(q.lengths, b, T);
+  double acc = 0.0;
+  const bool live = len > 0 && nb * q.TB < len;
+  if (live && nb == 0) {
+    for (int c = threadIdx.x; c < C; c += blockDim.x) acc += (double)q.s_out[(size_t)b * (T + 1) * C + c];
+  } else if (live) {
+    const int t_ref = nb * q.TB - 1;
+    const int s0 = max(0, t_ref - Kmax + 1);
+    const size_t row0 = (size_t)b * (T + 1);
+    const float* cum_b = q.cum + row0 * C;
+    const int n = (t_ref - s0 + 1) * C;
+    for (int w = threadIdx.x; w < n; w += blockDim.x) {
+      const int s = s0 + w / C, c = w % C;
+      // forward side: alpha level + u[s,c] (+ proj_start) - cum[s,c] log2 e - log2 Z
+      const float* ah = q.aval + (row0 + s) * C;
+      float mu = kMinusInf;
+      for (int cp = 0; cp < C; ++cp) mu = fmax2(mu, ah[cp] + q.trans[(size_t)cp * C + c] * kLog2e);
+      float su = 0.0f;
+      for (int cp = 0; cp < C; ++cp) su += exp2_hw((ah[cp] + q.trans[(size_t)cp * C + c] * kLog2e) - mu);
+      float ua = mu + log2_hw(su);
+      if (q.ps != nullptr) ua += q.ps[((size_t)b * T + s) * C + c] * kLog2e;
+      const double A = (q.alvl[row0 + s] + (double)ua) - (double)cum_b[(size_t)s * C + c] * kLog2eM - q.z2[b];
+      const int k0 = t_ref - s + 1, k1 = min(Kmax, len - s);
+      float sk = 0.0f;
+      for (int k = k0; k <= k1; ++k) {
+        const int e = s + k;
+        float xb = q.bval[(row0 + e) * C + c];
+        if (q.pe != nullptr) xb += q.pe[((size_t)b * T + e - 1) * C + c] * kLog2e;
+        const double x = (q.blvl[row0 + e] + (double)xb) + (double)cum_b[(size_t)e * C + c] * kLog2eM;
+        const float dk = q.db[(size_t)(K == 1 ? 0 : min(k, K - 1)) * C + c] * kLog2e;
+        sk += exp2_hw((float)(A + x) + dk);
+      }
+      acc += (double)sk;
+    }
+  }
+  for (int m = 32; m >= 1; m >>= 1) acc += __shfl_xor(acc, m, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double cov = 0.0;
+    for (int i = 0; i < (int)(blockDim.x >> 6); ++i) cov += red[i];
+    bscale[(size_t)b * q.NB + nb] = (live && cov > 0.5 && cov < 2.0) ? 1.0 / cov : 1.0;
+  }
+}
+
 __global__ void finalize_rows_kernel(FinalParams f) {
   const int b = blockIdx.y;
   const int C = f.C, T = f.T;
@@ -245,12 +306,17 @@ __global__ void finalize_rows_kernel(FinalParams f) {
     float E = 0.0f, S = 0.0f;
     if (t <= len) {
       const int blk = t / f.TB, t0 = blk * f.TB;
+      // block scales (coverage pass), 1 without it
+      const float ks = (f.bscale != nullptr && blk < f.NB) ? (float)f.bscale[(size_t)b * f.NB + blk] : 1.0f;
       if (t > 0) {
         // own part: written by block blk (absent when t == NB*TB, i.e. t == T)
-        if (blk < f.NB) E = f.e_own[o];
-        if (blk >= 1 && t - t0 < f.Kmax) E += f.halo[(((size_t)b * f.NB + blk - 1) * f.Kmax + (t - t0)) * C + c];
+        if (blk < f.NB) E = ks * f.e_own[o];
+        if (blk >= 1 && t - t0 < f.Kmax) {
+          const float kp = f.bscale != nullptr ? (float)f.bscale[(size_t)b * f.NB + blk - 1] : 1.0f;
+          E += kp * f.halo[(((size_t)b * f.NB + blk - 1) * f.Kmax + (t - t0)) * C + c];
+        }
       }
-      if (t < len) S = f.s_out[o];
+      if (t < len) S = ks * f.s_out[o];
     }
     f.grad_cum[o] = g * (E - S);
     if (f.grad_ps != nullptr && t < T) f.grad_ps[((size_t)b * T + t) * C + c] = g * S;
@@ -292,7 +358,8 @@ __global__ void __launch_bounds__(256) finalize_shared_kernel(FinalParams f) {
   }
   double acc = 0.0;
   if (src != nullptr)
-    for (int j = lane; j < nparts; j += 64) acc += (double)f.grad_output[j / f.NB] * src[(size_t)j * per + off];
+    for (int j = lane; j < nparts; j += 64)
+      acc += (double)f.grad_output[j / f.NB] * (f.bscale != nullptr ? f.bscale[j] : 1.0) * src[(size_t)j * per + off];
   for (int m = 32; m >= 1; m >>= 1) acc += __shfl_xor(acc, m, 64);
   if (lane == 0) {
     if (idx < n_tr) f.grad_tr[idx] = (float)acc;
@@ -353,6 +420,12 @@ int launch_marginals(const Plan& pl, const MargParams& q, hipStream_t s) {
     case 64: return launch_marg_j<64>(pl, q, s);
     default: return (int)hipErrorInvalidValue;
   }
+}
+
+int launch_block_coverage(const Plan& pl, const MargParams& q, double* bscale, hipStream_t s) {
+  TimedLaunch tl(kKCoverage, s);
+  hipLaunchKernelGGL(block_coverage_kernel, dim3(q.NB, pl.B), dim3(1024), 0, s, q, bscale);
+  return hipGetLastError();
 }
 
 int launch_finalize(const Plan& pl, const FinalParams& f, hipStream_t s) {

@@ -23,7 +23,7 @@ const char* const kNames[kNumKernels] = {
     "finalize_shared_kernel", "checkpoints_kernel", "viterbi_kernel",       "backtrace_kernel",
     "retry_kernel",      "dense_prep_kernel",    "gold_kernels",
     "prologue_kernels",  "u_rows_kernel",        "trans_grad_kernel",       "fused_rows_kernel",
-    "fused_shared_kernel",
+    "fused_shared_kernel", "coverage_kernels",
 };
 
 struct Pending {

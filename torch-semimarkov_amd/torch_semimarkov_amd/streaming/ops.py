@@ -39,6 +39,19 @@ def _trans_rows(transition: Tensor) -> int:
     return int(transition.shape[0]) if transition.dim() == 3 else 0
 
 
+def _check_cooperative(rec: Tensor, B: int, T: int, C: int, K: int, semiring: int, tr_rows: int, what: str) -> None:
+    """The cooperative scans (label sets whose rings need several CUs) bound every
+    wait on their partner blocks; a group that gives up marks its sequences with
+    recomputed = -1 and NaN results.  For those plans only, read the marks (one
+    host synchronisation) and raise instead of returning NaN."""
+    if semiring != N.TSM_SEMIRING_LOG or tr_rows != 0 or not N.plan_info(B, T, C, K)["coop"]:
+        return
+    bad = torch.nonzero(rec < 0).flatten().tolist()
+    if bad:
+        raise RuntimeError(f"{what}: the cooperative scan gave up waiting for its partner blocks "
+                           f"(sequences {bad[:8]}); the results would be NaN")
+
+
 # --------------------------------------------------------------------------- forward
 @torch.library.custom_op("tsm_amd::scan_forward", mutates_args=())
 def scan_forward(
@@ -71,6 +84,7 @@ def scan_forward(
             N.ptr(rec), N.ptr(ws), ws.numel(), _stream(dev),
         )
     N.check(rc, "tsm_forward")
+    _check_cooperative(rec, B, T, C, K, semiring, tr_rows, "tsm_forward")
     return part, z2, ah, al, rec
 
 
@@ -116,6 +130,7 @@ def scan_backward(
             N.ptr(ws), ws.numel(), _stream(dev),
         )
     N.check(rc, "tsm_backward")
+    _check_cooperative(rec, B, T, C, K, semiring, tr_rows, "tsm_backward")
     empty = torch.empty(0, device=dev, dtype=torch.float32)
     return g_cum, g_tr, g_db, g_ps if g_ps is not None else empty, g_pe if g_pe is not None else empty.clone(), rec
 
