@@ -113,6 +113,31 @@ int tsm_forward(const float* cum_scores, const float* transition, const float* d
                 size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * tsm_forward without a workspace argument: for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  No counterpart in the reference, whose launchers
+ * always allocate through torch.
+ * Same arguments, outputs and results as tsm_forward (the same kernels run);
+ * the workspace is a static device array of TSM_NOALLOC_SCRATCH_BYTES in the
+ * library, one per GPU, allocated when the library's code is loaded on that
+ * GPU and held until the process ends.  The call allocates nothing (no
+ * hipMalloc / hipFree, no allocating library routine).
+ *   - A problem whose workspace (tsm_forward_workspace) exceeds
+ *     TSM_NOALLOC_SCRATCH_BYTES is refused with TSM_ERR_UNSUPPORTED before
+ *     anything is launched.
+ *   - Every call on one GPU shares that GPU's scratch: calls that overlap in
+ *     time on one GPU (different streams or threads without ordering) race and
+ *     give wrong results.  Calls ordered on one stream are safe; each call
+ *     initialises what it reads of the scratch.
+ * ------------------------------------------------------------------------- */
+#define TSM_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int tsm_forward_noalloc(const float* cum_scores, const float* transition, const float* duration_bias,
+                        const int64_t* lengths, const float* proj_start, const float* proj_end, int64_t B,
+                        int64_t T, int64_t C, int64_t K, int64_t trans_rows, int semiring, float* partition,
+                        double* log2_partition, float* alpha_hat, double* alpha_level, int32_t* recomputed,
+                        void* stream);
+
+/* ---------------------------------------------------------------------------
  * Backward: gradients of sum_b grad_output[b] * partition[b].
  * Replaces:
  *   streaming/triton_backward.py:556-790  launch_streaming_triton_backward

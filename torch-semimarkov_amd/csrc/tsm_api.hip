@@ -793,7 +793,8 @@ int tsm_forward_workspace(int64_t B, int64_t T, int64_t C, int64_t K, int64_t tr
 
 namespace {
 
-// tsm_forward's work on a given workspace.
+// tsm_forward's work on a given workspace (the caller's, or the static scratch of
+// tsm_forward_noalloc).
 int forward_impl(const float* cum, const float* tr, const float* db, const int64_t* len, const float* ps,
                  const float* pe, int64_t B, int64_t T, int64_t C, int64_t K, int64_t trans_rows, int semiring,
                  float* partition, double* log2_partition, float* alpha_hat, double* alpha_level,
@@ -830,6 +831,41 @@ int forward_impl(const float* cum, const float* tr, const float* db, const int64
   return TSM_OK;
 }
 
+// Scratch of tsm_forward_noalloc: a file-scope device array, so a call needs no
+// allocation.  Every device holds its own copy (allocated with the code object,
+// kept until the process ends).  In host code `scratch` names a host-side
+// stand-in, not device memory: its device address on the current device comes
+// from hipGetSymbolAddress, once per device, and only that address is used.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices];
+
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[TSM_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+// The device address of `scratch` on the current device (looked up on the first
+// call on each device, with that device current).
+int scratch_address(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "tsm_forward_noalloc (hipGetDevice)");
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(TSM_ERR_UNSUPPORTED, "tsm_forward_noalloc: device index %d outside [0, %d)", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch_dev[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "tsm_forward_noalloc (hipGetSymbolAddress of the scratch array)");
+    if (p == nullptr) return fail(TSM_ERR_HIP, "tsm_forward_noalloc: hipGetSymbolAddress returned NULL");
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return TSM_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -840,6 +876,31 @@ int tsm_forward(const float* cum, const float* tr, const float* db, const int64_
                 void* workspace, size_t ws_bytes, void* stream) {
   return forward_impl(cum, tr, db, len, ps, pe, B, T, C, K, trans_rows, semiring, partition, log2_partition,
                       alpha_hat, alpha_level, recomputed, workspace, ws_bytes, stream, "tsm_forward");
+}
+
+int tsm_forward_noalloc(const float* cum, const float* tr, const float* db, const int64_t* len, const float* ps,
+                        const float* pe, int64_t B, int64_t T, int64_t C, int64_t K, int64_t trans_rows,
+                        int semiring, float* partition, double* log2_partition, float* alpha_hat,
+                        double* alpha_level, int32_t* recomputed, void* stream) {
+  // plan and size first (host only), so an oversized problem is refused before
+  // the scratch is touched
+  int rc = check_common(cum, tr, db, len, semiring);
+  if (rc) return rc;
+  Plan pl;
+  rc = make_plan(B, T, C, K, ps != nullptr, pe != nullptr, trans_rows, &pl);
+  if (rc) return rc;
+  const size_t need = forward_ws_bytes(pl, semiring);
+  if (need > (size_t)TSM_NOALLOC_SCRATCH_BYTES)
+    return fail(TSM_ERR_UNSUPPORTED,
+                "tsm_forward_noalloc: this problem needs %zu bytes of scratch, more than the %zu-byte static "
+                "scratch; call tsm_forward with a workspace of tsm_forward_workspace() bytes instead",
+                need, (size_t)TSM_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  rc = scratch_address(&ws);
+  if (rc) return rc;
+  return forward_impl(cum, tr, db, len, ps, pe, B, T, C, K, trans_rows, semiring, partition, log2_partition,
+                      alpha_hat, alpha_level, recomputed, ws, (size_t)TSM_NOALLOC_SCRATCH_BYTES, stream,
+                      "tsm_forward_noalloc");
 }
 
 int tsm_backward_workspace(int64_t B, int64_t T, int64_t C, int64_t K, int64_t trans_rows, int has_ps, int has_pe,

@@ -23,6 +23,7 @@ TSM_DTYPE_F16 = 2
 TSM_VITERBI_AUTO = 0
 TSM_VITERBI_EXACT = 1
 TSM_VITERBI_FACTORISED = 2
+TSM_NOALLOC_SCRATCH_BYTES = 64 << 20  # include/tsm_hip.h
 _ERRORS = {1: ValueError, 2: NotImplementedError, 3: RuntimeError, 4: RuntimeError}
 
 PLAN_FIELDS = (
@@ -47,6 +48,8 @@ _SIGNATURES = {
     "tsm_forward_workspace": ([_i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32, ctypes.POINTER(_sz)], _i32),
     "tsm_forward": (
         [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _p, _p, _p, _p, _p, _p, _sz, _p], _i32),
+    "tsm_forward_noalloc": (
+        [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _p, _p, _p, _p, _p, _p], _i32),
     "tsm_backward_workspace": ([_i64, _i64, _i64, _i64, _i64, _i32, _i32, ctypes.POINTER(_sz)], _i32),
     "tsm_backward": (
         [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _p, _p, _p, _p,
