@@ -397,6 +397,38 @@ def test_verifier_recomputes_non_mixing_chunks(scan_path):
     assert_grads(grads, g64)
 
 
+def test_speculation_threshold_within_gradient_bar(monkeypatch):
+    """Slowly mixing input (self-transition bonus 4, weak emissions): after the
+    warm-up, some speculative chunks' boundary spreads lie between the default
+    acceptance threshold (4e-6 log2 units, set from the gradient bar: an
+    accepted spread s moves a marginal by at most ~1.4 s relative) and 2e-4.
+    With TSM_SPEC_TOL=2e-4 those chunks are accepted as they are, so the result
+    differs from the default run, which runs them again; the default's partition
+    and gradients are within the bar of the fp64 oracle."""
+    from oracle import cref
+
+    monkeypatch.delenv("TSM_SCAN_PATH", raising=False)
+    B, T, C, K = 1, 8000, 6, 20
+    g = torch.Generator().manual_seed(77)
+    em = 0.3 * torch.randn(B, T, C, generator=g)
+    cum = torch.zeros(B, T + 1, C)
+    cum[:, 1:] = em.cumsum(1)
+    tr = 4.0 * torch.eye(C) - 4.0 / C + 0.05 * torch.randn(C, C, generator=g)
+    db = 0.1 * torch.randn(K, C, generator=g)
+    L = torch.tensor([T])
+    assert N.plan_info(B, T, C, K)["P"] > 8
+    monkeypatch.setenv("TSM_SPEC_TOL", "2e-4")
+    p_loose, g_loose = run_hip(cum, tr, db, L, K)
+    monkeypatch.delenv("TSM_SPEC_TOL")
+    part, grads = run_hip(cum, tr, db, L, K)
+    assert any(not torch.equal(a, b) for a, b in zip(g_loose, grads)), "no spread landed in (4e-6, 2e-4]"
+    ref = cref.backward(cum, tr, db, L, K)
+    np.testing.assert_allclose(part.double().numpy(), ref["logZ"], rtol=RTOL_Z)
+    for got, key in zip(grads, ("grad_cum", "grad_transition", "grad_duration_bias")):
+        want = ref[key] if key == "grad_cum" else ref[key].sum(0)
+        np.testing.assert_allclose(got.double().numpy(), want, **GRAD_TOL, err_msg=key)
+
+
 def test_grad_output_weighting_and_isolation(scan_path):
     """tests/test_streaming_triton.py:901-1087: shared grads are sum_b g_b * grad_b, per-sequence
     grads are scaled, a zero weight isolates a sequence."""
