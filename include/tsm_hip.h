@@ -48,7 +48,7 @@ extern "C" {
 #define TSM_DTYPE_BF16 1
 #define TSM_DTYPE_F16 2
 
-#define TSM_VITERBI_AUTO 0       /* factorised for large problems when it fits, else exact */
+#define TSM_VITERBI_AUTO 0       /* factorised for large or long problems when it fits, else exact */
 #define TSM_VITERBI_EXACT 1      /* the reference's fp32 operation order, bit-identical scores */
 #define TSM_VITERBI_FACTORISED 2 /* K*C + C^2 terms per step, chunked over all CUs */
 
@@ -177,9 +177,10 @@ int tsm_backward(const float* cum_scores, const float* transition, const float* 
  *                           with verification like the log-semiring scan:
  *                           scores within 1e-5 relative, segmentations identical
  *                           when no two candidates tie;
- *   TSM_VITERBI_AUTO        factorised for problems of >= 2^28 cells
- *                           (B*T*K*C^2) when the register-resident scan fits,
- *                           exact otherwise.
+ *   TSM_VITERBI_AUTO        factorised when the register-resident scan fits
+ *                           and the problem has >= 2^28 cells (B*T*K*C^2) or
+ *                           its plan cuts each sequence into several chunks
+ *                           (tsm_plan_info P >= 2); exact otherwise.
  * Duration-dependent transitions (trans_rows > 0) always run the exact kernel
  * (the factorisation does not hold; TSM_VITERBI_FACTORISED is refused).
  * Ties: the smallest duration, then the first source label, then the first

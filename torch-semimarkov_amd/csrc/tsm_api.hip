@@ -706,13 +706,17 @@ size_t viterbi_ws_bytes(const Plan& pl, int with_tb) {
   return cv.off + 256;
 }
 
-// Factorised Viterbi is used for algorithm 2, and for algorithm 0 on problems
-// of at least 2^28 cells (B*T*K*C^2) when the register-resident scan fits.
+// Factorised Viterbi is used for algorithm 2, and for algorithm 0 when the
+// register-resident scan fits and either the problem has at least 2^28 cells
+// (B*T*K*C^2) or the plan cuts each sequence into several chunks: the exact
+// kernel runs one workgroup per sequence through all T steps, so few long
+// sequences leave most CUs idle (cfg1, B=4 x 1000 steps: 3.2 ms) while the
+// chunked scan spreads them over the chip.
 bool viterbi_factorised(const Plan& pl, int algorithm) {
   if (algorithm == TSM_VITERBI_EXACT || !pl.fast || pl.dense) return false;
   if (algorithm == TSM_VITERBI_FACTORISED) return true;
   const double cells = (double)pl.B * pl.T * pl.K * (double)pl.C * pl.C;
-  return cells >= (double)(1 << 28);
+  return cells >= (double)(1 << 28) || pl.P >= 2;
 }
 
 // Gold-path scoring: sizes, LDS of the label window, workspace.
