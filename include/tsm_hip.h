@@ -249,6 +249,57 @@ int tsm_gold_score_backward(const int64_t* labels, const int64_t* lengths, int64
                             size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Emission input: forward, backward, Viterbi and gold-path score on the
+ * projected scores (B, T, C) fp32, T >= 1, instead of cumulative scores.
+ * Replaces the head's prologue + scan (nn.py:196-220: cum_scores built with
+ * torch.zeros + cumsum, then semi_crf_streaming_forward) and its gold score
+ * (nn.py:297, helpers.py:365-544) -- the emission prologue fused into the
+ * scans' streamed loads (cum[t] = sum_{u<t} scores[u] in fp64, as the
+ * prologue computes it).  Arguments and outputs as the cumulative-score entry
+ * points, with:
+ *   tsm_backward_emissions   grad_scores (B, T, C) = d/dscores, already scaled by
+ *                            grad_output[b] (the suffix sums of the cum gradient)
+ *   tsm_gold_score_emissions_backward  grad_scores[b,t,c] = grad_output[b] *
+ *                            [t < len and labels[b,t] == c]
+ * The register-resident scans and marginals read the scores themselves and
+ * build no (B, T+1, C) tensor; plans that run other kernels (tsm_plan_info:
+ * fast = 0, coop = 1 or dense = 1, the max semiring forward / backward, the
+ * exact Viterbi kernel) build cum in the workspace first.  The gold score uses
+ * the workspace of tsm_gold_score_workspace.
+ * ------------------------------------------------------------------------- */
+int tsm_forward_emissions_workspace(int64_t B, int64_t T, int64_t C, int64_t K, int64_t trans_rows, int semiring,
+                                    int has_proj_start, int has_proj_end, size_t* bytes);
+int tsm_forward_emissions(const float* scores, const float* transition, const float* duration_bias,
+                          const int64_t* lengths, const float* proj_start, const float* proj_end, int64_t B,
+                          int64_t T, int64_t C, int64_t K, int64_t trans_rows, int semiring, float* partition,
+                          double* log2_partition, float* alpha_hat, double* alpha_level, int32_t* recomputed,
+                          void* workspace, size_t workspace_bytes, void* stream);
+int tsm_backward_emissions_workspace(int64_t B, int64_t T, int64_t C, int64_t K, int64_t trans_rows, int semiring,
+                                     int has_proj_start, int has_proj_end, size_t* bytes);
+int tsm_backward_emissions(const float* scores, const float* transition, const float* duration_bias,
+                           const int64_t* lengths, const float* proj_start, const float* proj_end, int64_t B,
+                           int64_t T, int64_t C, int64_t K, int64_t trans_rows, int semiring,
+                           const float* alpha_hat, const double* alpha_level, const double* log2_partition,
+                           const float* grad_output, float* grad_scores, float* grad_transition,
+                           float* grad_duration_bias, float* grad_proj_start, float* grad_proj_end,
+                           int32_t* recomputed, void* workspace, size_t workspace_bytes, void* stream);
+int tsm_viterbi_emissions_workspace(int64_t B, int64_t T, int64_t C, int64_t K, int64_t trans_rows,
+                                    int with_traceback, int algorithm, size_t* bytes);
+int tsm_viterbi_emissions(const float* scores, const float* transition, const float* duration_bias,
+                          const int64_t* lengths, const float* proj_start, const float* proj_end, int64_t B,
+                          int64_t T, int64_t C, int64_t K, int64_t trans_rows, float* score, int with_traceback,
+                          int algorithm, int32_t* seg_count, int32_t* segments, void* workspace,
+                          size_t workspace_bytes, void* stream);
+int tsm_gold_score_emissions(const float* scores, const float* transition, const float* duration_bias,
+                             const int64_t* labels, const int64_t* lengths, int64_t B, int64_t T, int64_t C,
+                             int64_t K, int64_t db_rows, float* score, void* workspace, size_t workspace_bytes,
+                             void* stream);
+int tsm_gold_score_emissions_backward(const int64_t* labels, const int64_t* lengths, int64_t B, int64_t T,
+                                      int64_t C, int64_t K, int64_t db_rows, const float* grad_output,
+                                      float* grad_scores, float* grad_transition, float* grad_duration_bias,
+                                      void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Ring checkpoints in the reference's layout (B, n_ckpt, K, C), raw alpha in
  * natural log units, rebuilt from tsm_forward's alpha_hat/alpha_level.
  * Replaces the ring_checkpoints output of

@@ -820,8 +820,9 @@ namespace {
 int forward_impl(const float* cum, const float* tr, const float* db, const int64_t* len, const float* ps,
                  const float* pe, int64_t B, int64_t T, int64_t C, int64_t K, int64_t trans_rows, int semiring,
                  float* partition, double* log2_partition, float* alpha_hat, double* alpha_level,
-                 int32_t* recomputed, void* workspace, size_t ws_bytes, void* stream, const char* what) {
-  int rc = check_common(cum, tr, db, len, semiring);
+                 int32_t* recomputed, void* workspace, size_t ws_bytes, void* stream, const char* what,
+                 const float* emit = nullptr) {
+  int rc = check_common(emit != nullptr ? emit : cum, tr, db, len, semiring);
   if (rc) return rc;
   if (!partition) return fail(TSM_ERR_INVALID, "partition output is required");
   if ((alpha_hat == nullptr) != (alpha_level == nullptr))
@@ -837,6 +838,7 @@ int forward_impl(const float* cum, const float* tr, const float* db, const int64
   ScanWs w = carve_scan(cv, pl, forward_generic(pl, semiring));
   const DenseTr dt = carve_dense(cv, pl);
   tsm::ScanParams p = scan_params(pl, w, cum, tr, db, len, ps, pe);
+  p.emit = emit;
   if (pl.dense) {
     const int e = tsm::launch_dense_prep(pl, tr, dt.trf, dt.trb, (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(e, "tsm_forward (transition tables)");
@@ -935,13 +937,20 @@ int tsm_backward_workspace(int64_t B, int64_t T, int64_t C, int64_t K, int64_t t
   return TSM_OK;
 }
 
-int tsm_backward(const float* cum, const float* tr, const float* db, const int64_t* len, const float* ps,
-                 const float* pe, int64_t B, int64_t T, int64_t C, int64_t K, int64_t trans_rows, int semiring,
-                 const float* alpha_hat,
-                 const double* alpha_level, const double* log2_partition, const float* grad_output,
-                 float* grad_cum, float* grad_tr, float* grad_db, float* grad_ps, float* grad_pe,
-                 int32_t* recomputed, void* workspace, size_t ws_bytes, void* stream) {
-  int rc = check_common(cum, tr, db, len, semiring);
+}  // extern "C"
+
+namespace {
+
+// tsm_backward's work.  emit != null (the emission entry point, on a plan whose
+// kernels read projected scores): the kernels take emit in place of cum, and
+// grad_cum is the (B, T, C) output with row t >= 1 of the cum gradient at row
+// t-1, which the caller turns into the score gradient in place.
+int backward_impl(const float* cum, const float* emit, const float* tr, const float* db, const int64_t* len,
+                  const float* ps, const float* pe, int64_t B, int64_t T, int64_t C, int64_t K, int64_t trans_rows,
+                  int semiring, const float* alpha_hat, const double* alpha_level, const double* log2_partition,
+                  const float* grad_output, float* grad_cum, float* grad_tr, float* grad_db, float* grad_ps,
+                  float* grad_pe, int32_t* recomputed, void* workspace, size_t ws_bytes, void* stream) {
+  int rc = check_common(emit != nullptr ? emit : cum, tr, db, len, semiring);
   if (rc) return rc;
   if (!alpha_hat || !alpha_level || !log2_partition || !grad_output || !grad_cum || !grad_tr || !grad_db)
     return fail(TSM_ERR_INVALID, "alpha_hat, alpha_level, log2_partition, grad_output and the gradient outputs are required");
@@ -969,8 +978,12 @@ int tsm_backward(const float* cum, const float* tr, const float* db, const int64
   double* tr_part = bw.tr_part;
 
   tsm::ScanParams p = scan_params(pl, w, cum, tr, db, len, ps, pe);
+  p.emit = emit;
+  const int shift = emit != nullptr ? 1 : 0;
   if (pl.mfused) {
     tsm::FusedParams f{};
+    f.emit = emit;
+    f.shift = shift;
     f.lengths = len;
     f.trans = tr;
     f.aval = alpha_hat;
@@ -1040,6 +1053,7 @@ int tsm_backward(const float* cum, const float* tr, const float* db, const int64
 
   tsm::MargParams q{};
   q.cum = cum;
+  q.emit = emit;
   q.trans = tr;
   q.db = db;
   q.lengths = len;
@@ -1102,9 +1116,26 @@ int tsm_backward(const float* cum, const float* tr, const float* db, const int64
   f.grad_tr = grad_tr;
   f.grad_db = grad_db;
   f.bscale = coverage ? bw.bscale : nullptr;
+  f.shift = shift;
   e = tsm::launch_finalize(pl, f, st);
   if (e != hipSuccess) return hip_fail(e, "tsm_backward (finalize)");
   return TSM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tsm_backward(const float* cum, const float* tr, const float* db, const int64_t* len, const float* ps,
+                 const float* pe, int64_t B, int64_t T, int64_t C, int64_t K, int64_t trans_rows, int semiring,
+                 const float* alpha_hat,
+                 const double* alpha_level, const double* log2_partition, const float* grad_output,
+                 float* grad_cum, float* grad_tr, float* grad_db, float* grad_ps, float* grad_pe,
+                 int32_t* recomputed, void* workspace, size_t ws_bytes, void* stream) {
+  if (!cum) return fail(TSM_ERR_INVALID, "cum_scores, transition, duration_bias and lengths are required");
+  return backward_impl(cum, nullptr, tr, db, len, ps, pe, B, T, C, K, trans_rows, semiring, alpha_hat, alpha_level,
+                       log2_partition, grad_output, grad_cum, grad_tr, grad_db, grad_ps, grad_pe, recomputed,
+                       workspace, ws_bytes, stream);
 }
 
 int tsm_viterbi_workspace(int64_t B, int64_t T, int64_t C, int64_t K, int64_t trans_rows, int with_tb,
@@ -1117,11 +1148,18 @@ int tsm_viterbi_workspace(int64_t B, int64_t T, int64_t C, int64_t K, int64_t tr
   return TSM_OK;
 }
 
-int tsm_viterbi(const float* cum, const float* tr, const float* db, const int64_t* len, const float* ps,
-                const float* pe, int64_t B, int64_t T, int64_t C, int64_t K, int64_t trans_rows, float* score,
-                int with_tb, int algorithm, int32_t* seg_count, int32_t* segments, void* workspace, size_t ws_bytes,
-                void* stream) {
-  int rc = check_common(cum, tr, db, len, TSM_SEMIRING_MAX);
+}  // extern "C"
+
+namespace {
+
+// tsm_viterbi's work.  emit != null (the emission entry point): the factorised
+// scan reads the projected scores; the exact kernel is never given them (the
+// caller builds cum first for a call that runs it).
+int viterbi_impl(const float* cum, const float* emit, const float* tr, const float* db, const int64_t* len,
+                 const float* ps, const float* pe, int64_t B, int64_t T, int64_t C, int64_t K, int64_t trans_rows,
+                 float* score, int with_tb, int algorithm, int32_t* seg_count, int32_t* segments, void* workspace,
+                 size_t ws_bytes, void* stream) {
+  int rc = check_common(emit != nullptr ? emit : cum, tr, db, len, TSM_SEMIRING_MAX);
   if (rc) return rc;
   if (!score) return fail(TSM_ERR_INVALID, "score output is required");
   if (with_tb && (!seg_count || !segments)) return fail(TSM_ERR_INVALID, "traceback needs seg_count and segments");
@@ -1148,6 +1186,7 @@ int tsm_viterbi(const float* cum, const float* tr, const float* db, const int64_
     const tsm::BtPlan btp = tsm::backtrace_plan(pl.B, pl.T, pl.C, pl.Kmax);
     void* bt_ws = with_tb ? cv.take<char>(tsm::backtrace_ws_bytes(btp, pl.B)) : nullptr;
     tsm::ScanParams p = scan_params(pl, w, cum, tr, db, len, ps, pe);
+    p.emit = emit;
     p.val = nullptr;
     p.lvl = nullptr;
     p.zout = score;
@@ -1164,6 +1203,7 @@ int tsm_viterbi(const float* cum, const float* tr, const float* db, const int64_
     }
     return TSM_OK;
   }
+  if (cum == nullptr) return fail(TSM_ERR_INVALID, "tsm_viterbi: the exact kernel needs cum_scores");
   const DeviceInfo di = device_info();
   const size_t lds = tsm::viterbi_lds_bytes(pl.C, pl.Kmax, pl.RS, ps != nullptr);
   if (lds > (size_t)di.max_lds)
@@ -1207,6 +1247,19 @@ int tsm_viterbi(const float* cum, const float* tr, const float* db, const int64_
   return TSM_OK;
 }
 
+}  // namespace
+
+extern "C" {
+
+int tsm_viterbi(const float* cum, const float* tr, const float* db, const int64_t* len, const float* ps,
+                const float* pe, int64_t B, int64_t T, int64_t C, int64_t K, int64_t trans_rows, float* score,
+                int with_tb, int algorithm, int32_t* seg_count, int32_t* segments, void* workspace, size_t ws_bytes,
+                void* stream) {
+  if (!cum) return fail(TSM_ERR_INVALID, "cum_scores, transition, duration_bias and lengths are required");
+  return viterbi_impl(cum, nullptr, tr, db, len, ps, pe, B, T, C, K, trans_rows, score, with_tb, algorithm,
+                      seg_count, segments, workspace, ws_bytes, stream);
+}
+
 int tsm_prologue_workspace(int64_t B, int64_t T, int64_t C, size_t* bytes) {
   if (!bytes) return fail(TSM_ERR_INVALID, "bytes is NULL");
   if (B < 1 || T < 1 || C < 1)
@@ -1246,6 +1299,12 @@ static int run_prologue(const void* x, int dtype, const float* g, int64_t B, int
   q.C = (int)C;
   q.NBL = (int)nbl;
   q.centre = centre ? 1 : 0;
+  q.GR = (int)T + 1;
+  q.goff = 0;
+  if (g != nullptr && g == gx) {  // the cum gradient held in grad_x itself, row u at row u-1
+    q.GR = (int)T;
+    q.goff = -1;
+  }
   const int e = tsm::launch_prologue(q, g != nullptr, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, what);
   return TSM_OK;
@@ -1317,6 +1376,241 @@ int tsm_gold_score_backward(const int64_t* labels, const int64_t* len, int64_t B
   g.gdb = grad_db;
   const int e = tsm::launch_gold_backward(g, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "tsm_gold_score_backward");
+  return TSM_OK;
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Emission input: the same passes on projected scores (B, T, C) instead of
+// cumulative scores.  The register-resident scans and marginals (and the
+// coverage passes) read the scores themselves and carry cum in registers, so
+// no (B, T+1, C) cumulative tensor is built; a call whose plan runs other
+// kernels (generic or cooperative scans, duration-dependent transitions, the
+// exact Viterbi kernel) builds cum in its workspace with the prologue first.
+// ---------------------------------------------------------------------------
+namespace {
+
+bool emit_fused_fwd(const Plan& pl, int semiring) {
+  return semiring == TSM_SEMIRING_LOG && pl.fast && !pl.dense && pl.T >= 1;
+}
+bool emit_fused_bwd(const Plan& pl, int semiring) {
+  return semiring == TSM_SEMIRING_LOG && pl.fast && !pl.dense && (pl.mfused || pl.mfast) && pl.T >= 1;
+}
+
+size_t prologue_bytes(const Plan& pl) {
+  size_t n = 0;
+  tsm_prologue_workspace(pl.B, pl.T, pl.C, &n);
+  return n;
+}
+
+// workspace of the built-cum path: cum (B, T+1, C) and the prologue's scratch
+size_t emit_cum_bytes(const Plan& pl) {
+  Carver cv(nullptr);
+  cv.take<float>((size_t)pl.B * (pl.T + 1) * pl.C);
+  cv.take<char>(prologue_bytes(pl));
+  return (cv.off + 255) & ~size_t(255);
+}
+
+// Builds cum from the scores at the start of the workspace; returns the rest.
+int emit_build_cum(const Plan& pl, const float* scores, void* ws, size_t ws_bytes, void* stream, float** cum,
+                   void** rest, size_t* rest_bytes, const char* what) {
+  const size_t head = emit_cum_bytes(pl);
+  if (!ws || ws_bytes < head) return fail(TSM_ERR_WORKSPACE, "%s: workspace too small: %zu < %zu bytes", what, ws_bytes, head);
+  Carver cv(ws);
+  *cum = cv.take<float>((size_t)pl.B * (pl.T + 1) * pl.C);
+  const size_t pb = prologue_bytes(pl);
+  void* pw = cv.take<char>(pb);
+  const int rc = run_prologue(scores, TSM_DTYPE_F32, nullptr, pl.B, pl.T, pl.C, 0, *cum, nullptr, pw, pb, stream, what);
+  if (rc) return rc;
+  *rest = static_cast<char*>(ws) + head;
+  *rest_bytes = ws_bytes - head;
+  return TSM_OK;
+}
+
+int emit_plan(const float* scores, int64_t B, int64_t T, int64_t C, int64_t K, int has_ps, int has_pe,
+              int64_t trans_rows, Plan* pl, const char* what) {
+  if (!scores) return fail(TSM_ERR_INVALID, "%s: scores are required", what);
+  if (T < 1) return fail(TSM_ERR_INVALID, "%s: scores need T >= 1 positions (got %lld)", what, (long long)T);
+  return make_plan(B, T, C, K, has_ps, has_pe, trans_rows, pl);
+}
+
+}  // namespace
+
+extern "C" {
+
+int tsm_forward_emissions_workspace(int64_t B, int64_t T, int64_t C, int64_t K, int64_t trans_rows, int semiring,
+                                    int has_ps, int has_pe, size_t* bytes) {
+  if (!bytes) return fail(TSM_ERR_INVALID, "bytes is NULL");
+  if (semiring != TSM_SEMIRING_LOG && semiring != TSM_SEMIRING_MAX) return fail(TSM_ERR_INVALID, "bad semiring %d", semiring);
+  if (T < 1) return fail(TSM_ERR_INVALID, "scores need T >= 1 positions (got %lld)", (long long)T);
+  Plan p;
+  const int rc = make_plan(B, T, C, K, has_ps, has_pe, trans_rows, &p);
+  if (rc) return rc;
+  *bytes = forward_ws_bytes(p, semiring) + (emit_fused_fwd(p, semiring) ? 0 : emit_cum_bytes(p));
+  return TSM_OK;
+}
+
+int tsm_forward_emissions(const float* scores, const float* tr, const float* db, const int64_t* len, const float* ps,
+                          const float* pe, int64_t B, int64_t T, int64_t C, int64_t K, int64_t trans_rows,
+                          int semiring, float* partition, double* log2_partition, float* alpha_hat,
+                          double* alpha_level, int32_t* recomputed, void* workspace, size_t ws_bytes, void* stream) {
+  Plan pl;
+  int rc = emit_plan(scores, B, T, C, K, ps != nullptr, pe != nullptr, trans_rows, &pl, "tsm_forward_emissions");
+  if (rc) return rc;
+  if (emit_fused_fwd(pl, semiring))
+    return forward_impl(nullptr, tr, db, len, ps, pe, B, T, C, K, trans_rows, semiring, partition, log2_partition,
+                        alpha_hat, alpha_level, recomputed, workspace, ws_bytes, stream, "tsm_forward_emissions",
+                        scores);
+  float* cum = nullptr;
+  void* rest = nullptr;
+  size_t rest_bytes = 0;
+  rc = emit_build_cum(pl, scores, workspace, ws_bytes, stream, &cum, &rest, &rest_bytes, "tsm_forward_emissions");
+  if (rc) return rc;
+  return forward_impl(cum, tr, db, len, ps, pe, B, T, C, K, trans_rows, semiring, partition, log2_partition,
+                      alpha_hat, alpha_level, recomputed, rest, rest_bytes, stream, "tsm_forward_emissions");
+}
+
+int tsm_backward_emissions_workspace(int64_t B, int64_t T, int64_t C, int64_t K, int64_t trans_rows, int semiring,
+                                     int has_ps, int has_pe, size_t* bytes) {
+  if (!bytes) return fail(TSM_ERR_INVALID, "bytes is NULL");
+  if (semiring != TSM_SEMIRING_LOG && semiring != TSM_SEMIRING_MAX) return fail(TSM_ERR_INVALID, "bad semiring %d", semiring);
+  if (T < 1) return fail(TSM_ERR_INVALID, "scores need T >= 1 positions (got %lld)", (long long)T);
+  Plan p;
+  const int rc = make_plan(B, T, C, K, has_ps, has_pe, trans_rows, &p);
+  if (rc) return rc;
+  const size_t tail = (backward_ws_bytes(p) + 255) & ~size_t(255);
+  if (emit_fused_bwd(p, semiring)) {
+    *bytes = tail + prologue_bytes(p);
+  } else {
+    // cum and its prologue scratch, the cum gradient, the backward's own workspace
+    *bytes = emit_cum_bytes(p) + (((size_t)p.B * (p.T + 1) * p.C * 4 + 255) & ~size_t(255)) + tail;
+  }
+  return TSM_OK;
+}
+
+int tsm_backward_emissions(const float* scores, const float* tr, const float* db, const int64_t* len,
+                           const float* ps, const float* pe, int64_t B, int64_t T, int64_t C, int64_t K,
+                           int64_t trans_rows, int semiring, const float* alpha_hat, const double* alpha_level,
+                           const double* log2_partition, const float* grad_output, float* grad_scores,
+                           float* grad_tr, float* grad_db, float* grad_ps, float* grad_pe, int32_t* recomputed,
+                           void* workspace, size_t ws_bytes, void* stream) {
+  Plan pl;
+  int rc = emit_plan(scores, B, T, C, K, ps != nullptr, pe != nullptr, trans_rows, &pl, "tsm_backward_emissions");
+  if (rc) return rc;
+  if (!grad_scores) return fail(TSM_ERR_INVALID, "tsm_backward_emissions: grad_scores is required");
+  size_t need = 0;
+  rc = tsm_backward_emissions_workspace(B, T, C, K, trans_rows, semiring, ps != nullptr, pe != nullptr, &need);
+  if (rc) return rc;
+  if (!workspace || ws_bytes < need)
+    return fail(TSM_ERR_WORKSPACE, "tsm_backward_emissions: workspace too small: %zu < %zu bytes", ws_bytes, need);
+  if (emit_fused_bwd(pl, semiring)) {
+    // the kernels read the scores; the finalize leaves row t >= 1 of the cum gradient
+    // at row t-1 of grad_scores, and the suffix sums run in place there
+    const size_t tail = (backward_ws_bytes(pl) + 255) & ~size_t(255);
+    rc = backward_impl(nullptr, scores, tr, db, len, ps, pe, B, T, C, K, trans_rows, semiring, alpha_hat,
+                       alpha_level, log2_partition, grad_output, grad_scores, grad_tr, grad_db, grad_ps, grad_pe,
+                       recomputed, workspace, tail, stream);
+    if (rc) return rc;
+    return run_prologue(nullptr, TSM_DTYPE_F32, grad_scores, B, T, C, 0, nullptr, grad_scores,
+                        static_cast<char*>(workspace) + tail, ws_bytes - tail, stream,
+                        "tsm_backward_emissions (score gradient)");
+  }
+  float* cum = nullptr;
+  void* rest = nullptr;
+  size_t rest_bytes = 0;
+  rc = emit_build_cum(pl, scores, workspace, ws_bytes, stream, &cum, &rest, &rest_bytes, "tsm_backward_emissions");
+  if (rc) return rc;
+  const size_t gbytes = ((size_t)pl.B * (pl.T + 1) * pl.C * 4 + 255) & ~size_t(255);
+  float* gcum = static_cast<float*>(rest);
+  rc = backward_impl(cum, nullptr, tr, db, len, ps, pe, B, T, C, K, trans_rows, semiring, alpha_hat, alpha_level,
+                     log2_partition, grad_output, gcum, grad_tr, grad_db, grad_ps, grad_pe, recomputed,
+                     static_cast<char*>(rest) + gbytes, rest_bytes - gbytes, stream);
+  if (rc) return rc;
+  // the prologue's scratch (in the cum head of the workspace) is free again
+  Carver cv(workspace);
+  cv.take<float>((size_t)pl.B * (pl.T + 1) * pl.C);
+  void* pw = cv.take<char>(prologue_bytes(pl));
+  return run_prologue(nullptr, TSM_DTYPE_F32, gcum, B, T, C, 0, nullptr, grad_scores, pw, prologue_bytes(pl), stream,
+                      "tsm_backward_emissions (score gradient)");
+}
+
+int tsm_viterbi_emissions_workspace(int64_t B, int64_t T, int64_t C, int64_t K, int64_t trans_rows, int with_tb,
+                                    int algorithm, size_t* bytes) {
+  if (!bytes) return fail(TSM_ERR_INVALID, "bytes is NULL");
+  if (T < 1) return fail(TSM_ERR_INVALID, "scores need T >= 1 positions (got %lld)", (long long)T);
+  Plan p;
+  const int rc = make_plan(B, T, C, K, 0, 0, trans_rows, &p);
+  if (rc) return rc;
+  *bytes = viterbi_ws_bytes(p, with_tb) + (viterbi_factorised(p, algorithm) ? 0 : emit_cum_bytes(p));
+  return TSM_OK;
+}
+
+int tsm_viterbi_emissions(const float* scores, const float* tr, const float* db, const int64_t* len,
+                          const float* ps, const float* pe, int64_t B, int64_t T, int64_t C, int64_t K,
+                          int64_t trans_rows, float* score, int with_tb, int algorithm, int32_t* seg_count,
+                          int32_t* segments, void* workspace, size_t ws_bytes, void* stream) {
+  Plan pl;
+  int rc = emit_plan(scores, B, T, C, K, ps != nullptr, pe != nullptr, trans_rows, &pl, "tsm_viterbi_emissions");
+  if (rc) return rc;
+  if (algorithm < TSM_VITERBI_AUTO || algorithm > TSM_VITERBI_FACTORISED)
+    return fail(TSM_ERR_INVALID, "algorithm must be TSM_VITERBI_AUTO (0), _EXACT (1) or _FACTORISED (2), got %d",
+                algorithm);
+  if (viterbi_factorised(pl, algorithm))
+    return viterbi_impl(nullptr, scores, tr, db, len, ps, pe, B, T, C, K, trans_rows, score, with_tb, algorithm,
+                        seg_count, segments, workspace, ws_bytes, stream);
+  float* cum = nullptr;
+  void* rest = nullptr;
+  size_t rest_bytes = 0;
+  rc = emit_build_cum(pl, scores, workspace, ws_bytes, stream, &cum, &rest, &rest_bytes, "tsm_viterbi_emissions");
+  if (rc) return rc;
+  return viterbi_impl(cum, nullptr, tr, db, len, ps, pe, B, T, C, K, trans_rows, score, with_tb, algorithm,
+                      seg_count, segments, rest, rest_bytes, stream);
+}
+
+int tsm_gold_score_emissions(const float* scores, const float* tr, const float* db, const int64_t* labels,
+                             const int64_t* len, int64_t B, int64_t T, int64_t C, int64_t K, int64_t db_rows,
+                             float* score, void* workspace, size_t ws_bytes, void* stream) {
+  if (!scores || !tr || !db || !labels || !len || !score)
+    return fail(TSM_ERR_INVALID, "scores, transition, duration_bias, labels, lengths and score are required");
+  int rc = check_gold(B, T, C, K, db_rows);
+  if (rc) return rc;
+  size_t need = 0;
+  tsm_gold_score_workspace(B, T, C, K, db_rows, &need);
+  if (!workspace || ws_bytes < need)
+    return fail(TSM_ERR_WORKSPACE, "gold score workspace too small: %zu < %zu bytes", ws_bytes, need);
+  Carver cv(workspace);
+  const GoldWs w = carve_gold(cv, B, T, C, db_rows);
+  tsm::GoldParams g = gold_params(w, nullptr, tr, db, labels, len, B, T, C, K, db_rows);
+  g.emit = scores;
+  g.score = score;
+  const int e = tsm::launch_gold_score(g, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "tsm_gold_score_emissions");
+  return TSM_OK;
+}
+
+int tsm_gold_score_emissions_backward(const int64_t* labels, const int64_t* len, int64_t B, int64_t T, int64_t C,
+                                      int64_t K, int64_t db_rows, const float* grad_output, float* grad_scores,
+                                      float* grad_tr, float* grad_db, void* workspace, size_t ws_bytes,
+                                      void* stream) {
+  if (!labels || !len || !grad_output || !grad_scores || !grad_tr || !grad_db)
+    return fail(TSM_ERR_INVALID, "labels, lengths, grad_output and the gradient outputs are required");
+  int rc = check_gold(B, T, C, K, db_rows);
+  if (rc) return rc;
+  size_t need = 0;
+  tsm_gold_score_workspace(B, T, C, K, db_rows, &need);
+  if (!workspace || ws_bytes < need)
+    return fail(TSM_ERR_WORKSPACE, "gold score workspace too small: %zu < %zu bytes", ws_bytes, need);
+  Carver cv(workspace);
+  const GoldWs w = carve_gold(cv, B, T, C, db_rows);
+  tsm::GoldParams g = gold_params(w, nullptr, nullptr, nullptr, labels, len, B, T, C, K, db_rows);
+  g.gout = grad_output;
+  g.gcum = grad_scores;
+  g.emit_grad = 1;
+  g.gtr = grad_tr;
+  g.gdb = grad_db;
+  const int e = tsm::launch_gold_backward(g, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "tsm_gold_score_emissions_backward");
   return TSM_OK;
 }
 

@@ -27,6 +27,15 @@
 //
 // sgn = +1 forward (content cum[t]-cum[t-k]), -1 backward (cum[t+k]-cum[t]).
 //
+// Emission input (EMIT, for p.emit != null): the chunk reads the projected scores
+// (B, T, C) instead of cumulative scores and carries cum itself, in fp64, in a
+// frame of its own: cum = 0 at its first position t_start, a running sum of
+// the score rows stepped over after it, and prefix sums over the score rows
+// behind a position for the ring entries there (behind_em).  The recursion
+// only uses differences of cum along one label, so the frame drops out of every
+// output; the emission prologue is fused into the scan's streamed loads and no
+// (B, T+1, C) cumulative tensor is built.
+//
 // MARG (backward, log semiring, 16-lane groups): the beta scan also produces the
 // segment marginals of the starts it owns.  The pull's term r of label c at
 // step t is 2^(x[t+k] + db[k] - y0); times F = 2^(y0 + A[t,c]), with A the
@@ -58,7 +67,7 @@ __device__ __forceinline__ void lds_barrier() { __asm__ volatile("s_waitcnt lgkm
 // of the same words by other lanes (LDS executes a wave's operations in order).
 __device__ __forceinline__ void wave_lds_order() { __asm__ volatile("" ::: "memory"); }
 
-template <int J, int R, bool FWD, bool LOGSR, bool MARG = false, int CJ = 4>
+template <int J, int R, bool FWD, bool LOGSR, bool MARG = false, int CJ = 4, bool EMIT = false>
 struct Chunk {
   static_assert(!MARG || (!FWD && LOGSR && J == 16), "fused marginals: backward log scan, 16-lane DPP rows");
   static constexpr int kCJ = CJ;
@@ -67,6 +76,31 @@ struct Chunk {
   static constexpr int kMaxThreads = R > 16 ? 512 : 1024;
   __device__ static double* red(char* smem, const ScanParams& p) {
     return reinterpret_cast<double*>(smem + fast_lds_layout(p.C, p.RL, p.RS).red);
+  }
+  // Emission input: sgn * cum * log2(e), in the chunk's frame, of the position i
+  // behind `base` (FWD: base - i, BWD: base + i), for i = i0 + lj of one block of
+  // J consecutive i.  `carry` holds the value of position i0 - 1 (of base itself
+  // when i0 == 0, where lane 0 adds nothing) and advances to i0 + J - 1.
+  // Stepping back over a position lowers the value by that position's score row
+  // times log2(e) in both directions.  Rows outside [0, T) are clamped: the
+  // positions they lead to lie outside the sequence and are never used.  Every
+  // lane of the J-lane group takes part (shuffles within the group).
+  __device__ static double behind_em(const float* em_b, int C, int c, int T, int lj, int base, int i,
+                                     double& carry) {
+    double d = 0.0;
+    if (i >= 1) {
+      int row = FWD ? base - i : base + i - 1;
+      row = row < 0 ? 0 : (row > T - 1 ? T - 1 : row);
+      d = (double)em_b[(size_t)row * C + c];
+    }
+#pragma unroll
+    for (int o = 1; o < J; o <<= 1) {
+      const double v = __shfl_up(d, o, J);
+      if (lj >= o) d += v;
+    }
+    const double val = carry - d * kLog2eD;
+    carry = __shfl(val, J - 1, J);
+    return val;
   }
   // ---------------------------------------------------------------------------
   // One chunk of one sequence.
@@ -89,7 +123,9 @@ struct Chunk {
     const int g = tid / J, lj = tid % J;
     const bool cval = g < C;
     const int c = cval ? g : C - 1;  // padding groups shadow the last label and never write
-    const float* cum_b = p.cum + (size_t)b * (T + 1) * C;
+    constexpr bool emit = EMIT;
+    const float* cum_b = emit ? nullptr : p.cum + (size_t)b * (T + 1) * C;
+    const float* em_b = emit ? p.emit + (size_t)b * T * C : nullptr;
     const bool has_ps = p.ps != nullptr, has_pe = p.pe != nullptr;
     const float* ps_b = has_ps ? p.ps + (size_t)b * T * C : nullptr;
     const float* pe_b = has_pe ? p.pe + (size_t)b * T * C : nullptr;
@@ -248,14 +284,22 @@ struct Chunk {
         if (cval && lj == 0 && store) p.val[((size_t)b * (T + 1) + len) * C + c] = 0.0f;
         if (tid == 0 && store) p.lvl[(size_t)b * (T + 1) + len] = 0.0;
       }
-      if (cval && lj == 0) rc[A0] = (double)v0 - cumx(pos);
+      if (cval && lj == 0) rc[A0] = (double)v0 - (emit ? 0.0 : cumx(pos));
       if (tid == 0) lring[pos % RS] = 0.0;
     } else {
       lvl_prev = (mode == 1) ? 0.0 : init_lv[0];
       // positions t_start -/+ i, i < Kmax
       if (cval) {
-        for (int i = lj; i < Kmax; i += J) {
+        double carry = 0.0;  // emission input: the chunk's frame has cum = 0 at t_start
+        for (int i0 = EMIT ? 0 : lj; i0 < Kmax; i0 += J) {
+          const int i = EMIT ? i0 + lj : i0;
+          double cxp = 0.0;
+          if constexpr (EMIT) {
+            cxp = behind_em(em_b, C, c, T, lj, t_start, i, carry);
+            if (i >= Kmax) continue;
+          }
           const int pos = FWD ? t_start - i : t_start + i;
+          if constexpr (!EMIT) cxp = cumx(pos);
           float v;
           if (mode == 1) {
             if (FWD) v = has_ps ? ps_b[(size_t)pos * C + c] * kLog2e : 0.0f;
@@ -264,7 +308,7 @@ struct Chunk {
             v = init_st[(size_t)i * C + c];
           }
           const double lv = (mode == 1) ? 0.0 : init_lv[i];
-          rc[A0 + i] = lv + (double)v - cumx(pos);
+          rc[A0 + i] = lv + (double)v - cxp;
         }
       }
       for (int i = tid; i < Kmax; i += NT) {
@@ -283,13 +327,25 @@ struct Chunk {
     // projection operands: forward adds proj_end[t-1] to the pull and proj_start[t]
     // to the ring entry; backward adds proj_start[t] to the pull and proj_end[t-1]
     // to the ring entry.  Absent projections read cum and are scaled by 0.
-    const float* pa_src = FWD ? (has_pe ? pe_b : cum_b) : (has_ps ? ps_b : cum_b);
-    const float* pb_src = FWD ? (has_ps ? ps_b : cum_b) : (has_pe ? pe_b : cum_b);
+    // per step: cum[t] (cum input) or the score row stepped over, t-1 forward and t
+    // backward (emission input), whose running sum is the chunk-frame cum
+    const float* xs_b = emit ? em_b : cum_b;
+    auto xs_row = [&](int t) { return emit ? clampT1(FWD ? t - 1 : t) : clampT(t); };
+    const float* pa_src = FWD ? (has_pe ? pe_b : xs_b) : (has_ps ? ps_b : xs_b);
+    const float* pb_src = FWD ? (has_ps ? ps_b : xs_b) : (has_pe ? pe_b : xs_b);
     const float pa_scale = (FWD ? has_pe : has_ps) ? kLog2e : 0.0f;
     const float pb_scale = (FWD ? has_ps : has_pe) ? kLog2e : 0.0f;
     auto pa_row = [&](int t) { return FWD ? clampT1(t - 1) : clampT1(t); };
     auto pb_row = [&](int t) { return FWD ? clampT1(t) : clampT1(t - 1); };
-    float cum_n = cum_b[(size_t)clampT(t_first) * C + c];
+    float cum_n = xs_b[(size_t)xs_row(t_first) * C + c];
+    // emission input: the running sgn * cum * log2(e) of the previous position sits in
+    // LDS (one word per label, written by the group's lane 0 at the end of each step),
+    // so it holds no register across steps
+    [[maybe_unused]] double* cxs = reinterpret_cast<double*>(smem + L.cx);
+    if constexpr (EMIT) {
+      if (cval && lj == 0) cxs[c] = 0.0;
+      wave_lds_order();
+    }
     float pa_n = pa_src[(size_t)pa_row(t_first) * C + c];
     float pb_n = pb_src[(size_t)pb_row(t_first) * C + c];
     [[maybe_unused]] float u_n = 0.0f;
@@ -314,11 +370,19 @@ struct Chunk {
           const size_t row0 = (size_t)bo * (T + 1);
           double m = -1e300;
           if (cval) {
-            for (int i = lj; i < Kmax; i += J) {
+            double carry = 0.0;
+            if constexpr (EMIT) carry = cxs[c];  // position t_hi (the previous step, or t_start)
+            for (int i0 = EMIT ? 0 : lj; i0 < Kmax; i0 += J) {
+              const int i = EMIT ? i0 + lj : i0;
               const int pos = t_hi + i;
+              double cxv = 0.0;
+              if constexpr (EMIT) {
+                cxv = behind_em(em_b, C, c, T, lj, t_hi, i, carry);
+                if (i >= Kmax) continue;
+              }
               if (pos <= len) {
                 const double pbv = (has_pe && pos >= 1) ? (double)(p.pe[((size_t)bo * T + pos - 1) * C + c] * kLog2e) : 0.0;
-                const double cxv = -(double)p.cum[(row0 + pos) * C + c] * kLog2eD;
+                if constexpr (!EMIT) cxv = -(double)p.cum[(row0 + pos) * C + c] * kLog2eD;
                 const double lb = (rc[A + i] - pbv) + cxv;  // log2 beta(pos, c), chunk frame
                 const double la = (double)p.aval[(row0 + pos) * C + c] + p.alvl[row0 + pos];
                 m = fmax(m, la + lb);
@@ -344,7 +408,9 @@ struct Chunk {
         }
         A = A0 - 1;
       }
-      const double cx_t = sgn * (double)cum_n * kLog2eD;
+      double cx_t;
+      if constexpr (EMIT) cx_t = cxs[c] + (double)cum_n * kLog2eD;
+      else cx_t = sgn * (double)cum_n * kLog2eD;
       const float pa_t = pa_n * ((FWD ? t >= 1 : true) ? pa_scale : 0.0f);
       const float pb_t = pb_n * ((FWD ? true : t >= 1) ? pb_scale : 0.0f);
       [[maybe_unused]] const float u_t = u_n;
@@ -355,7 +421,7 @@ struct Chunk {
           u_n = u_b[(size_t)clampT(tn) * C + c];
           la_n = al_b[clampT(tn)];
         }
-        cum_n = cum_b[(size_t)clampT(tn) * C + c];
+        cum_n = xs_b[(size_t)xs_row(tn) * C + c];
         pa_n = pa_src[(size_t)pa_row(tn) * C + c];
         pb_n = pb_src[(size_t)pb_row(tn) * C + c];
       }
@@ -412,6 +478,7 @@ struct Chunk {
         // the lane's terms relative to the previous position's level
         const double yrel = (y0 + cx_t) - lvl_prev;
         [[maybe_unused]] double lam = 0.0;
+        [[maybe_unused]] float sp = 0.0f;  // emission input: the lane's sum of P (start sum)
         if constexpr (MARG) {
           if (t < t_hi) {
             // P(t,k,c) = term * 2^(y0 + A[t,c]) in the chunk frame
@@ -439,6 +506,7 @@ struct Chunk {
             for (int r = R - 1; r >= 0; --r) {
               const float P = tm[r] * F;
               d32[r] += P;
+              if constexpr (EMIT) sp += P;
               const float prv = (r >= 1) ? ea[r - 1] : 0.0f;
               // a bitwise merge: a select would become a register-array read at a lane-dependent index
               const float sl = __int_as_float((__float_as_int(prv) & lane_last) | (__float_as_int(ea[r]) & ~lane_last));
@@ -450,8 +518,17 @@ struct Chunk {
         a2 = group_lse2<J>((float)yrel, s) + pa_t;
         if constexpr (MARG) {
           if (t < t_hi) {
-            // start sum: sum_k P = 2^(lvl_prev + a2 + alpha level + u - zd)
-            if (cval && lj == 0) s_out_b[(size_t)t * C + c] = exp2_hw((float)(lam + (double)a2) + u_t);
+            // start sum: sum_k P = 2^(lvl_prev + a2 + alpha level + u - zd).  Emission
+            // input: the sum of the same P terms the end sums take, so that the score
+            // gradient, a running sum of E - S over all positions, carries no
+            // relative bias between the two (the exp2 / log2 of the log-sum would
+            // leave one of ~1e-7, which the running sum accumulates)
+            if constexpr (EMIT) {
+              const float St = group_sum<J>(sp);
+              if (cval && lj == 0) s_out_b[(size_t)t * C + c] = St;
+            } else {
+              if (cval && lj == 0) s_out_b[(size_t)t * C + c] = exp2_hw((float)(lam + (double)a2) + u_t);
+            }
             if (((t_hi - 1 - t) & 127) == 127) fold_d();
           }
         }
@@ -547,7 +624,10 @@ struct Chunk {
         if (tid == 0 && store && owned) p.lvl[(size_t)b * (T + 1) + t] = lvl_t;
       }
       // ---- ring entry for position t ----
-      if (cval && lj == 0) rc[A] = (lvl_t + (double)(mixv + pb_t)) - cx_t;
+      if (cval && lj == 0) {
+        rc[A] = (lvl_t + (double)(mixv + pb_t)) - cx_t;
+        if constexpr (EMIT) cxs[c] = cx_t;
+      }
       if (tid == 0) lring[t % RS] = lvl_t;
       lvl_prev = lvl_t;
       wave_lds_order();
@@ -557,12 +637,19 @@ struct Chunk {
         float* st = (t == rec_spec ? p.st_spec : p.st_end) + (size_t)item * Kmax * C;
         double* lv = (t == rec_spec ? p.lv_spec : p.lv_end) + (size_t)item * Kmax;
         if (cval) {
-          for (int i = lj; i < Kmax; i += J) {
+          double carry = cx_t;  // emission input
+          for (int i0 = EMIT ? 0 : lj; i0 < Kmax; i0 += J) {
+            const int i = EMIT ? i0 + lj : i0;
+            [[maybe_unused]] double cxe = 0.0;
+            if constexpr (EMIT) {
+              cxe = behind_em(em_b, C, c, T, lj, t, i, carry);
+              if (i >= Kmax) continue;
+            }
             const int pos = FWD ? t - i : t + i;
             const double x = rc[A + i];
             const double lp = (i == 0) ? lvl_t : lring[pos % RS];
             // positions outside the sequence keep the "does not exist" marker
-            st[(size_t)i * C + c] = (x < -1e29) ? -1e30f : (float)((x - lp) + cumx(pos));
+            st[(size_t)i * C + c] = (x < -1e29) ? -1e30f : (float)((x - lp) + (EMIT ? cxe : cumx(pos)));
           }
         }
         for (int i = tid; i < Kmax; i += NT) {
@@ -594,27 +681,34 @@ struct Chunk {
 template <int J>
 inline bool narrow_mix(const ScanParams& p) { return p.C <= 2 * J; }
 
+// The instance of one (direction, semiring, fusion): label-mix width from C,
+// emission input from p.emit (each its own compiled kernel, so the cumulative-
+// score instances carry none of the emission code's registers).
+template <int J, int R, bool FWD, bool LOGSR, bool MARG>
+int launch_chunk_any(const Plan& pl, const ScanParams& p, hipStream_t st) {
+  const bool em = p.emit != nullptr;
+  if (narrow_mix<J>(p))
+    return em ? launch_chunk_dir<Chunk<J, R, FWD, LOGSR, MARG, 2, true>>(pl, p, pl.fast_lds, pl.FNT, st)
+              : launch_chunk_dir<Chunk<J, R, FWD, LOGSR, MARG, 2, false>>(pl, p, pl.fast_lds, pl.FNT, st);
+  return em ? launch_chunk_dir<Chunk<J, R, FWD, LOGSR, MARG, 4, true>>(pl, p, pl.fast_lds, pl.FNT, st)
+            : launch_chunk_dir<Chunk<J, R, FWD, LOGSR, MARG, 4, false>>(pl, p, pl.fast_lds, pl.FNT, st);
+}
+
 template <int J, int R>
 int launch_fast_jr(const Plan& pl, const ScanParams& p, bool fwd, hipStream_t st) {
-  if (narrow_mix<J>(p))
-    return fwd ? launch_chunk_dir<Chunk<J, R, true, true, false, 2>>(pl, p, pl.fast_lds, pl.FNT, st)
-               : launch_chunk_dir<Chunk<J, R, false, true, false, 2>>(pl, p, pl.fast_lds, pl.FNT, st);
-  return fwd ? launch_chunk_dir<Chunk<J, R, true, true, false, 4>>(pl, p, pl.fast_lds, pl.FNT, st)
-             : launch_chunk_dir<Chunk<J, R, false, true, false, 4>>(pl, p, pl.fast_lds, pl.FNT, st);
+  return fwd ? launch_chunk_any<J, R, true, true, false>(pl, p, st) : launch_chunk_any<J, R, false, true, false>(pl, p, st);
 }
 
 // Backward log scan with the segment marginals fused (16-lane groups).
 template <int R>
 int launch_fused_r(const Plan& pl, const ScanParams& p, hipStream_t st) {
-  if (narrow_mix<16>(p)) return launch_chunk_dir<Chunk<16, R, false, true, true, 2>>(pl, p, pl.fast_lds, pl.FNT, st);
-  return launch_chunk_dir<Chunk<16, R, false, true, true, 4>>(pl, p, pl.fast_lds, pl.FNT, st);
+  return launch_chunk_any<16, R, false, true, true>(pl, p, st);
 }
 
 // Max-semiring forward with backpointers (factorised Viterbi).
 template <int J, int R>
 int launch_fast_max_jr(const Plan& pl, const ScanParams& p, hipStream_t st) {
-  if (narrow_mix<J>(p)) return launch_chunk_dir<Chunk<J, R, true, false, false, 2>>(pl, p, pl.fast_lds, pl.FNT, st);
-  return launch_chunk_dir<Chunk<J, R, true, false, false, 4>>(pl, p, pl.fast_lds, pl.FNT, st);
+  return launch_chunk_any<J, R, true, false, false>(pl, p, st);
 }
 
 }  // namespace fastscan

@@ -199,13 +199,26 @@ __global__ void __launch_bounds__(1024) coverage_kernel(FusedParams f) {
     const int s0 = max(0, t_ref - Kmax + 1);
     const size_t item = (size_t)b * f.P + j;
     const float* st = f.st_end + item * Kmax * C;
-    const float* cum_b = f.cum + (size_t)b * (T + 1) * C;
-    const float* cref = cum_b + (size_t)t_ref * C;
+    const bool emit = f.emit != nullptr;
+    const float* cum_b = emit ? nullptr : f.cum + (size_t)b * (T + 1) * C;
+    const float* em_b = emit ? f.emit + (size_t)b * T * C : nullptr;
+    const float* cref = emit ? nullptr : cum_b + (size_t)t_ref * C;
     const int ni = min(Kmax, len - t_lo + 1);  // positions t_lo .. min(len, t_lo+Kmax-1)
     for (int i = threadIdx.x; i < ni; i += blockDim.x) lvs[i] = f.lv_end[item * Kmax + i];
-    for (int idx = threadIdx.x; idx < ni * C; idx += blockDim.x) {
-      const int i = idx / C, c = idx % C;
-      ew[idx] = st[idx] + (cum_b[(size_t)(t_lo + i) * C + c] - cref[c]) * kLog2e;
+    if (emit) {
+      // cum[t_lo+i] - cum[t_ref]: running sums of score rows t_ref .. t_lo+i-1, one thread per label
+      for (int c = threadIdx.x; c < C; c += blockDim.x) {
+        double run = 0.0;
+        for (int i = 0; i < ni; ++i) {
+          run += (double)em_b[(size_t)(t_ref + i) * C + c];
+          ew[i * C + c] = st[i * C + c] + (float)(run * kLog2eD);
+        }
+      }
+    } else {
+      for (int idx = threadIdx.x; idx < ni * C; idx += blockDim.x) {
+        const int i = idx / C, c = idx % C;
+        ew[idx] = st[idx] + (cum_b[(size_t)(t_lo + i) * C + c] - cref[c]) * kLog2e;
+      }
     }
     if constexpr (DBL) {
       for (int idx = threadIdx.x; idx < Kmax * C; idx += blockDim.x) {
@@ -219,7 +232,15 @@ __global__ void __launch_bounds__(1024) coverage_kernel(FusedParams f) {
     for (int w = threadIdx.x; w < n; w += blockDim.x) {
       const int s = s0 + w / C, c = w % C;
       const double al = f.alvl[(size_t)b * (T + 1) + s] + base;
-      float a = f.uval[((size_t)b * (T + 1) + s) * C + c] - (cum_b[(size_t)s * C + c] - cref[c]) * kLog2e;
+      float a = f.uval[((size_t)b * (T + 1) + s) * C + c];
+      if (emit) {
+        // cum[t_ref] - cum[s]: score rows s .. t_ref-1
+        double d = 0.0;
+        for (int u = s; u < t_ref; ++u) d += (double)em_b[(size_t)u * C + c];
+        a += (float)(d * kLog2eD);
+      } else {
+        a -= (cum_b[(size_t)s * C + c] - cref[c]) * kLog2e;
+      }
       if (f.ps != nullptr) a += f.ps[((size_t)b * T + s) * C + c] * kLog2e;
       const int k0 = t_ref - s + 1, k1 = min(Kmax, len - s);
       float sk0 = 0.0f, sk1 = 0.0f;
@@ -278,7 +299,8 @@ __global__ void fused_rows_kernel(FusedParams f) {
       }
       if (t < len) S = (float)(fj * (double)f.s_out[o]);
     }
-    f.grad_cum[o] = g * (E - S);
+    if (!f.shift) f.grad_cum[o] = g * (E - S);
+    else if (t >= 1) f.grad_cum[((size_t)b * T + t - 1) * C + c] = g * (E - S);
     if (f.grad_ps != nullptr && t < T) f.grad_ps[((size_t)b * T + t) * C + c] = g * S;
     if (f.grad_pe != nullptr && t >= 1) f.grad_pe[((size_t)b * T + t - 1) * C + c] = g * E;
   }

@@ -80,7 +80,8 @@ __global__ void __launch_bounds__(kGoldNT) gold_partial_kernel(GoldParams g) {
   const int p0 = chunk * kGoldTB;
   const int H = g.H;
   const int* lp = stage_labels(g, b, p0, len, H, lab);
-  const float* cum_b = g.cum + (size_t)b * (T + 1) * C;
+  const float* em_b = g.emit != nullptr ? g.emit + (size_t)b * T * C : nullptr;
+  const float* cum_b = em_b != nullptr ? nullptr : g.cum + (size_t)b * (T + 1) * C;
   const int cap = g.K - 1;
   double acc = 0.0;
   int bad = 0;
@@ -94,8 +95,10 @@ __global__ void __launch_bounds__(kGoldNT) gold_partial_kernel(GoldParams g) {
     }
     const int cprev = (p > 0) ? lp[i - 1] : -1;
     const int cnext = (p + 1 < len) ? lp[i + 1] : -1;
+    // emission input: a segment's content is the sum of its positions' scores
+    if (em_b != nullptr) acc += (double)em_b[(size_t)p * C + c];
     if (p == 0 || cprev != c) {
-      acc -= (double)cum_b[(size_t)p * C + c];
+      if (em_b == nullptr) acc -= (double)cum_b[(size_t)p * C + c];
       if (p > 0) {
         if (cprev < 0 || cprev >= C) bad = 1;
         else acc += (double)g.tr[(size_t)cprev * C + c];
@@ -103,7 +106,8 @@ __global__ void __launch_bounds__(kGoldNT) gold_partial_kernel(GoldParams g) {
     }
     if (p == len - 1 || cnext != c) {
       const int dur = (g.T > 1 && cap > 1) ? run_length(lp + i, p, c, cap) : 1;
-      acc += (double)cum_b[(size_t)(p + 1) * C + c] + (double)g.db[(size_t)gold_row(dur, g) * C + c];
+      if (em_b == nullptr) acc += (double)cum_b[(size_t)(p + 1) * C + c];
+      acc += (double)g.db[(size_t)gold_row(dur, g) * C + c];
     }
   }
   // block reduction (fp64 sum, flag or)
@@ -146,6 +150,18 @@ __global__ void gold_finish_kernel(GoldParams g) {
 __global__ void gold_grad_cum_kernel(GoldParams g) {
   const int C = g.C, T = g.T;
   const size_t n = (size_t)g.B * (T + 1) * C;
+  if (g.emit_grad) {
+    // emission input: d gold / d scores[b, p, c] = [p < len and labels[b, p] == c]
+    const size_t m = (size_t)g.B * T * C;
+    for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < m; idx += (size_t)gridDim.x * blockDim.x) {
+      const int c = (int)(idx % C);
+      const int p = (int)((idx / C) % T);
+      const int b = (int)(idx / ((size_t)C * T));
+      const bool on = p < glen(g.lengths, b, T) && g.labels[(size_t)b * T + p] == c;
+      g.gcum[idx] = on ? g.gout[b] : 0.0f;
+    }
+    return;
+  }
   for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < n; idx += (size_t)gridDim.x * blockDim.x) {
     const int c = (int)(idx % C);
     const int p = (int)((idx / C) % (T + 1));

@@ -14,6 +14,7 @@ enum Semiring : int { kLog = 0, kMax = 1 };
 struct ScanParams {
   // problem
   const float* cum;        // (B, T+1, C)
+  const float* emit;       // (B, T, C) projected scores in place of cum (register-resident scans), or null
   const float* trans;      // (C, C)  transition[c_src][c_dst], natural log units
   const float* db;         // (K, C)  duration bias
   const int64_t* lengths;  // (B,)
@@ -75,6 +76,7 @@ struct ScanParams {
 
 struct MargParams {
   const float* cum;
+  const float* emit;       // (B, T, C) projected scores in place of cum, or null
   const float* trans;
   const float* db;
   const int64_t* lengths;
@@ -114,6 +116,7 @@ struct FinalParams {
   float* grad_db;            // (K, C)
   int trows;                 // grad_tr is (trows, C, C) when > 0
   const double* bscale;      // (B, NB) block scales of the coverage pass, or null (1)
+  int shift;                 // 1: grad_cum is (B, T, C) and row t >= 1 goes to row t-1 (row 0 is dropped)
 };
 
 // Row passes of the backward with fused marginals (tsm_fused.hip).
@@ -135,6 +138,7 @@ struct FusedParams {
   // coverage pass: inputs, the forward's levels and log2 Z, the backward chunks'
   // recorded beta states (positions t_lo .. t_lo+Kmax-1 of chunk j >= 1)
   const float* cum;        // (B, T+1, C)
+  const float* emit;       // (B, T, C) projected scores in place of cum, or null
   const float* db;         // (K, C)
   const float* ps;         // (B, T, C) or null
   const double* alvl;      // (B, T+1)
@@ -147,6 +151,7 @@ struct FusedParams {
   float* grad_pe;
   float* grad_tr;
   float* grad_db;
+  int shift;               // 1: grad_cum is (B, T, C) and row t >= 1 goes to row t-1 (row 0 is dropped)
 };
 
 struct ViterbiParams {
@@ -166,6 +171,8 @@ struct ViterbiParams {
 // Gold-path score (segmentation implied by per-position labels) and its gradients.
 struct GoldParams {
   const float* cum;        // (B, T+1, C)
+  const float* emit;       // (B, T, C) projected scores in place of cum, or null
+  int emit_grad;           // backward: gcum is the (B, T, C) gradient of the projected scores
   const float* tr;         // (C, C)
   const float* db;         // (Kdb, C)
   const int64_t* labels;   // (B, T)
@@ -189,7 +196,8 @@ struct GoldParams {
 struct PrologueParams {
   const void* x;     // (B, T, C) scores, dtype TSM_DTYPE_*
   int dtype;
-  const float* g;    // backward: (B, T+1, C) gradient of cum
+  const float* g;    // backward: gradient of cum, row u of sequence b at g[(b*GR + u + goff)*C]
+  int GR, goff;      // (T+1, 0) for a (B, T+1, C) tensor; (T, -1) for row u kept at u-1 of a (B, T, C) one
   float* cum;        // (B, T+1, C)
   float* gx;         // backward: (B, T, C)
   double* part;      // (B, NBL, C) block sums, then carries

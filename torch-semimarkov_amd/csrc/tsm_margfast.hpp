@@ -32,6 +32,12 @@
 // Outputs follow the blocked layout of the generic marginal kernel (e_own /
 // halo / s_out rows, fp64 per-block partials), so the same finalize kernels
 // produce the gradients.
+// Emission input (q.emit != null): the kernel reads the projected scores
+// (B, T, C) and builds cum itself in fp64, in the block's own frame (cum = 0
+// at t0): each batch of J positions of the x stream and of the step stream is
+// one 16-lane prefix sum of its score rows plus the stream's running total
+// (kept in LDS).  Only differences of cum along one label enter P, so the
+// frame drops out.
 #pragma once
 
 #include "tsm_device.hpp"
@@ -111,7 +117,15 @@ __global__ void __launch_bounds__(64) margfast_kernel(MargParams q) {
   }
   __threadfence();  // the zeros before the first atomic add
   const bool has_ps = q.ps != nullptr, has_pe = q.pe != nullptr;
-  const float* cum_b = q.cum + (size_t)b * (T + 1) * C;
+  const bool emit = q.emit != nullptr;
+  const float* cum_b = emit ? nullptr : q.cum + (size_t)b * (T + 1) * C;
+  const float* em_b = emit ? q.emit + (size_t)b * T * C : nullptr;
+  // per position e: cum[e] (cum input) or the score row e-1 stepped over to reach e
+  auto xs_at = [&](int e) -> float {
+    if (!emit) return cum_b[(size_t)e * C + c];
+    const int r = e - 1 < 0 ? 0 : (e - 1 > T - 1 ? T - 1 : e - 1);
+    return em_b[(size_t)r * C + c];
+  };
   const float* ps_b = has_ps ? q.ps + (size_t)b * T * C : nullptr;
   const float* pe_b = has_pe ? q.pe + (size_t)b * T * C : nullptr;
   const float* av_b = q.aval + (size_t)b * (T + 1) * C;
@@ -124,7 +138,8 @@ __global__ void __launch_bounds__(64) margfast_kernel(MargParams q) {
   double* xr = reinterpret_cast<double*>(smem + L.xring) + (size_t)g * RL;
   // per-step operands of the current batch of J positions [tb, tb+J)
   double* alv = reinterpret_cast<double*>(smem + L.alv);  // [J]    alpha levels
-  float* cmv = reinterpret_cast<float*>(smem + L.cmv);    // [CB][J] cum of own labels
+  double* cmv = reinterpret_cast<double*>(smem + L.cmv);  // [CB][J] cum of own labels
+  double* crr = reinterpret_cast<double*>(smem + L.carry) + 2 * g;  // emission input: x / step stream totals
   float* psv = reinterpret_cast<float*>(smem + L.psv);    // [CB][J] proj_start of own labels
 
   // ---- constants ----
@@ -143,8 +158,21 @@ __global__ void __launch_bounds__(64) margfast_kernel(MargParams q) {
   }
 
   // x of position e (own label), or "does not exist" beyond len
-  auto x_of = [&](int e, float bv, double bl, float cm, float pe) -> double {
-    return (e <= len) ? (bl + (double)(bv + pe)) + (double)cm * kLog2eD : kInvD;
+  auto x_of = [&](int e, float bv, double bl, double cm, float pe) -> double {
+    return (e <= len) ? (bl + (double)(bv + pe)) + cm * kLog2eD : kInvD;
+  };
+  // emission input: cum of one batch of J consecutive positions from their score
+  // rows d (inclusive prefix over the group) and the stream's total before them
+  auto em_scan = [&](float d, double& total) -> double {
+    double v = (double)d;
+#pragma unroll
+    for (int o = 1; o < J; o <<= 1) {
+      const double w = __shfl_up(v, o, J);
+      if (lj >= o) v += w;
+    }
+    const double val = total + v;
+    total = __shfl(val, J - 1, J);
+    return val;
   };
   auto clampT = [&](int e) { return e > T ? T : e; };
 
@@ -153,12 +181,18 @@ __global__ void __launch_bounds__(64) margfast_kernel(MargParams q) {
   // batch appends J positions, and when the next batch would run past RL
   // entries the KP live positions move to the front.
   int ofs = t0 + 1;
+  double xtot = 0.0;  // emission input: cum of the x stream's last position (t0: 0)
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int e = t0 + 1 + lj + J * r;
     const int ec = clampT(e);
     const float pe = (has_pe && ec >= 1) ? pe_b[(size_t)(ec - 1) * C + c] * kLog2e : 0.0f;
-    xr[e - ofs] = x_of(e, bv_b[(size_t)ec * C + c], bl_b[ec], cum_b[(size_t)ec * C + c], pe);
+    const double cm = emit ? em_scan(xs_at(e), xtot) : (double)xs_at(ec);
+    xr[e - ofs] = x_of(e, bv_b[(size_t)ec * C + c], bl_b[ec], cm, pe);
+  }
+  if (emit && lj == 0) {
+    crr[0] = xtot;
+    crr[1] = 0.0;  // the step stream starts at t0, cum 0
   }
   // Batches of J steps.  At a batch start tb the registers loaded one batch
   // earlier are written to LDS -- x for positions tb+KP+1 .. tb+KP+J and the
@@ -172,11 +206,12 @@ __global__ void __launch_bounds__(64) margfast_kernel(MargParams q) {
     const int ec = clampT(e);
     sb_bv = bv_b[(size_t)ec * C + c];
     sb_bl = bl_b[ec];
-    sb_cm = cum_b[(size_t)ec * C + c];
+    sb_cm = emit ? xs_at(e) : xs_at(ec);
     sb_pe = (has_pe && ec >= 1) ? pe_b[(size_t)(ec - 1) * C + c] * kLog2e : 0.0f;
     ral = al_b[clampT(tb + (lane % J))];
     const int tp = clampT(tb + lj);
-    rcm = cum_b[(size_t)tp * C + c];
+    // emission input: position t0 adds nothing to its stream
+    rcm = emit ? (tb + lj > t0 ? xs_at(tb + lj) : 0.0f) : xs_at(tp);
     rps = has_ps ? ps_b[(size_t)min(tp, T - 1) * C + c] : 0.0f;
   };
   load_batch(t0, e_n);
@@ -242,9 +277,20 @@ __global__ void __launch_bounds__(64) margfast_kernel(MargParams q) {
         ofs = t + 1;
         wave_lds_order();
       }
-      xr[e_n - ofs] = x_of(e_n, sb_bv, sb_bl, sb_cm, sb_pe);
+      double cme = (double)sb_cm, cmt = (double)rcm;
+      if (emit) {
+        double xt = crr[0], st = crr[1];
+        cme = em_scan(sb_cm, xt);
+        cmt = em_scan(rcm, st);
+        wave_lds_order();
+        if (lj == 0) {
+          crr[0] = xt;
+          crr[1] = st;
+        }
+      }
+      xr[e_n - ofs] = x_of(e_n, sb_bv, sb_bl, cme, sb_pe);
       if (lane < J) alv[lane] = ral;
-      cmv[g * J + lj] = rcm;
+      cmv[g * J + lj] = cmt;
       psv[g * J + lj] = rps;
       e_n += J;
       load_batch(t + J, e_n);
@@ -256,7 +302,7 @@ __global__ void __launch_bounds__(64) margfast_kernel(MargParams q) {
     for (int i = 0; i < kCJ; ++i) rv[i] = rvn[i];
     load_row(t + 1);
     const double al = alv[ib];
-    const float cm = cmv[g * J + ib];
+    const double cm = cmv[g * J + ib];
     const float ps_t = psv[g * J + ib];
     // ---- u[t,c] and the softmax weights of the source labels ----
     float mq = kMinusInf;
@@ -273,7 +319,7 @@ __global__ void __launch_bounds__(64) margfast_kernel(MargParams q) {
     }
     const float S = group_sum<J>(sw);
     const float u2 = M + log2_hw(S);
-    const double At = ((al + (double)(u2 + ps_t * kLog2e)) - (double)cm * kLog2eD) - z2;
+    const double At = ((al + (double)(u2 + ps_t * kLog2e)) - cm * kLog2eD) - z2;
 
     // ---- segment marginals over the lane's durations ----
     // The previous step's end sums slide to positions t+1+lj+16r: lane 0 takes its

@@ -258,10 +258,17 @@ __global__ void __launch_bounds__(1024) block_coverage_kernel(MargParams q, doub
     const int t_ref = nb * q.TB - 1;
     const int s0 = max(0, t_ref - Kmax + 1);
     const size_t row0 = (size_t)b * (T + 1);
-    const float* cum_b = q.cum + row0 * C;
+    const bool emit = q.emit != nullptr;
+    const float* cum_b = emit ? nullptr : q.cum + row0 * C;
+    const float* em_b = emit ? q.emit + (size_t)b * T * C : nullptr;
     const int n = (t_ref - s0 + 1) * C;
     for (int w = threadIdx.x; w < n; w += blockDim.x) {
       const int s = s0 + w / C, c = w % C;
+      // emission input: cum[e] - cum[s] as a running sum of score rows, from
+      // e = t_ref + 1 (rows s .. t_ref) upward
+      double dse = 0.0;
+      if (emit)
+        for (int u = s; u <= t_ref; ++u) dse += (double)em_b[(size_t)u * C + c];
       // forward side: alpha level + u[s,c] (+ proj_start) - cum[s,c] log2 e - log2 Z
       const float* ah = q.aval + (row0 + s) * C;
       float mu = kMinusInf;
@@ -270,14 +277,20 @@ __global__ void __launch_bounds__(1024) block_coverage_kernel(MargParams q, doub
       for (int cp = 0; cp < C; ++cp) su += exp2_hw((ah[cp] + q.trans[(size_t)cp * C + c] * kLog2e) - mu);
       float ua = mu + log2_hw(su);
       if (q.ps != nullptr) ua += q.ps[((size_t)b * T + s) * C + c] * kLog2e;
-      const double A = (q.alvl[row0 + s] + (double)ua) - (double)cum_b[(size_t)s * C + c] * kLog2eM - q.z2[b];
+      const double A = (q.alvl[row0 + s] + (double)ua) - (emit ? 0.0 : (double)cum_b[(size_t)s * C + c] * kLog2eM) - q.z2[b];
       const int k0 = t_ref - s + 1, k1 = min(Kmax, len - s);
       float sk = 0.0f;
       for (int k = k0; k <= k1; ++k) {
         const int e = s + k;
         float xb = q.bval[(row0 + e) * C + c];
         if (q.pe != nullptr) xb += q.pe[((size_t)b * T + e - 1) * C + c] * kLog2e;
-        const double x = (q.blvl[row0 + e] + (double)xb) + (double)cum_b[(size_t)e * C + c] * kLog2eM;
+        double x = q.blvl[row0 + e] + (double)xb;
+        if (emit) {
+          x += dse * kLog2eM;
+          dse += (double)em_b[(size_t)min(e, T - 1) * C + c];
+        } else {
+          x += (double)cum_b[(size_t)e * C + c] * kLog2eM;
+        }
         const float dk = q.db[(size_t)(K == 1 ? 0 : min(k, K - 1)) * C + c] * kLog2e;
         sk += exp2_hw((float)(A + x) + dk);
       }
@@ -318,7 +331,8 @@ __global__ void finalize_rows_kernel(FinalParams f) {
       }
       if (t < len) S = ks * f.s_out[o];
     }
-    f.grad_cum[o] = g * (E - S);
+    if (!f.shift) f.grad_cum[o] = g * (E - S);
+    else if (t >= 1) f.grad_cum[((size_t)b * T + t - 1) * C + c] = g * (E - S);
     if (f.grad_ps != nullptr && t < T) f.grad_ps[((size_t)b * T + t) * C + c] = g * S;
     if (f.grad_pe != nullptr && t >= 1) f.grad_pe[((size_t)b * T + t - 1) * C + c] = g * E;
   }

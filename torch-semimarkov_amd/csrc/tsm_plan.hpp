@@ -73,7 +73,8 @@ __host__ __device__ inline size_t align16(size_t x) { return (x + 15) & ~size_t(
 struct MargFastLds {
   size_t xring;  // double[CB*RL]
   size_t alv;    // double[J]    alpha levels
-  size_t cmv;    // float[CB*J]  cumulative scores of the own labels
+  size_t cmv;    // double[CB*J] cumulative scores of the own labels (emission input: in the block's frame)
+  size_t carry;  // double[CB][2] emission input: running cum of the x and step streams
   size_t psv;    // float[CB*J]  proj_start of the own labels
   size_t total;
 };
@@ -83,7 +84,8 @@ __host__ __device__ inline MargFastLds margfast_lds_layout(int CB, int RL, int J
   size_t o = 0;
   L.xring = o; o = align16(o + 8 * (size_t)CB * RL);
   L.alv = o; o = align16(o + 8 * (size_t)J);
-  L.cmv = o; o = align16(o + 4 * (size_t)CB * J);
+  L.cmv = o; o = align16(o + 8 * (size_t)CB * J);
+  L.carry = o; o = align16(o + 16 * (size_t)CB);
   L.psv = o; o = align16(o + 4 * (size_t)CB * J);
   L.total = o;
   return L;
@@ -154,6 +156,7 @@ struct FastLds {
   size_t lring;  // double[RS]   per-position levels
   size_t row;    // float[2*C]   per-step row of all labels (double buffered)
   size_t red;    // double[64]   block reductions (verification)
+  size_t cx;     // double[C]    emission input: each label's running cumulative score
   size_t total;
 };
 
@@ -164,6 +167,7 @@ __host__ __device__ inline FastLds fast_lds_layout(int C, int RL, int RS) {
   L.lring = o; o = align16(o + sizeof(double) * RS);
   L.row = o; o = align16(o + sizeof(float) * 2 * C);
   L.red = o; o = align16(o + sizeof(double) * 64);
+  L.cx = o; o = align16(o + sizeof(double) * C);
   L.total = o;
   return L;
 }

@@ -9,6 +9,8 @@
 //
 //   forward : cum[b, 0, c] = 0,  cum[b, u, c] = sum_{t<u} (x[b,t,c] - centre * mean_t x[b,t,c])
 //   backward: G[b,t,c] = sum_{u>t} g[b,u,c];  grad_x = G - centre * mean_t G
+//             (g may also be held in grad_x itself, row u at row u-1: each thread
+//             reads a row of its own column before it writes it, so that runs in place)
 //             (sum_t G[t] = sum_u u * g[u], so the centring term is one more column sum)
 //
 // HBM-bound.  Three passes of reduce-then-scan: per block of TT positions
@@ -66,7 +68,7 @@ __global__ void __launch_bounds__(kPNT) prologue_reduce_kernel(PrologueParams q)
   if (act) {
     for (int r = r0 + rg; r < r1; r += RG) {
       if constexpr (BWD) {
-        const double v = (double)q.g[((size_t)b * (T + 1) + r) * C + c];
+        const double v = (double)q.g[((size_t)b * q.GR + r + q.goff) * C + c];
         s += v;
         s2 += (double)r * v;
       } else {
@@ -130,7 +132,7 @@ __global__ void __launch_bounds__(kPNT) prologue_scan_kernel(PrologueParams q) {
   const int base = BWD ? 1 + blk * kPTT : blk * kPTT;
   double s = 0.0;
   for (int i = ra; i < rb; ++i) {
-    if constexpr (BWD) s += (double)q.g[((size_t)b * (T + 1) + base + i) * C + c];
+    if constexpr (BWD) s += (double)q.g[((size_t)b * q.GR + base + i + q.goff) * C + c];
     else s += (double)load_x<DT>(q.x, ((size_t)b * T + base + i) * C + c);
   }
   tot[tid] = s;
@@ -152,7 +154,7 @@ __global__ void __launch_bounds__(kPNT) prologue_scan_kernel(PrologueParams q) {
     for (int i = rg + 1; i < RG; ++i) carry += tot[i * CG + tid % CG];
     for (int i = rb - 1; i >= ra; --i) {
       const int u = base + i;  // grad_x[u-1] = sum of g over rows >= u
-      carry += (double)q.g[((size_t)b * (T + 1) + u) * C + c];
+      carry += (double)q.g[((size_t)b * q.GR + u + q.goff) * C + c];
       q.gx[((size_t)b * T + u - 1) * C + c] = (float)(carry - mean);
     }
   }

@@ -11,10 +11,13 @@ Public API (same names and meanings as the reference package for this path):
 * :class:`UncertaintyMixin`, :class:`UncertaintySemiMarkovCRFHead` -- boundary /
   position marginals, streaming entropy, uncertainty-weighted loss
 * :func:`emission_cum_scores` -- projected scores to cumulative scores on the GPU
+* :func:`semi_crf_emissions_forward`, :func:`score_gold_emissions` -- the scan and
+  the gold-path score on projected scores, with the prefix sums fused into the
+  kernels (what the head's ``compute_loss`` / ``decode`` run)
 """
 
 from .duration import DurationDistribution, LearnedDuration
-from .helpers import Segment, ViterbiResult, score_gold_vectorized
+from .helpers import Segment, ViterbiResult, score_gold_emissions, score_gold_vectorized
 from .nn import SemiMarkovCRFHead
 from .streaming import (
     HAS_HIP,
@@ -22,6 +25,7 @@ from .streaming import (
     SemiCRFStreamingHIP,
     compute_edge_block_streaming,
     emission_cum_scores,
+    semi_crf_emissions_forward,
     semi_crf_streaming_forward,
 )
 from .uncertainty import UncertaintyMixin, UncertaintySemiMarkovCRFHead
@@ -43,4 +47,6 @@ __all__ = [
     "UncertaintyMixin",
     "UncertaintySemiMarkovCRFHead",
     "emission_cum_scores",
+    "semi_crf_emissions_forward",
+    "score_gold_emissions",
 ]

@@ -3,9 +3,13 @@
 :class:`SemiMarkovCRFHead` has the constructor, parameters, initialisation
 order and methods of the reference's ``SemiMarkovCRFHead`` (``nn.py:55-565``):
 ``forward`` / ``compute_loss`` / ``decode`` / ``decode_with_traceback``.  The
-scan always runs on the GPU through :func:`semi_crf_streaming_forward`;
-``decode_with_traceback`` uses the exact Viterbi kernel with an on-device
-backtrace instead of the reference's per-sequence Python loop.
+scan always runs on the GPU.  ``compute_loss`` and ``decode`` hand the projected
+scores straight to the scan (:func:`semi_crf_emissions_forward`,
+:func:`score_gold_emissions`), whose kernels carry the prefix sums themselves:
+the ``(B, T+1, C)`` cumulative scores are built only where the reference's API
+returns or reads them (``forward``'s ``"cum_scores"``, the segment scores of
+``decode_with_traceback``).  ``decode_with_traceback`` runs the Viterbi with an
+on-device backtrace instead of the reference's per-sequence Python loop.
 """
 
 from __future__ import annotations
@@ -18,9 +22,9 @@ import torch.nn as nn
 from torch import Tensor
 
 from .duration import DurationDistribution, LearnedDuration
-from .helpers import Segment, ViterbiResult, score_gold_vectorized
+from .helpers import Segment, ViterbiResult, score_gold_emissions, score_gold_vectorized
 from .streaming import ops
-from .streaming.autograd import prepare_inputs, semi_crf_streaming_forward
+from .streaming.autograd import prepare_inputs, semi_crf_emissions_forward, semi_crf_streaming_forward
 from .streaming.prologue import emission_cum_scores
 
 
@@ -71,13 +75,17 @@ class SemiMarkovCRFHead(nn.Module):
         return self.duration_dist()
 
     # ------------------------------------------------------------------ helpers
-    def _cum_scores(self, hidden_states: Tensor) -> Tensor:
-        """``(B, T+1, C)`` fp32 prefix sums of the projected scores, row 0 = 0 (``nn.py:196-209``),
-        built by the HIP emission prologue (fp64 prefix sums rounded once)."""
+    def _scores(self, hidden_states: Tensor) -> Tensor:
+        """Projected scores ``(B, T, C)`` (``nn.py:197-201``)."""
         scores = self.projection(hidden_states) if self.projection is not None else hidden_states
         if scores.shape[-1] != self.num_classes:
             raise ValueError(f"scores have {scores.shape[-1]} labels, the head {self.num_classes}")
-        return emission_cum_scores(scores)
+        return scores
+
+    def _cum_scores(self, hidden_states: Tensor) -> Tensor:
+        """``(B, T+1, C)`` fp32 prefix sums of the projected scores, row 0 = 0 (``nn.py:196-209``),
+        built by the HIP emission prologue (fp64 prefix sums rounded once)."""
+        return emission_cum_scores(self._scores(hidden_states))
 
     # ------------------------------------------------------------------ API
     def forward(self, hidden_states: Tensor, lengths: Tensor, use_triton: bool = True) -> dict:
@@ -93,9 +101,20 @@ class SemiMarkovCRFHead(nn.Module):
         self, hidden_states: Tensor, lengths: Tensor, labels: Tensor, use_triton: bool = True,
         reduction: str = "mean",
     ) -> Tensor:
-        """Negative log-likelihood ``log Z - score(gold)`` (``nn.py:224-271``)."""
-        res = self.forward(hidden_states, lengths, use_triton)
-        nll = res["partition"] - self._score_gold(res["cum_scores"], labels, lengths)
+        """Negative log-likelihood ``log Z - score(gold)`` (``nn.py:224-271``).
+
+        The partition and the gold score are computed from the projected scores
+        directly (the scan kernels carry the prefix sums), with the values of the
+        reference's ``forward`` + ``score_gold_vectorized`` on ``cum_scores``."""
+        scores = self._scores(hidden_states)
+        partition = semi_crf_emissions_forward(
+            scores, self.transition, self.duration_bias, lengths, self.max_duration, semiring="log",
+        )
+        gold = score_gold_emissions(
+            scores=scores, labels=labels, lengths=lengths, transition=self.transition,
+            duration_bias=self.duration_bias, max_duration=self.max_duration,
+        )
+        nll = partition - gold
         if reduction == "mean":
             return nll.mean()
         if reduction == "sum":
@@ -109,11 +128,10 @@ class SemiMarkovCRFHead(nn.Module):
         )
 
     def decode(self, hidden_states: Tensor, lengths: Tensor, use_triton: bool = True) -> Tensor:
-        """Viterbi score ``(B,)`` (``nn.py:306-358``)."""
-        cum = self._cum_scores(hidden_states)
-        return semi_crf_streaming_forward(
-            cum, self.transition, self.duration_bias, lengths, self.max_duration,
-            semiring="max", use_triton=use_triton,
+        """Viterbi score ``(B,)`` (``nn.py:306-358``), from the projected scores directly."""
+        return semi_crf_emissions_forward(
+            self._scores(hidden_states), self.transition, self.duration_bias, lengths, self.max_duration,
+            semiring="max",
         )
 
     def decode_with_traceback(

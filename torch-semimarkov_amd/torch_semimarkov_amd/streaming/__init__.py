@@ -19,10 +19,12 @@ import torch
 
 from .. import _native
 from .autograd import (
+    SemiCRFEmissionsHIP,
     SemiCRFStreamingHIP,
     _compute_checkpoint_interval,
     launch_streaming_hip_backward,
     launch_streaming_hip_kernel,
+    semi_crf_emissions_forward,
     semi_crf_streaming_forward,
 )
 from .constants import NEG_INF
@@ -69,7 +71,9 @@ def compute_edge_block_streaming(
 
 __all__ = [
     "semi_crf_streaming_forward",
+    "semi_crf_emissions_forward",
     "SemiCRFStreamingHIP",
+    "SemiCRFEmissionsHIP",
     "SemiCRFStreamingTriton",
     "compute_edge_block_streaming",
     "launch_streaming_hip_kernel",

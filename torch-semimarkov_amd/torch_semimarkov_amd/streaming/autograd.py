@@ -11,10 +11,17 @@ Differences from the reference, all deliberate:
 
 * ``use_triton`` / ``use_compile`` are accepted for signature compatibility and
   ignored: the HIP backend is the only backend.
-* Inference with ``semiring="max"`` runs the exact Viterbi kernel, which is
-  bit-identical to the reference's fp32 max recursion.  With gradients the max
-  semiring uses the factorised scan (soft max-marginals in the backward, as the
-  reference's CPU backward computes them, ``pytorch_reference.py:458-467``).
+* Inference with ``semiring="max"`` runs ``tsm_viterbi`` with the AUTO
+  algorithm: the exact Viterbi kernel (bit-identical to the reference's fp32 max
+  recursion) for problems that fit one chunk per sequence, the chunked
+  factorised scan otherwise (scores within 1e-5 of the fp64 optimum).  With
+  gradients the max semiring uses the factorised scan (soft max-marginals in the
+  backward, as the reference's CPU backward computes them,
+  ``pytorch_reference.py:458-467``).
+* :func:`semi_crf_emissions_forward` takes the projected scores ``(B, T, C)``
+  themselves (no reference counterpart: the reference's head builds
+  ``cum_scores`` with ``torch.cumsum`` first, ``nn.py:196-209``); its kernels
+  carry the prefix sums in registers.
 * Inputs are validated up front (shapes, devices, ``0 <= lengths <= T`` when
   ``lengths`` is on the host); the reference validates only the semiring.
 * Duration-dependent ``(K, C, C)`` transitions (``transition[k]`` for a segment of
@@ -47,8 +54,10 @@ def _as_f32(x: torch.Tensor) -> torch.Tensor:
     return x if x.dtype == torch.float32 else x.float()
 
 
-def prepare_inputs(cum_scores, transition, duration_bias, lengths, K, proj_start=None, proj_end=None):
-    """Validate and normalise the operator inputs.
+def prepare_inputs(cum_scores, transition, duration_bias, lengths, K, proj_start=None, proj_end=None,
+                   emissions=False):
+    """Validate and normalise the operator inputs (``emissions=True``: the first
+    argument is the projected scores ``(B, T, C)`` instead of ``(B, T+1, C)``).
 
     Returns ``(cum, transition, duration_bias_eff, lengths, proj_start, proj_end)`` as
     contiguous fp32 tensors (int64 lengths) on the device of ``cum_scores``.  The
@@ -56,18 +65,19 @@ def prepare_inputs(cum_scores, transition, duration_bias, lengths, K, proj_start
     so that row ``min(k, K-1)`` holds the reference's row ``min(k, duration_bias.shape[0]-1)``
     (``pytorch_reference.py:90-92``); the re-indexing is an autograd-tracked gather.
     """
+    what = "scores" if emissions else "cum_scores"
     if not isinstance(cum_scores, torch.Tensor) or cum_scores.dim() != 3:
-        raise ValueError("cum_scores must be a (batch, T+1, C) tensor")
+        raise ValueError(f"{what} must be a (batch, {'T' if emissions else 'T+1'}, C) tensor")
     if not cum_scores.is_cuda:
         raise RuntimeError(
-            "torch_semimarkov_amd runs on AMD GPUs only: cum_scores is on "
+            f"torch_semimarkov_amd runs on AMD GPUs only: {what} is on "
             f"{cum_scores.device}; move the inputs to a ROCm device (e.g. .to('cuda'))"
         )
     dev = cum_scores.device
     B, Tp1, C = cum_scores.shape
-    T = Tp1 - 1
+    T = Tp1 if emissions else Tp1 - 1
     if T < 1:
-        raise ValueError("cum_scores must have at least 2 rows along dim 1 (T >= 1)")
+        raise ValueError(f"{what} must have at least {1 if emissions else 2} rows along dim 1 (T >= 1)")
     K = int(K)
     if K < 1:
         raise ValueError(f"K (max_duration) must be >= 1, got {K}")
@@ -202,6 +212,80 @@ def semi_crf_streaming_forward(
     return out if out.dtype == out_dtype else out.to(out_dtype)
 
 
+class SemiCRFEmissionsHIP(torch.autograd.Function):
+    r""":class:`SemiCRFStreamingHIP` on the projected scores ``(B, T, C)``.
+
+    ``apply(scores, transition, duration_bias, lengths, K, semiring, proj_start,
+    proj_end)``; the backward returns the gradient w.r.t. ``scores`` (the suffix
+    sums of the cumulative-score gradient: the posterior label occupancy of each
+    position, weighted by ``grad_output``) in place of ``cum_scores``'s.
+    """
+
+    @staticmethod
+    def forward(ctx, scores, transition, duration_bias, lengths, K, semiring="log", proj_start=None, proj_end=None):
+        sr = SEMIRINGS[semiring]
+        part, z2, ah, al, _ = ops.scan_forward_em(
+            scores.detach(), transition.detach(), duration_bias.detach(), lengths, int(K), sr,
+            proj_start.detach() if proj_start is not None else None,
+            proj_end.detach() if proj_end is not None else None, True,
+        )
+        ctx.save_for_backward(scores, transition, duration_bias, lengths, proj_start, proj_end, ah, al, z2)
+        ctx.K = int(K)
+        ctx.semiring = sr
+        return part
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        sc, tr, db, lengths, ps, pe, ah, al, z2 = ctx.saved_tensors
+        g = grad_output.detach().to(torch.float32).contiguous()
+        g_sc, g_tr, g_db, g_ps, g_pe, _ = ops.scan_backward_em(
+            sc.detach(), tr.detach(), db.detach(), lengths, ctx.K, ctx.semiring,
+            ps.detach() if ps is not None else None, pe.detach() if pe is not None else None,
+            ah, al, z2, g,
+        )
+        return (
+            g_sc, g_tr, g_db, None, None, None,
+            g_ps if ps is not None else None,
+            g_pe if pe is not None else None,
+        )
+
+
+def semi_crf_emissions_forward(
+    scores: torch.Tensor,
+    transition: torch.Tensor,
+    duration_bias: torch.Tensor,
+    lengths: torch.Tensor,
+    K: int,
+    semiring: str = "log",
+    proj_start: Optional[torch.Tensor] = None,
+    proj_end: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    r""":func:`semi_crf_streaming_forward` of ``cum_scores = [0, cumsum(scores, dim=1)]``,
+    computed from the projected scores ``(B, T, C)`` directly.
+
+    The emission prologue of the reference's head (``nn.py:196-209``: a zeroed
+    ``(B, T+1, C)`` buffer filled by ``torch.cumsum``) is fused into the scans'
+    streamed loads: the register-resident kernels keep the prefix sums in fp64
+    registers, so no ``(B, T+1, C)`` tensor is built (other plans build it in the
+    workspace).  Differentiable in ``scores``, ``transition``, ``duration_bias``
+    and the projections.
+    """
+    if semiring not in SEMIRINGS:
+        raise ValueError(f"semiring must be 'log' or 'max', got {semiring!r}")
+    out_dtype = scores.dtype if scores.is_floating_point() else torch.float32
+    sc, tr, db, lengths, ps, pe = prepare_inputs(
+        scores, transition, duration_bias, lengths, K, proj_start, proj_end, emissions=True
+    )
+    needs_grad = torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (sc, tr, db, ps, pe))
+    if needs_grad:
+        out = SemiCRFEmissionsHIP.apply(sc, tr, db, lengths, int(K), semiring, ps, pe)
+    elif semiring == "log":
+        out = ops.scan_forward_em(sc, tr, db, lengths, int(K), SEMIRINGS["log"], ps, pe, False)[0]
+    else:
+        out = ops.viterbi_em(sc, tr, db, lengths, int(K), ps, pe, False)[0]
+    return out if out.dtype == out_dtype else out.to(out_dtype)
+
+
 def launch_streaming_hip_kernel(
     cum_scores, transition, duration_bias, lengths, K, semiring="log", checkpoint_interval=None,
     proj_start=None, proj_end=None,
@@ -253,6 +337,8 @@ def launch_streaming_hip_backward(
 __all__ = [
     "SemiCRFStreamingHIP",
     "semi_crf_streaming_forward",
+    "SemiCRFEmissionsHIP",
+    "semi_crf_emissions_forward",
     "launch_streaming_hip_kernel",
     "launch_streaming_hip_backward",
     "_compute_checkpoint_interval",

@@ -284,6 +284,187 @@ def _(labels, lengths, grad_output, T, C, K, Kdb):
     return f(B, T + 1, C), f(C, C), f(Kdb, C)
 
 
+# --------------------------------------------------------------------------- emission input
+# The same passes on projected scores (B, T, C) fp32 instead of cumulative scores
+# (tsm_*_emissions): the register-resident scans read the scores and carry the
+# prefix sums themselves, so no (B, T+1, C) tensor is built (see include/tsm_hip.h).
+@torch.library.custom_op("tsm_amd::scan_forward_em", mutates_args=())
+def scan_forward_em(
+    scores: Tensor, transition: Tensor, duration_bias: Tensor, lengths: Tensor, K: int, semiring: int,
+    proj_start: Optional[Tensor], proj_end: Optional[Tensor], store: bool,
+) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """As :func:`scan_forward` on ``scores`` (B, T, C), T >= 1."""
+    lib = N.lib()
+    B, T, C = scores.shape
+    dev = scores.device
+    part = torch.empty(B, device=dev, dtype=torch.float32)
+    z2 = torch.empty(B, device=dev, dtype=torch.float64)
+    rec = torch.empty(B, device=dev, dtype=torch.int32)
+    if store:
+        ah = torch.empty(B, T + 1, C, device=dev, dtype=torch.float32)
+        al = torch.empty(B, T + 1, device=dev, dtype=torch.float64)
+    else:
+        ah = torch.empty(0, device=dev, dtype=torch.float32)
+        al = torch.empty(0, device=dev, dtype=torch.float64)
+    tr_rows = _trans_rows(transition)
+    nbytes = _size(lib.tsm_forward_emissions_workspace, B, T, C, K, tr_rows, semiring, proj_start is not None,
+                   proj_end is not None)
+    ws = _workspace(nbytes, dev)
+    with torch.cuda.device(dev):
+        rc = lib.tsm_forward_emissions(
+            N.ptr(scores), N.ptr(transition), N.ptr(duration_bias), N.ptr(lengths),
+            N.ptr(proj_start), N.ptr(proj_end), B, T, C, K, tr_rows, semiring,
+            N.ptr(part), N.ptr(z2), N.ptr(ah) if store else None, N.ptr(al) if store else None,
+            N.ptr(rec), N.ptr(ws), ws.numel(), _stream(dev),
+        )
+    N.check(rc, "tsm_forward_emissions")
+    _check_cooperative(rec, B, T, C, K, semiring, tr_rows, "tsm_forward_emissions")
+    return part, z2, ah, al, rec
+
+
+@scan_forward_em.register_fake
+def _(scores, transition, duration_bias, lengths, K, semiring, proj_start, proj_end, store):
+    B, T, C = scores.shape
+    part = scores.new_empty(B)
+    z2 = scores.new_empty(B, dtype=torch.float64)
+    rec = scores.new_empty(B, dtype=torch.int32)
+    if store:
+        return part, z2, scores.new_empty(B, T + 1, C), scores.new_empty(B, T + 1, dtype=torch.float64), rec
+    return part, z2, scores.new_empty(0), scores.new_empty(0, dtype=torch.float64), rec
+
+
+@torch.library.custom_op("tsm_amd::scan_backward_em", mutates_args=())
+def scan_backward_em(
+    scores: Tensor, transition: Tensor, duration_bias: Tensor, lengths: Tensor, K: int, semiring: int,
+    proj_start: Optional[Tensor], proj_end: Optional[Tensor], alpha_hat: Tensor, alpha_level: Tensor,
+    log2_partition: Tensor, grad_output: Tensor,
+) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """As :func:`scan_backward`, with grad_scores (B, T, C) in place of grad_cum."""
+    lib = N.lib()
+    B, T, C = scores.shape
+    dev = scores.device
+    g_sc = torch.empty(B, T, C, device=dev, dtype=torch.float32)
+    g_tr = torch.empty(transition.shape, device=dev, dtype=torch.float32)
+    g_db = torch.empty(K, C, device=dev, dtype=torch.float32)
+    g_ps = torch.empty(B, T, C, device=dev, dtype=torch.float32) if proj_start is not None else None
+    g_pe = torch.empty(B, T, C, device=dev, dtype=torch.float32) if proj_end is not None else None
+    rec = torch.empty(B, device=dev, dtype=torch.int32)
+    tr_rows = _trans_rows(transition)
+    nbytes = _size(lib.tsm_backward_emissions_workspace, B, T, C, K, tr_rows, semiring, proj_start is not None,
+                   proj_end is not None)
+    ws = _workspace(nbytes, dev)
+    with torch.cuda.device(dev):
+        rc = lib.tsm_backward_emissions(
+            N.ptr(scores), N.ptr(transition), N.ptr(duration_bias), N.ptr(lengths),
+            N.ptr(proj_start), N.ptr(proj_end), B, T, C, K, tr_rows, semiring,
+            N.ptr(alpha_hat), N.ptr(alpha_level), N.ptr(log2_partition), N.ptr(grad_output),
+            N.ptr(g_sc), N.ptr(g_tr), N.ptr(g_db), N.ptr(g_ps), N.ptr(g_pe), N.ptr(rec),
+            N.ptr(ws), ws.numel(), _stream(dev),
+        )
+    N.check(rc, "tsm_backward_emissions")
+    _check_cooperative(rec, B, T, C, K, semiring, tr_rows, "tsm_backward_emissions")
+    empty = torch.empty(0, device=dev, dtype=torch.float32)
+    return g_sc, g_tr, g_db, g_ps if g_ps is not None else empty, g_pe if g_pe is not None else empty.clone(), rec
+
+
+@scan_backward_em.register_fake
+def _(scores, transition, duration_bias, lengths, K, semiring, proj_start, proj_end, alpha_hat, alpha_level,
+      log2_partition, grad_output):
+    B, T, C = scores.shape
+    g_ps = scores.new_empty(B, T, C) if proj_start is not None else scores.new_empty(0)
+    g_pe = scores.new_empty(B, T, C) if proj_end is not None else scores.new_empty(0)
+    return (scores.new_empty(B, T, C), transition.new_empty(transition.shape), scores.new_empty(K, C), g_ps, g_pe,
+            scores.new_empty(B, dtype=torch.int32))
+
+
+@torch.library.custom_op("tsm_amd::viterbi_em", mutates_args=())
+def viterbi_em(
+    scores: Tensor, transition: Tensor, duration_bias: Tensor, lengths: Tensor, K: int,
+    proj_start: Optional[Tensor], proj_end: Optional[Tensor], traceback: bool, algorithm: int = 0,
+) -> tuple[Tensor, Tensor, Tensor]:
+    """As :func:`viterbi` on ``scores`` (B, T, C), T >= 1."""
+    lib = N.lib()
+    B, T, C = scores.shape
+    dev = scores.device
+    score = torch.empty(B, device=dev, dtype=torch.float32)
+    if traceback:
+        cnt = torch.empty(B, device=dev, dtype=torch.int32)
+        segs = torch.empty(B, T, 4, device=dev, dtype=torch.int32)
+    else:
+        cnt = torch.empty(0, device=dev, dtype=torch.int32)
+        segs = torch.empty(0, device=dev, dtype=torch.int32)
+    tr_rows = _trans_rows(transition)
+    nbytes = _size(lib.tsm_viterbi_emissions_workspace, B, T, C, K, tr_rows, int(traceback), int(algorithm))
+    ws = _workspace(nbytes, dev)
+    with torch.cuda.device(dev):
+        rc = lib.tsm_viterbi_emissions(
+            N.ptr(scores), N.ptr(transition), N.ptr(duration_bias), N.ptr(lengths),
+            N.ptr(proj_start), N.ptr(proj_end), B, T, C, K, tr_rows, N.ptr(score), int(traceback), int(algorithm),
+            N.ptr(cnt) if traceback else None, N.ptr(segs) if traceback else None,
+            N.ptr(ws), ws.numel(), _stream(dev),
+        )
+    N.check(rc, "tsm_viterbi_emissions")
+    return score, cnt, segs
+
+
+@viterbi_em.register_fake
+def _(scores, transition, duration_bias, lengths, K, proj_start, proj_end, traceback, algorithm=0):
+    B, T, C = scores.shape
+    if traceback:
+        return (scores.new_empty(B), scores.new_empty(B, dtype=torch.int32),
+                scores.new_empty(B, T, 4, dtype=torch.int32))
+    return scores.new_empty(B), scores.new_empty(0, dtype=torch.int32), scores.new_empty(0, dtype=torch.int32)
+
+
+@torch.library.custom_op("tsm_amd::gold_score_em", mutates_args=())
+def gold_score_em(scores: Tensor, transition: Tensor, duration_bias: Tensor, labels: Tensor, lengths: Tensor,
+                  K: int) -> Tensor:
+    """As :func:`gold_score` on ``scores`` (B, T, C): a segment's content is the sum of its scores."""
+    lib = N.lib()
+    B, T, C = scores.shape
+    dev = scores.device
+    Kdb = duration_bias.shape[0]
+    score = torch.empty(B, device=dev, dtype=torch.float32)
+    ws = _workspace(_size(lib.tsm_gold_score_workspace, B, T, C, K, Kdb), dev)
+    with torch.cuda.device(dev):
+        rc = lib.tsm_gold_score_emissions(N.ptr(scores), N.ptr(transition), N.ptr(duration_bias), N.ptr(labels),
+                                          N.ptr(lengths), B, T, C, K, Kdb, N.ptr(score), N.ptr(ws), ws.numel(),
+                                          _stream(dev))
+    N.check(rc, "tsm_gold_score_emissions")
+    return score
+
+
+@gold_score_em.register_fake
+def _(scores, transition, duration_bias, labels, lengths, K):
+    return scores.new_empty(scores.shape[0])
+
+
+@torch.library.custom_op("tsm_amd::gold_score_em_backward", mutates_args=())
+def gold_score_em_backward(labels: Tensor, lengths: Tensor, grad_output: Tensor, T: int, C: int, K: int,
+                           Kdb: int) -> tuple[Tensor, Tensor, Tensor]:
+    """grad_scores (B,T,C) (scaled by grad_output), grad_transition (C,C), grad_duration_bias (Kdb,C)."""
+    lib = N.lib()
+    B = labels.shape[0]
+    dev = labels.device
+    g_sc = torch.empty(B, T, C, device=dev, dtype=torch.float32)
+    g_tr = torch.empty(C, C, device=dev, dtype=torch.float32)
+    g_db = torch.empty(Kdb, C, device=dev, dtype=torch.float32)
+    ws = _workspace(_size(lib.tsm_gold_score_workspace, B, T, C, K, Kdb), dev)
+    with torch.cuda.device(dev):
+        rc = lib.tsm_gold_score_emissions_backward(N.ptr(labels), N.ptr(lengths), B, T, C, K, Kdb,
+                                                   N.ptr(grad_output), N.ptr(g_sc), N.ptr(g_tr), N.ptr(g_db),
+                                                   N.ptr(ws), ws.numel(), _stream(dev))
+    N.check(rc, "tsm_gold_score_emissions_backward")
+    return g_sc, g_tr, g_db
+
+
+@gold_score_em_backward.register_fake
+def _(labels, lengths, grad_output, T, C, K, Kdb):
+    B = labels.shape[0]
+    f = grad_output.new_empty
+    return f(B, T, C), f(C, C), f(Kdb, C)
+
+
 # --------------------------------------------------------------------------- checkpoints
 @torch.library.custom_op("tsm_amd::ring_checkpoints", mutates_args=())
 def ring_checkpoints(alpha_hat: Tensor, alpha_level: Tensor, lengths: Tensor, K: int, interval: int,
