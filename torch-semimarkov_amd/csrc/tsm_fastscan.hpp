@@ -202,27 +202,42 @@ struct Chunk {
     [[maybe_unused]] float* halo_i = MARG ? p.halo + (size_t)item * Kmax * C : nullptr;
     [[maybe_unused]] const int own_hi = (FWD || j < jl) ? t_hi : len + 1;  // rows [t_lo, own_hi) are this chunk's
     [[maybe_unused]] const int lane_last = (lj == J - 1) ? -1 : 0;       // all bits set on the row's last lane
-    // Duration sums: fp32 per lane, added every 128 owned steps (and at the end)
-    // to the chunk's fp64 partials with no-return atomics -- each (k, c) has one
-    // lane, so they never contend, and nothing waits for them.  (An fp32 sum of
-    // at most 128 positive terms is within 128 ulp; the atomics leave the XCD,
-    // 8 bytes each, so fewer folds mean less fabric traffic.)
+    // Duration sums: fp32 per lane, added every 128 owned steps (each (k, c) has
+    // one lane; an fp32 sum of at most 128 positive terms is within 128 ulp) to
+    // fp64 sums.  Up to 20 durations per lane those are registers, written to
+    // the chunk's partials once at the end: the kernel runs one workgroup per CU
+    // (its rings fill the LDS), so the 2R extra registers cost no occupancy,
+    // where the periodic 8-byte atomics they replace wrote about 0.5 GB per
+    // launch at cfg3.  Longer lanes (no room in 256 registers) add into the
+    // zeroed partials with no-return atomics, which never contend.
+    constexpr bool kRegD = R <= 20;
     double zd = 0.0;
     float d32[MARG ? R : 1], ea[MARG ? R : 1];
+    double d64[MARG && kRegD ? R : 1];
     [[maybe_unused]] double* dbp = MARG ? p.db_part + (size_t)item * Kmax * C : nullptr;
     if constexpr (MARG) {
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         d32[r] = 0.0f;
         ea[r] = 0.0f;
-        const int k = 1 + lj + J * r;
-        if (cval && k <= Kmax) dbp[(size_t)(k - 1) * C + c] = 0.0;
+        if constexpr (kRegD) {
+          d64[r] = 0.0;
+        } else {
+          const int k = 1 + lj + J * r;
+          if (cval && k <= Kmax) dbp[(size_t)(k - 1) * C + c] = 0.0;
+        }
       }
       if (tid == 0) p.mframe[item] = 0.0;
-      __threadfence();  // the zeros before the first atomic add
+      if constexpr (!kRegD) __threadfence();  // the zeros before the first atomic add
     }
     auto fold_d = [&]() {
-      if constexpr (MARG) {
+      if constexpr (MARG && kRegD) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          d64[r] += (double)d32[r];
+          d32[r] = 0.0f;
+        }
+      } else if constexpr (MARG) {
         // addresses and masks from an opaque copy of the lane index: otherwise they
         // are hoisted out of the step loop and held in registers throughout
         int ljo = lj;
@@ -338,14 +353,8 @@ struct Chunk {
     auto pa_row = [&](int t) { return FWD ? clampT1(t - 1) : clampT1(t); };
     auto pb_row = [&](int t) { return FWD ? clampT1(t) : clampT1(t - 1); };
     float cum_n = xs_b[(size_t)xs_row(t_first) * C + c];
-    // emission input: the running sgn * cum * log2(e) of the previous position sits in
-    // LDS (one word per label, written by the group's lane 0 at the end of each step),
-    // so it holds no register across steps
-    [[maybe_unused]] double* cxs = reinterpret_cast<double*>(smem + L.cx);
-    if constexpr (EMIT) {
-      if (cval && lj == 0) cxs[c] = 0.0;
-      wave_lds_order();
-    }
+    // emission input: the running sgn * cum * log2(e) of the previous position
+    [[maybe_unused]] double cx_run = 0.0;
     float pa_n = pa_src[(size_t)pa_row(t_first) * C + c];
     float pb_n = pb_src[(size_t)pb_row(t_first) * C + c];
     [[maybe_unused]] float u_n = 0.0f;
@@ -371,7 +380,7 @@ struct Chunk {
           double m = -1e300;
           if (cval) {
             double carry = 0.0;
-            if constexpr (EMIT) carry = cxs[c];  // position t_hi (the previous step, or t_start)
+            if constexpr (EMIT) carry = cx_run;  // position t_hi (the previous step, or t_start)
             for (int i0 = EMIT ? 0 : lj; i0 < Kmax; i0 += J) {
               const int i = EMIT ? i0 + lj : i0;
               const int pos = t_hi + i;
@@ -409,7 +418,7 @@ struct Chunk {
         A = A0 - 1;
       }
       double cx_t;
-      if constexpr (EMIT) cx_t = cxs[c] + (double)cum_n * kLog2eD;
+      if constexpr (EMIT) cx_t = cx_run = cx_run + (double)cum_n * kLog2eD;
       else cx_t = sgn * (double)cum_n * kLog2eD;
       const float pa_t = pa_n * ((FWD ? t >= 1 : true) ? pa_scale : 0.0f);
       const float pb_t = pb_n * ((FWD ? true : t >= 1) ? pb_scale : 0.0f);
@@ -626,7 +635,6 @@ struct Chunk {
       // ---- ring entry for position t ----
       if (cval && lj == 0) {
         rc[A] = (lvl_t + (double)(mixv + pb_t)) - cx_t;
-        if constexpr (EMIT) cxs[c] = cx_t;
       }
       if (tid == 0) lring[t % RS] = lvl_t;
       lvl_prev = lvl_t;
@@ -673,6 +681,15 @@ struct Chunk {
         if (lj == 0) e_own_b[(size_t)t_lo * C + c] = 0.0f;
       }
       fold_d();
+      if constexpr (kRegD) {
+        if (cval) {
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            const int k = 1 + lj + J * r;
+            if (k <= Kmax) dbp[(size_t)(k - 1) * C + c] = d64[r];
+          }
+        }
+      }
     }
   }
 };

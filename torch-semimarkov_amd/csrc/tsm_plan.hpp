@@ -156,7 +156,6 @@ struct FastLds {
   size_t lring;  // double[RS]   per-position levels
   size_t row;    // float[2*C]   per-step row of all labels (double buffered)
   size_t red;    // double[64]   block reductions (verification)
-  size_t cx;     // double[C]    emission input: each label's running cumulative score
   size_t total;
 };
 
@@ -167,7 +166,6 @@ __host__ __device__ inline FastLds fast_lds_layout(int C, int RL, int RS) {
   L.lring = o; o = align16(o + sizeof(double) * RS);
   L.row = o; o = align16(o + sizeof(float) * 2 * C);
   L.red = o; o = align16(o + sizeof(double) * 64);
-  L.cx = o; o = align16(o + sizeof(double) * C);
   L.total = o;
   return L;
 }
