@@ -151,33 +151,33 @@ class SemiMarkovCRFHead(nn.Module):
             db = self.duration_bias.detach()
             cum_p, tr_p, db_p, len_p, _, _ = prepare_inputs(cum, tr, db, lengths, self.max_duration)
             score, cnt, segs = ops.viterbi(cum_p, tr_p, db_p, len_p, self.max_duration, None, None, True)
-            B = cum.shape[0]
-            lens = len_p.cpu().tolist()
-            counts = cnt.cpu().tolist()
-            want = [b for b in range(B) if 0 < lens[b] <= max_traceback_length and counts[b] > 0]
+            B, T = cum.shape[0], cum.shape[1] - 1
+            # every row (start, end, label, previous label) with its fp32 score terms, gathered on
+            # the GPU over all T rows (rows at or beyond a sequence's count are unwritten: zeroed
+            # first) and brought to the host in one transfer, the counts and lengths in another
+            live = torch.arange(T, device=cum.device).view(1, T) < cnt.to(cum.device).view(B, 1)
+            rows = torch.where(live.unsqueeze(-1), segs.long(), torch.zeros_like(segs, dtype=torch.long))
+            bidx = torch.arange(B, device=cum.device).view(B, 1).expand(B, T)
+            start, end, lab, prev = rows[..., 0], rows[..., 1], rows[..., 2], rows[..., 3]
+            # fp32 content exactly as (cum[end+1, l] - cum[start, l])
+            content = cum[bidx, (end + 1).clamp(max=T), lab] - cum[bidx, start, lab]
+            K = self.max_duration
+            dscore = db[torch.clamp(end - start + 1, max=K - 1), lab]
+            tscore = tr[prev, lab]
+            packed = torch.stack([start.double(), end.double(), lab.double(), content.double(), dscore.double(),
+                                  tscore.double()], dim=-1).cpu().numpy()
+            meta = torch.stack([cnt.to(len_p.device).long(), len_p.long()]).cpu().tolist()
+            counts, lens = meta
             all_segments: list[list[Segment]] = [[] for _ in range(B)]
-            if want:
-                nmax = max(counts[b] for b in want)
-                rows = segs[:, :nmax].long()  # (B, nmax, 4), last segment first
-                # rows at or beyond a sequence's count are unwritten: zero them before gathering
-                live = torch.arange(nmax, device=cum.device).view(1, nmax) < cnt.to(cum.device).view(B, 1)
-                rows = torch.where(live.unsqueeze(-1), rows, torch.zeros_like(rows))
-                bidx = torch.arange(B, device=cum.device).view(B, 1).expand(B, nmax)
-                start, end, lab, prev = rows[..., 0], rows[..., 1], rows[..., 2], rows[..., 3]
-                # fp32 content exactly as (cum[end+1, l] - cum[start, l])
-                content = cum[bidx, (end + 1).clamp(max=cum.shape[1] - 1), lab] - cum[bidx, start, lab]
-                K = self.max_duration
-                dur_idx = torch.clamp(end - start + 1, max=K - 1)
-                dscore = db[dur_idx, lab]
-                tscore = tr[prev, lab]
-                host = torch.stack([content, dscore, tscore], dim=-1).cpu().numpy().astype(np.float64)
-                rows_h = rows.cpu().numpy()
-                for b in want:
-                    n = counts[b]
-                    # first segment first; plain Python ints / floats via tolist()
-                    r = rows_h[b, :n][::-1].tolist()
-                    h = host[b, :n][::-1].tolist()
-                    all_segments[b] = [Segment(s_, e_, l_, (c_ + d_) + t_) for (s_, e_, l_, _), (c_, d_, t_) in zip(r, h)]
+            for b in range(B):
+                n = counts[b]
+                if not (0 < lens[b] <= max_traceback_length and n > 0):
+                    continue
+                r = packed[b, :n][::-1]  # first segment first
+                sc = (r[:, 3] + r[:, 4]) + r[:, 5]  # (content + duration) + transition, fp64 of fp32 terms
+                ints = r[:, :3].astype(np.int64)
+                all_segments[b] = list(map(Segment, ints[:, 0].tolist(), ints[:, 1].tolist(), ints[:, 2].tolist(),
+                                           sc.tolist()))
         return ViterbiResult(scores=score, segments=all_segments)
 
     def extra_repr(self) -> str:
