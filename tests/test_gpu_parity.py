@@ -263,6 +263,10 @@ CASES = [
     (2, 40, 9, 12, [40, 33], True, "log"),      # 32-lane label groups
     (2, 36, 5, 16, [36, 20], False, "max"),
     (1, 30, 4, 70, None, False, "log"),         # 4-lane groups
+    # unit durations (Kmax = 1): the position-parallel marginal kernel
+    (3, 70, 2, 5, [70, 41, 1], True, "log"),
+    (2, 90, 1, 16, [90, 64], True, "max"),
+    (2, 300, 1, 3, [300, 299], False, "log"),
 ]
 
 # Plans outside the register / LDS-ring fast path: more than 32 durations per

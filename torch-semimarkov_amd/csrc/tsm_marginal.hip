@@ -419,10 +419,114 @@ int launch_marg_j(const Plan& pl, const MargParams& q, hipStream_t st) {
   return hipGetLastError();
 }
 
+// Marginals of unit-duration segments (Kmax = 1: K = 1 or 2, the HMM).  Every
+// start t has the one segment [t, t+1), so the marginals need no walk over the
+// block: P(t,c) = 2^(A[t,c] + x[t+1,c] + db[c]) with
+//   A = alpha level + u[t,c] (+ proj_start) - cum[t,c] - log2 Z,
+//   x = beta level + beta-hat[t+1,c] (+ proj_end[t]) + cum[t+1,c]
+// (cum[t+1]-cum[t] = scores[t] with emission input), and every (t, c) is
+// independent.  Thread (lane, c) takes label c of the positions t0+lane,
+// t0+lane+NL, ... (NL = 256 / C lanes); its transition-gradient column G[:, c]
+// and duration sum accumulate in fp64 registers, then the lanes are summed in
+// fp64 through LDS.  The register-
+// resident kernel walks a block one position per step (latency-bound: 0.21 ms
+// at B=32, T=10^4, C=8).  Outputs: the blocked layout of the other marginal
+// kernels (e_own / halo / s_out rows, fp64 block partials).  C <= kUnitMaxC.
+constexpr int kUnitMaxC = 16;
+
+__global__ void __launch_bounds__(256) unit_marginal_kernel(MargParams q) {
+  extern __shared__ double usm[];  // [NL][C] duration sums, then [NL][C][C] transition sums
+  const int C = q.C, T = q.T, K = q.K;
+  const int blk = blockIdx.x, b = blockIdx.y;
+  const int NL = 256 / C;
+  const int tid = threadIdx.x, c = tid % C, lane = tid / C;
+  const bool act = lane < NL;
+  const int len = mlen(q.lengths, b, T);
+  const int t0 = blk * q.TB, own_hi = t0 + q.TB;
+  const int t1 = min(own_hi, len);
+  const size_t row0 = (size_t)b * (T + 1);
+  float* e_own_b = q.e_own + row0 * C;
+  float* s_out_b = q.s_out + row0 * C;
+  float* halo_b = q.halo + ((size_t)b * q.NB + blk) * C;  // Kmax = 1: one row
+  double* dbp = q.db_part + ((size_t)b * q.NB + blk) * C;
+  double* trp = q.tr_part + ((size_t)b * q.NB + blk) * C * C;
+  const bool emit = q.emit != nullptr;
+  double G[kUnitMaxC];
+  float trc[kUnitMaxC];
+#pragma unroll
+  for (int i = 0; i < kUnitMaxC; ++i) {
+    G[i] = 0.0;
+    trc[i] = (i < C) ? q.trans[(size_t)i * C + c] * kLog2e : 0.0f;  // source i -> destination c
+  }
+  double D = 0.0;
+  const float dbk = q.db[(size_t)(K == 1 ? 0 : 1) * C + c] * kLog2e;  // duration 1: row min(1, K-1)
+  const double z2 = q.z2[b];
+  if (act && t0 == len && lane == 0) e_own_b[(size_t)len * C + c] = 0.0f;
+  if (act && t0 < len) {
+    if (lane == 0) e_own_b[(size_t)t0 * C + c] = 0.0f;  // no start of this block ends at t0
+    for (int t = t0 + lane; t < t1; t += NL) {
+      const float* ah = q.aval + (row0 + t) * C;
+      float mx = kMinusInf;
+#pragma unroll
+      for (int i = 0; i < kUnitMaxC; ++i)
+        if (i < C) mx = fmax2(mx, ah[i] + trc[i]);
+      float sw = 0.0f;
+#pragma unroll
+      for (int i = 0; i < kUnitMaxC; ++i)
+        if (i < C) sw += exp2_hw((ah[i] + trc[i]) - mx);
+      const float u2 = mx + log2_hw(sw);
+      float ua = u2, xb = q.bval[(row0 + t + 1) * C + c];
+      if (q.ps != nullptr) ua += q.ps[((size_t)b * T + t) * C + c] * kLog2e;
+      if (q.pe != nullptr) xb += q.pe[((size_t)b * T + t) * C + c] * kLog2e;
+      const double dc = emit ? (double)q.emit[((size_t)b * T + t) * C + c] * kLog2eM
+                             : ((double)q.cum[(row0 + t + 1) * C + c] - (double)q.cum[(row0 + t) * C + c]) * kLog2eM;
+      const double ax = ((q.alvl[row0 + t] + (double)ua) + (q.blvl[row0 + t + 1] + (double)xb)) - z2;
+      const float P = exp2_hw((float)(ax + dc) + dbk);
+      s_out_b[(size_t)t * C + c] = P;
+      if (t + 1 < own_hi) e_own_b[(size_t)(t + 1) * C + c] = P;
+      else halo_b[c] = P;
+      D += P;
+      // the source weights of u: 2^(alpha-hat + tr - u) = 2^(alpha-hat + tr - mx) / sw
+      const float wS = P / sw;
+#pragma unroll
+      for (int i = 0; i < kUnitMaxC; ++i)
+        if (i < C) G[i] += (double)(exp2_hw((ah[i] + trc[i]) - mx) * wS);
+    }
+  }
+  // lanes -> block partials (fp64)
+  double* dl = usm;
+  double* gl = usm + (size_t)NL * C;
+  if (act) {
+    dl[lane * C + c] = D;
+#pragma unroll
+    for (int i = 0; i < kUnitMaxC; ++i)
+      if (i < C) gl[((size_t)lane * C + c) * C + i] = G[i];
+  }
+  __syncthreads();
+  for (int e = tid; e < C + C * C; e += blockDim.x) {
+    double a = 0.0;
+    if (e < C) {
+      for (int l = 0; l < NL; ++l) a += dl[l * C + e];
+      dbp[e] = a;
+    } else {
+      const int cs = (e - C) / C, cd = (e - C) % C;  // tr_part[c_src][c_dst]
+      for (int l = 0; l < NL; ++l) a += gl[((size_t)l * C + cd) * C + cs];
+      trp[(size_t)cs * C + cd] = a;
+    }
+  }
+}
+
 }  // namespace
 
 int launch_marginals(const Plan& pl, const MargParams& q, hipStream_t s) {
   if (pl.dense) return launch_dense_marginals(pl, q, s);
+  if (pl.mfast && pl.Kmax == 1 && pl.C <= kUnitMaxC && q.trows == 0) {
+    TimedLaunch tl(kKMarginal, s);
+    const int NL = 256 / pl.C;
+    const size_t lds = sizeof(double) * ((size_t)NL * pl.C + (size_t)NL * pl.C * pl.C);
+    hipLaunchKernelGGL(unit_marginal_kernel, dim3(q.NB, pl.B), dim3(256), lds, s, q);
+    return hipGetLastError();
+  }
   if (pl.mfast) return launch_margfast_j16(pl, q, s);
   switch (pl.JM) {
     case 1: return launch_marg_j<1>(pl, q, s);
