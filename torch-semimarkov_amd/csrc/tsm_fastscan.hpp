@@ -124,7 +124,7 @@ struct Chunk {
     const bool cval = g < C;
     const int c = cval ? g : C - 1;  // padding groups shadow the last label and never write
     constexpr bool emit = EMIT;
-    const float* cum_b = emit ? nullptr : p.cum + (size_t)b * (T + 1) * C;
+    const float* cum_b = p.cum + (size_t)b * (T + 1) * C;  // not read with emission input
     const float* em_b = emit ? p.emit + (size_t)b * T * C : nullptr;
     const bool has_ps = p.ps != nullptr, has_pe = p.pe != nullptr;
     const float* ps_b = has_ps ? p.ps + (size_t)b * T * C : nullptr;
@@ -304,26 +304,39 @@ struct Chunk {
     } else {
       lvl_prev = (mode == 1) ? 0.0 : init_lv[0];
       // positions t_start -/+ i, i < Kmax
-      if (cval) {
-        double carry = 0.0;  // emission input: the chunk's frame has cum = 0 at t_start
-        for (int i0 = EMIT ? 0 : lj; i0 < Kmax; i0 += J) {
-          const int i = EMIT ? i0 + lj : i0;
-          double cxp = 0.0;
-          if constexpr (EMIT) {
-            cxp = behind_em(em_b, C, c, T, lj, t_start, i, carry);
+      if constexpr (EMIT) {
+        if (cval) {
+          double carry = 0.0;  // the chunk's frame has cum = 0 at t_start
+          for (int i0 = 0; i0 < Kmax; i0 += J) {
+            const int i = i0 + lj;
+            const double cxp = behind_em(em_b, C, c, T, lj, t_start, i, carry);
             if (i >= Kmax) continue;
+            const int pos = FWD ? t_start - i : t_start + i;
+            float v;
+            if (mode == 1) {
+              if (FWD) v = has_ps ? ps_b[(size_t)pos * C + c] * kLog2e : 0.0f;
+              else v = has_pe ? pe_b[(size_t)(pos - 1) * C + c] * kLog2e : 0.0f;
+            } else {
+              v = init_st[(size_t)i * C + c];
+            }
+            const double lv = (mode == 1) ? 0.0 : init_lv[i];
+            rc[A0 + i] = lv + (double)v - cxp;
           }
-          const int pos = FWD ? t_start - i : t_start + i;
-          if constexpr (!EMIT) cxp = cumx(pos);
-          float v;
-          if (mode == 1) {
-            if (FWD) v = has_ps ? ps_b[(size_t)pos * C + c] * kLog2e : 0.0f;
-            else v = has_pe ? pe_b[(size_t)(pos - 1) * C + c] * kLog2e : 0.0f;
-          } else {
-            v = init_st[(size_t)i * C + c];
+        }
+      } else {
+        if (cval) {
+          for (int i = lj; i < Kmax; i += J) {
+            const int pos = FWD ? t_start - i : t_start + i;
+            float v;
+            if (mode == 1) {
+              if (FWD) v = has_ps ? ps_b[(size_t)pos * C + c] * kLog2e : 0.0f;
+              else v = has_pe ? pe_b[(size_t)(pos - 1) * C + c] * kLog2e : 0.0f;
+            } else {
+              v = init_st[(size_t)i * C + c];
+            }
+            const double lv = (mode == 1) ? 0.0 : init_lv[i];
+            rc[A0 + i] = lv + (double)v - cumx(pos);
           }
-          const double lv = (mode == 1) ? 0.0 : init_lv[i];
-          rc[A0 + i] = lv + (double)v - cxp;
         }
       }
       for (int i = tid; i < Kmax; i += NT) {
@@ -378,23 +391,32 @@ struct Chunk {
           __asm__ volatile("" : "+s"(bo));
           const size_t row0 = (size_t)bo * (T + 1);
           double m = -1e300;
-          if (cval) {
-            double carry = 0.0;
-            if constexpr (EMIT) carry = cx_run;  // position t_hi (the previous step, or t_start)
-            for (int i0 = EMIT ? 0 : lj; i0 < Kmax; i0 += J) {
-              const int i = EMIT ? i0 + lj : i0;
-              const int pos = t_hi + i;
-              double cxv = 0.0;
-              if constexpr (EMIT) {
-                cxv = behind_em(em_b, C, c, T, lj, t_hi, i, carry);
-                if (i >= Kmax) continue;
+          if constexpr (EMIT) {
+            if (cval) {
+              double carry = cx_run;  // position t_hi (the previous step, or t_start)
+              for (int i0 = 0; i0 < Kmax; i0 += J) {
+                const int i = i0 + lj;
+                const double cxv = behind_em(em_b, C, c, T, lj, t_hi, i, carry);
+                const int pos = t_hi + i;
+                if (i < Kmax && pos <= len) {
+                  const double pbv = (has_pe && pos >= 1) ? (double)(p.pe[((size_t)bo * T + pos - 1) * C + c] * kLog2e) : 0.0;
+                  const double lb = (rc[A + i] - pbv) + cxv;  // log2 beta(pos, c), chunk frame
+                  const double la = (double)p.aval[(row0 + pos) * C + c] + p.alvl[row0 + pos];
+                  m = fmax(m, la + lb);
+                }
               }
-              if (pos <= len) {
-                const double pbv = (has_pe && pos >= 1) ? (double)(p.pe[((size_t)bo * T + pos - 1) * C + c] * kLog2e) : 0.0;
-                if constexpr (!EMIT) cxv = -(double)p.cum[(row0 + pos) * C + c] * kLog2eD;
-                const double lb = (rc[A + i] - pbv) + cxv;  // log2 beta(pos, c), chunk frame
-                const double la = (double)p.aval[(row0 + pos) * C + c] + p.alvl[row0 + pos];
-                m = fmax(m, la + lb);
+            }
+          } else {
+            if (cval) {
+              for (int i = lj; i < Kmax; i += J) {
+                const int pos = t_hi + i;
+                if (pos <= len) {
+                  const double pbv = (has_pe && pos >= 1) ? (double)(p.pe[((size_t)bo * T + pos - 1) * C + c] * kLog2e) : 0.0;
+                  const double cxv = -(double)p.cum[(row0 + pos) * C + c] * kLog2eD;
+                  const double lb = (rc[A + i] - pbv) + cxv;  // log2 beta(pos, c), chunk frame
+                  const double la = (double)p.aval[(row0 + pos) * C + c] + p.alvl[row0 + pos];
+                  m = fmax(m, la + lb);
+                }
               }
             }
           }
@@ -644,20 +666,29 @@ struct Chunk {
       if (t == rec_spec || t == rec_end) {
         float* st = (t == rec_spec ? p.st_spec : p.st_end) + (size_t)item * Kmax * C;
         double* lv = (t == rec_spec ? p.lv_spec : p.lv_end) + (size_t)item * Kmax;
-        if (cval) {
-          double carry = cx_t;  // emission input
-          for (int i0 = EMIT ? 0 : lj; i0 < Kmax; i0 += J) {
-            const int i = EMIT ? i0 + lj : i0;
-            [[maybe_unused]] double cxe = 0.0;
-            if constexpr (EMIT) {
-              cxe = behind_em(em_b, C, c, T, lj, t, i, carry);
+        if constexpr (EMIT) {
+          if (cval) {
+            double carry = cx_t;
+            for (int i0 = 0; i0 < Kmax; i0 += J) {
+              const int i = i0 + lj;
+              const double cxe = behind_em(em_b, C, c, T, lj, t, i, carry);
               if (i >= Kmax) continue;
+              const int pos = FWD ? t - i : t + i;
+              const double x = rc[A + i];
+              const double lp = (i == 0) ? lvl_t : lring[pos % RS];
+              // positions outside the sequence keep the "does not exist" marker
+              st[(size_t)i * C + c] = (x < -1e29) ? -1e30f : (float)((x - lp) + cxe);
             }
-            const int pos = FWD ? t - i : t + i;
-            const double x = rc[A + i];
-            const double lp = (i == 0) ? lvl_t : lring[pos % RS];
-            // positions outside the sequence keep the "does not exist" marker
-            st[(size_t)i * C + c] = (x < -1e29) ? -1e30f : (float)((x - lp) + (EMIT ? cxe : cumx(pos)));
+          }
+        } else {
+          if (cval) {
+            for (int i = lj; i < Kmax; i += J) {
+              const int pos = FWD ? t - i : t + i;
+              const double x = rc[A + i];
+              const double lp = (i == 0) ? lvl_t : lring[pos % RS];
+              // positions outside the sequence keep the "does not exist" marker
+              st[(size_t)i * C + c] = (x < -1e29) ? -1e30f : (float)((x - lp) + cumx(pos));
+            }
           }
         }
         for (int i = tid; i < Kmax; i += NT) {

@@ -14,7 +14,6 @@ enum Semiring : int { kLog = 0, kMax = 1 };
 struct ScanParams {
   // problem
   const float* cum;        // (B, T+1, C)
-  const float* emit;       // (B, T, C) projected scores in place of cum (register-resident scans), or null
   const float* trans;      // (C, C)  transition[c_src][c_dst], natural log units
   const float* db;         // (K, C)  duration bias
   const int64_t* lengths;  // (B,)
@@ -72,6 +71,8 @@ struct ScanParams {
   float* halo;             // (B*P, Kmax, C) end sums of rows t_hi .. t_hi+Kmax-1 of chunk j < jl
   double* db_part;         // (B*P, Kmax, C) duration sums
   double* mframe;          // (B*P) the chunk's frame estimate fr (log2)
+  // emission input: (B, T, C) projected scores in place of cum (register-resident scans), or null
+  const float* emit;
 };
 
 struct MargParams {
