@@ -300,6 +300,49 @@ int tsm_gold_score_emissions_backward(const int64_t* labels, const int64_t* leng
                                       void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Bounded-memory (checkpointed) forward + backward, log semiring: the forward
+ * keeps no alpha table, only per window start (windows of `window` positions,
+ * whole chunks of the forward's plan) the scan's ring state there and the
+ * alpha-hat row; the backward recomputes alpha one window at a time, top
+ * window first, and runs the fused backward over that window from the state
+ * the window above handed down.  Workspace: one window's tables instead of
+ * O(B*T*C).  Replaces the memory scheme of
+ *   streaming/pytorch_reference.py:380-423 (ring checkpoints every
+ *   sqrt(T*K) positions, alpha recomputed per segment in the backward)
+ * Static (C, C) transitions, cumulative-score input, plans with the 16-lane
+ * register-resident scans and fused marginals (C <= 64, K <= 513); other
+ * problems get TSM_ERR_UNSUPPORTED.
+ *   tsm_checkpoint_plan   the window (a multiple of the chunk length) whose
+ *                         backward workspace fits budget_bytes (0: about eight
+ *                         windows), the window count nw = ceil(T / window),
+ *                         and the two workspace sizes
+ *   tsm_checkpointed_workspace  the two workspace sizes for a given window
+ *   tsm_forward_checkpointed  partition / log2_partition as tsm_forward, and
+ *                         ck_state (B, nw, Kmax, C) f32, ck_level (B, nw, Kmax)
+ *                         f64, ck_alpha (B, nw, C) f32, ck_alpha_level (B, nw)
+ *                         f64 (Kmax = max(K-1, 1); entries of window 0 unused)
+ *   tsm_backward_checkpointed  the gradients of tsm_backward (same outputs,
+ *                         fully written) from the inputs and the checkpoints
+ * ------------------------------------------------------------------------- */
+int tsm_checkpoint_plan(int64_t B, int64_t T, int64_t C, int64_t K, int has_proj_start, int has_proj_end,
+                        size_t budget_bytes, int64_t* window, int64_t* n_windows, size_t* forward_workspace_bytes,
+                        size_t* backward_workspace_bytes);
+int tsm_checkpointed_workspace(int64_t B, int64_t T, int64_t C, int64_t K, int has_proj_start, int has_proj_end,
+                               int64_t window, size_t* forward_workspace_bytes, size_t* backward_workspace_bytes);
+int tsm_forward_checkpointed(const float* cum_scores, const float* transition, const float* duration_bias,
+                             const int64_t* lengths, const float* proj_start, const float* proj_end, int64_t B,
+                             int64_t T, int64_t C, int64_t K, int64_t window, float* partition,
+                             double* log2_partition, float* ck_state, double* ck_level, float* ck_alpha,
+                             double* ck_alpha_level, void* workspace, size_t workspace_bytes, void* stream);
+int tsm_backward_checkpointed(const float* cum_scores, const float* transition, const float* duration_bias,
+                              const int64_t* lengths, const float* proj_start, const float* proj_end, int64_t B,
+                              int64_t T, int64_t C, int64_t K, int64_t window, const float* ck_state,
+                              const double* ck_level, const float* ck_alpha, const double* ck_alpha_level,
+                              const double* log2_partition, const float* grad_output, float* grad_cum,
+                              float* grad_transition, float* grad_duration_bias, float* grad_proj_start,
+                              float* grad_proj_end, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Ring checkpoints in the reference's layout (B, n_ckpt, K, C), raw alpha in
  * natural log units, rebuilt from tsm_forward's alpha_hat/alpha_level.
  * Replaces the ring_checkpoints output of

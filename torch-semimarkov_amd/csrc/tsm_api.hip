@@ -93,13 +93,13 @@ bool fast_instantiated(int J, int R) {
 // duration range and wave count give the least work per step; leave p.fast = 0
 // when no instance fits.  TSM_SCAN_PATH=generic in the environment disables
 // the fast path (used by the tests to exercise the generic kernels).
-void plan_fast(Plan& p, const DeviceInfo& di) {
+void plan_fast(Plan& p, const DeviceInfo& di, int fj_only = 0) {
   p.fast = 0;
   const char* env = getenv("TSM_SCAN_PATH");
   if (env != nullptr && strcmp(env, "generic") == 0) return;
   double best = 1e300;
   const char* jenv = getenv("TSM_FAST_J");  // diagnostics: only this lane-group size
-  const int jonly = jenv != nullptr ? atoi(jenv) : 0;
+  const int jonly = fj_only != 0 ? fj_only : (jenv != nullptr ? atoi(jenv) : 0);
   for (int J : {8, 16, 32, 64}) {
     if (jonly != 0 && J != jonly) continue;
     if (p.C > 4 * J) continue;  // the label mix handles at most 4 labels per lane
@@ -248,7 +248,9 @@ int plan_dense(Plan& p, const DeviceInfo& di) {
 
 // Thread mapping, rings, chunking and marginal blocking for a problem shape.
 // trows > 0: the transition is (trows, C, C), one matrix per duration index.
-int make_plan(int64_t B, int64_t T, int64_t C, int64_t K, int has_ps, int has_pe, int64_t trows, Plan* out) {
+// fj_only != 0: register-resident scans with that many lanes per label only
+int make_plan(int64_t B, int64_t T, int64_t C, int64_t K, int has_ps, int has_pe, int64_t trows, Plan* out,
+              int fj_only = 0) {
   if (B < 1 || T < 1 || C < 1 || K < 1) return fail(TSM_ERR_INVALID, "need B, T, C, K >= 1 (got %lld, %lld, %lld, %lld)",
                                                     (long long)B, (long long)T, (long long)C, (long long)K);
   if (C > 512) return fail(TSM_ERR_UNSUPPORTED, "num_classes C=%lld > 512 is not supported", (long long)C);
@@ -343,7 +345,7 @@ int make_plan(int64_t B, int64_t T, int64_t C, int64_t K, int has_ps, int has_pe
     *out = p;
     return TSM_OK;
   }
-  plan_fast(p, di);
+  plan_fast(p, di, fj_only);
   if (!p.fast) plan_coop(p, di);
   if (p.coop) {
     // fewer, longer chunks (one per group): a 4x longer warm-up up front, which
@@ -1611,6 +1613,342 @@ int tsm_gold_score_emissions_backward(const int64_t* labels, const int64_t* len,
   g.gdb = grad_db;
   const int e = tsm::launch_gold_backward(g, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "tsm_gold_score_emissions_backward");
+  return TSM_OK;
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Bounded-memory (checkpointed) forward and backward.  The forward keeps no
+// alpha table: only, per window start (windows of whole chunks), the ring
+// state that the chunk ending there recorded and the alpha-hat row there.  The
+// backward runs each window as a problem of its own, top window first: the
+// forward over the window from its start state (alpha-hat for one window),
+// then the fused backward from the state that the window above recorded at its
+// position 0; rows at window edges add up across windows.  Memory: one
+// window's tables instead of the whole sequence's.  Reference counterpart:
+// the ring checkpoints and per-segment alpha recomputation of
+// streaming/pytorch_reference.py:380-423.
+// ---------------------------------------------------------------------------
+namespace {
+
+int ck_plan(int64_t B, int64_t T, int64_t C, int64_t K, int has_ps, int has_pe, Plan* pl) {
+  const int rc = make_plan(B, T, C, K, has_ps, has_pe, 0, pl, 16);
+  if (rc) return rc;
+  if (!pl->fast || pl->FJ != 16 || !pl->mfused)
+    return fail(TSM_ERR_UNSUPPORTED,
+                "the bounded-memory backward runs the 16-lane register-resident scans with fused marginals "
+                "(C <= 64, K <= 513, static transitions); this problem has no such plan");
+  return TSM_OK;
+}
+
+// One window's buffers: alpha-hat and levels, scratch outputs of its forward,
+// the forward's scan workspace and the backward's workspace.
+struct WinWs {
+  float* ah;
+  double* al;
+  double* z2;
+  float* zout;
+  ScanWs fs;
+  BwdWs bw;
+};
+
+WinWs carve_window(Carver& cv, const Plan& pw) {
+  WinWs w;
+  w.ah = cv.take<float>((size_t)(pw.T + 1) * pw.C);
+  w.al = cv.take<double>((size_t)pw.T + 1);
+  w.z2 = cv.take<double>(1);
+  w.zout = cv.take<float>(1);
+  w.fs = carve_scan(cv, pw, false);
+  w.bw = carve_backward(cv, pw);
+  return w;
+}
+
+struct CkGeom {
+  Plan full, win, last;
+  int Wlen = 0, nw = 0;
+};
+
+// Fixed part of the backward workspace (per-window lengths and flags, the
+// states handed between windows, the end sums beyond a window) and the window
+// region (the larger of a full and the last window).
+struct CkFixed {
+  int64_t* lenw;
+  int *okf, *okb;
+  float *st[2], *thalo;
+  double* lv[2];
+};
+
+CkFixed carve_ck_fixed(Carver& cv, const CkGeom& g) {
+  CkFixed f;
+  const size_t n = (size_t)g.full.B * g.nw;
+  const size_t KC = (size_t)g.full.Kmax * g.full.C;
+  f.lenw = cv.take<int64_t>(n);
+  f.okf = cv.take<int>(n);
+  f.okb = cv.take<int>(n);
+  for (int i = 0; i < 2; ++i) {
+    f.st[i] = cv.take<float>(KC);
+    f.lv[i] = cv.take<double>(g.full.Kmax);
+  }
+  f.thalo = cv.take<float>(KC);
+  return f;
+}
+
+size_t ck_backward_bytes(const CkGeom& g) {
+  Carver cf(nullptr);
+  carve_ck_fixed(cf, g);
+  const size_t fixed = (cf.off + 255) & ~size_t(255);
+  Carver a(nullptr), b(nullptr);
+  carve_window(a, g.win);
+  carve_window(b, g.last);
+  return fixed + std::max(a.off, b.off) + 256;
+}
+
+int ck_window_plans(CkGeom& g, int has_ps, int has_pe) {
+  const int64_t T = g.full.T;
+  int rc = ck_plan(1, std::min<int64_t>(g.Wlen, T), g.full.C, g.full.K, has_ps, has_pe, &g.win);
+  if (rc) return rc;
+  const int64_t last = T - (int64_t)(g.nw - 1) * g.Wlen;
+  return ck_plan(1, last, g.full.C, g.full.K, has_ps, has_pe, &g.last);
+}
+
+int ck_geometry(int64_t B, int64_t T, int64_t C, int64_t K, int has_ps, int has_pe, int64_t window, CkGeom* g) {
+  int rc = ck_plan(B, T, C, K, has_ps, has_pe, &g->full);
+  if (rc) return rc;
+  const int Lc = g->full.Lc;
+  if (window < Lc || window % Lc != 0)
+    return fail(TSM_ERR_INVALID, "window must be a positive multiple of the chunk length %d (got %lld)", Lc,
+                (long long)window);
+  g->Wlen = (int)std::min<int64_t>(window, (int64_t)cdiv(T, Lc) * Lc);
+  g->nw = (int)cdiv(T, g->Wlen);
+  return ck_window_plans(*g, has_ps, has_pe);
+}
+
+}  // namespace
+
+extern "C" {
+
+int tsm_checkpoint_plan(int64_t B, int64_t T, int64_t C, int64_t K, int has_ps, int has_pe, size_t budget_bytes,
+                        int64_t* window, int64_t* n_windows, size_t* forward_ws, size_t* backward_ws) {
+  if (!window || !n_windows || !forward_ws || !backward_ws) return fail(TSM_ERR_INVALID, "null output pointer");
+  CkGeom g;
+  int rc = ck_plan(B, T, C, K, has_ps, has_pe, &g.full);
+  if (rc) return rc;
+  const int Lc = g.full.Lc, P = (int)cdiv(T, Lc);
+  // the longest window of whole chunks whose backward workspace fits the budget
+  // (budget 0: about eight windows)
+  int best = 1;
+  if (budget_bytes == 0) {
+    best = std::max(1, (int)cdiv(P, 8));
+  } else {
+    for (int wc = P; wc >= 1; wc = (wc > 8 ? wc - (wc + 7) / 8 : wc - 1)) {
+      CkGeom h = g;
+      h.Wlen = wc * Lc;
+      h.nw = (int)cdiv(T, h.Wlen);
+      if (ck_window_plans(h, has_ps, has_pe)) return TSM_ERR_UNSUPPORTED;
+      if (ck_backward_bytes(h) <= budget_bytes) {
+        best = wc;
+        break;
+      }
+    }
+  }
+  rc = ck_geometry(B, T, C, K, has_ps, has_pe, (int64_t)best * Lc, &g);
+  if (rc) return rc;
+  *window = g.Wlen;
+  *n_windows = g.nw;
+  Carver cv(nullptr);
+  carve_scan(cv, g.full, false);
+  *forward_ws = cv.off + 256;
+  *backward_ws = ck_backward_bytes(g);
+  return TSM_OK;
+}
+
+int tsm_checkpointed_workspace(int64_t B, int64_t T, int64_t C, int64_t K, int has_ps, int has_pe, int64_t window,
+                               size_t* forward_ws, size_t* backward_ws) {
+  if (!forward_ws || !backward_ws) return fail(TSM_ERR_INVALID, "null output pointer");
+  CkGeom g;
+  const int rc = ck_geometry(B, T, C, K, has_ps, has_pe, window, &g);
+  if (rc) return rc;
+  Carver cv(nullptr);
+  carve_scan(cv, g.full, false);
+  *forward_ws = cv.off + 256;
+  *backward_ws = ck_backward_bytes(g);
+  return TSM_OK;
+}
+
+int tsm_forward_checkpointed(const float* cum, const float* tr, const float* db, const int64_t* len, const float* ps,
+                             const float* pe, int64_t B, int64_t T, int64_t C, int64_t K, int64_t window,
+                             float* partition, double* log2_partition, float* ck_state, double* ck_level,
+                             float* ck_alpha, double* ck_alpha_level, void* workspace, size_t ws_bytes,
+                             void* stream) {
+  int rc = check_common(cum, tr, db, len, TSM_SEMIRING_LOG);
+  if (rc) return rc;
+  if (!partition || !ck_state || !ck_level || !ck_alpha || !ck_alpha_level)
+    return fail(TSM_ERR_INVALID, "partition and the checkpoint outputs are required");
+  CkGeom g;
+  rc = ck_geometry(B, T, C, K, ps != nullptr, pe != nullptr, window, &g);
+  if (rc) return rc;
+  Carver need(nullptr);
+  carve_scan(need, g.full, false);
+  if (!workspace || ws_bytes < need.off + 256)
+    return fail(TSM_ERR_WORKSPACE, "tsm_forward_checkpointed: workspace too small: %zu < %zu bytes", ws_bytes,
+                need.off + 256);
+  hipStream_t st = (hipStream_t)stream;
+  Carver cv(workspace);
+  ScanWs w = carve_scan(cv, g.full, false);
+  tsm::ScanParams p = scan_params(g.full, w, cum, tr, db, len, ps, pe);
+  p.win = 1;
+  p.val = nullptr;
+  p.lvl = nullptr;
+  if (log2_partition) p.z2 = log2_partition;
+  p.zout = partition;
+  p.ck_ah = ck_alpha;
+  p.ck_al = ck_alpha_level;
+  p.ck_every = g.Wlen;
+  p.ck_n = g.nw;
+  int e = tsm::launch_scan_forward(g.full, p, TSM_SEMIRING_LOG, st);
+  if (e != hipSuccess) return hip_fail(e, "tsm_forward_checkpointed");
+  e = tsm::launch_ck_extract(w.st_end, w.lv_end, w.offs, g.full.B, g.full.P, g.Wlen / g.full.Lc, g.full.Kmax, g.full.C,
+                             g.nw, ck_state, ck_level, ck_alpha_level, st);
+  if (e != hipSuccess) return hip_fail(e, "tsm_forward_checkpointed (checkpoints)");
+  return TSM_OK;
+}
+
+int tsm_backward_checkpointed(const float* cum, const float* tr, const float* db, const int64_t* len,
+                              const float* ps, const float* pe, int64_t B, int64_t T, int64_t C, int64_t K,
+                              int64_t window, const float* ck_state, const double* ck_level, const float* ck_alpha,
+                              const double* ck_alpha_level, const double* log2_partition, const float* grad_output,
+                              float* grad_cum, float* grad_tr, float* grad_db, float* grad_ps, float* grad_pe,
+                              void* workspace, size_t ws_bytes, void* stream) {
+  int rc = check_common(cum, tr, db, len, TSM_SEMIRING_LOG);
+  if (rc) return rc;
+  if (!ck_state || !ck_level || !ck_alpha || !ck_alpha_level || !log2_partition || !grad_output || !grad_cum ||
+      !grad_tr || !grad_db)
+    return fail(TSM_ERR_INVALID, "the checkpoints, log2_partition, grad_output and the gradient outputs are required");
+  if ((ps != nullptr) != (grad_ps != nullptr) || (pe != nullptr) != (grad_pe != nullptr))
+    return fail(TSM_ERR_INVALID, "a projection gradient buffer is needed exactly when the projection is given");
+  CkGeom g;
+  rc = ck_geometry(B, T, C, K, ps != nullptr, pe != nullptr, window, &g);
+  if (rc) return rc;
+  const size_t need = ck_backward_bytes(g);
+  if (!workspace || ws_bytes < need)
+    return fail(TSM_ERR_WORKSPACE, "tsm_backward_checkpointed: workspace too small: %zu < %zu bytes", ws_bytes, need);
+  hipStream_t st = (hipStream_t)stream;
+  const int Kmax = g.full.Kmax;
+  const size_t KC = (size_t)Kmax * C;
+  // the outputs accumulate over windows
+  int e = tsm::launch_fill_zero(grad_cum, (size_t)B * (T + 1) * C, st);
+  if (e == hipSuccess) e = tsm::launch_fill_zero(grad_tr, (size_t)C * C, st);
+  if (e == hipSuccess) e = tsm::launch_fill_zero(grad_db, (size_t)K * C, st);
+  if (e == hipSuccess) e = tsm::launch_fill_zero(grad_ps, grad_ps ? (size_t)B * T * C : 0, st);
+  if (e == hipSuccess) e = tsm::launch_fill_zero(grad_pe, grad_pe ? (size_t)B * T * C : 0, st);
+  if (e != hipSuccess) return hip_fail(e, "tsm_backward_checkpointed (zero outputs)");
+  Carver cv(workspace);
+  const CkFixed fx = carve_ck_fixed(cv, g);
+  char* region = static_cast<char*>(workspace) + ((cv.off + 255) & ~size_t(255));
+  e = tsm::launch_window_setup(len, (int)B, (int)T, g.Wlen, g.nw, fx.lenw, fx.okf, fx.okb, st);
+  if (e != hipSuccess) return hip_fail(e, "tsm_backward_checkpointed (windows)");
+  for (int64_t b = 0; b < B; ++b) {
+    int cur = 0;
+    for (int w = g.nw - 1; w >= 0; --w) {
+      const Plan& pw = (w == g.nw - 1) ? g.last : g.win;
+      const int64_t a = (int64_t)w * g.Wlen, Tw = pw.T;
+      const size_t o = (size_t)b * g.nw + w;
+      Carver wc(region);
+      const WinWs ww = carve_window(wc, pw);
+      const float* cum_w = cum + ((size_t)b * (T + 1) + a) * C;
+      const float* ps_w = ps ? ps + ((size_t)b * T + a) * C : nullptr;
+      const float* pe_w = pe ? pe + ((size_t)b * T + a) * C : nullptr;
+      // alpha over the window, from the forward's checkpoint at its start
+      e = tsm::launch_window_row0(ck_alpha, ck_alpha_level, fx.okf, o, (int)C, ww.ah, ww.al, st);
+      if (e != hipSuccess) return hip_fail(e, "tsm_backward_checkpointed (window start)");
+      tsm::ScanParams p = scan_params(pw, ww.fs, cum_w, tr, db, fx.lenw + o, ps_w, pe_w);
+      p.win = 1;
+      p.org_st = ck_state + o * KC;
+      p.org_lv = ck_level + o * Kmax;
+      p.org_ok = fx.okf + o;
+      p.val = ww.ah;
+      p.lvl = ww.al;
+      p.z2 = ww.z2;
+      p.zout = ww.zout;
+      e = tsm::launch_scan_forward(pw, p, TSM_SEMIRING_LOG, st);
+      if (e != hipSuccess) return hip_fail(e, "tsm_backward_checkpointed (window forward)");
+      // the fused backward over the window, from the state the window above recorded
+      const BwdWs& bw = ww.bw;
+      tsm::FusedParams f{};
+      f.lengths = fx.lenw + o;
+      f.trans = tr;
+      f.aval = ww.ah;
+      f.uval = bw.uval;
+      f.B = 1;
+      f.T = (int)Tw;
+      f.C = (int)C;
+      f.K = pw.K;
+      f.Kmax = Kmax;
+      f.P = pw.P;
+      f.Lc = pw.Lc;
+      f.GNB = pw.GNB;
+      f.GTB = pw.GTB;
+      f.offs = bw.scan.offs;
+      f.mframe = bw.mframe;
+      f.cum = cum_w;
+      f.db = db;
+      f.ps = ps_w;
+      f.alvl = ww.al;
+      f.z2 = log2_partition + b;
+      f.st_end = bw.scan.st_end;
+      f.lv_end = bw.scan.lv_end;
+      f.e_own = bw.e_own;
+      f.s_out = bw.s_out;
+      f.halo = bw.halo;
+      f.db_part = bw.db_part;
+      f.tr_part = bw.tr_part;
+      f.grad_output = grad_output + b;
+      f.grad_cum = grad_cum + ((size_t)b * (T + 1) + a) * C;
+      f.grad_ps = grad_ps ? grad_ps + ((size_t)b * T + a) * C : nullptr;
+      f.grad_pe = grad_pe ? grad_pe + ((size_t)b * T + a) * C : nullptr;
+      f.grad_tr = grad_tr;
+      f.grad_db = grad_db;
+      f.accum = 1;
+      f.org_ok = fx.okf + o;
+      f.end_ok = fx.okb + o;
+      e = tsm::launch_u_rows(pw, f, st);
+      if (e != hipSuccess) return hip_fail(e, "tsm_backward_checkpointed (u rows)");
+      tsm::ScanParams q = scan_params(pw, bw.scan, cum_w, tr, db, fx.lenw + o, ps_w, pe_w);
+      q.win = 1;
+      q.org_st = fx.st[cur];
+      q.org_lv = fx.lv[cur];
+      q.org_ok = fx.okb + o;
+      q.thalo = fx.thalo;
+      // (no window below window 0: nothing to record, and no row before its position 0)
+      q.tst_st = w >= 1 ? fx.st[1 - cur] : nullptr;
+      q.tst_lv = w >= 1 ? fx.lv[1 - cur] : nullptr;
+      q.val = nullptr;
+      q.lvl = nullptr;
+      q.zout = nullptr;
+      q.uval = bw.uval;
+      q.aval = ww.ah;
+      q.alvl = ww.al;
+      q.mz2 = log2_partition + b;
+      q.e_own = bw.e_own;
+      q.s_out = bw.s_out;
+      q.halo = bw.halo;
+      q.db_part = bw.db_part;
+      q.mframe = bw.mframe;
+      e = tsm::launch_scan_backward_fused(pw, q, st);
+      if (e != hipSuccess) return hip_fail(e, "tsm_backward_checkpointed (window beta scan)");
+      e = tsm::launch_fused_finalize(pw, f, st);
+      if (e != hipSuccess) return hip_fail(e, "tsm_backward_checkpointed (window finalize)");
+      e = tsm::launch_window_state_fix(fx.lv[1 - cur], bw.scan.offs, Kmax, st);
+      if (e == hipSuccess)
+        e = tsm::launch_window_halo_add(fx.thalo, bw.halo, bw.mframe, fx.lenw, fx.okb, o, pw.Lc, Kmax, (int)C,
+                                        (int)(T - (a + Tw)), grad_output + b,
+                                        grad_cum + ((size_t)b * (T + 1) + a + Tw) * C,
+                                        grad_pe ? grad_pe + ((size_t)b * T + a + Tw) * C : nullptr, st);
+      if (e != hipSuccess) return hip_fail(e, "tsm_backward_checkpointed (window edges)");
+      cur = 1 - cur;
+    }
+  }
   return TSM_OK;
 }
 

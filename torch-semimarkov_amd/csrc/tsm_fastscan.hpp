@@ -67,8 +67,27 @@ __device__ __forceinline__ void lds_barrier() { __asm__ volatile("s_waitcnt lgkm
 // of the same words by other lanes (LDS executes a wave's operations in order).
 __device__ __forceinline__ void wave_lds_order() { __asm__ volatile("" ::: "memory"); }
 
-template <int J, int R, bool FWD, bool LOGSR, bool MARG = false, int CJ = 4, bool EMIT = false>
+// IN: the kind of problem a compiled instance serves -- kInCum (cumulative
+// scores), kInEmit (projected scores, see above) or kInWin (cumulative scores,
+// the problem being one window of a longer sequence in the bounded-memory
+// backward, see below).  Each is its own kernel, so the plain instances carry
+// none of the other kinds' code.
+constexpr int kInCum = 0, kInEmit = 1, kInWin = 2;
+
+template <int J, int R, bool FWD, bool LOGSR, bool MARG = false, int CJ = 4, int IN = kInCum>
 struct Chunk {
+  static constexpr bool EMIT = IN == kInEmit;
+  // Window of a longer sequence (bounded-memory backward): chunks that would
+  // start exactly from the sequence start (forward) or end (backward) start
+  // from the state the caller hands over instead (p.org_st / p.org_lv, per
+  // sequence, where p.org_ok[b] is set), in the ring format the chunks record
+  // (positions 0, -1, ... forward; len, len+1, ... backward; global levels).
+  // The forward can also record alpha-hat rows at multiples of p.ck_every
+  // (p.ck_ah / p.ck_al).  The fused backward's top chunk then is exact in the
+  // global frame (frame factor 1), sends the end sums of positions beyond len
+  // to p.thalo, and chunk 0 records its boundary state at position 0 in
+  // p.tst_st / p.tst_lv for the window below.
+  static constexpr bool WIN = IN == kInWin;
   static_assert(!MARG || (!FWD && LOGSR && J == 16), "fused marginals: backward log scan, 16-lane DPP rows");
   static constexpr int kCJ = CJ;
   static constexpr bool kFwd = FWD;
@@ -124,6 +143,14 @@ struct Chunk {
     const bool cval = g < C;
     const int c = cval ? g : C - 1;  // padding groups shadow the last label and never write
     constexpr bool emit = EMIT;
+    // window: a chunk that starts from the handed-over state
+    [[maybe_unused]] const bool from_org = WIN && mode == 0 && p.org_st != nullptr && p.org_ok[b] != 0;
+    if constexpr (WIN) {
+      if (from_org) {
+        init_st = p.org_st + (size_t)b * Kmax * C;
+        init_lv = p.org_lv + (size_t)b * Kmax;
+      }
+    }
     const float* cum_b = p.cum + (size_t)b * (T + 1) * C;  // not read with emission input
     const float* em_b = emit ? p.emit + (size_t)b * T * C : nullptr;
     const bool has_ps = p.ps != nullptr, has_pe = p.pe != nullptr;
@@ -252,7 +279,7 @@ struct Chunk {
       }
     };
     // ---- initial state ----
-    if (mode == 0) {
+    if (mode == 0 && !from_org) {
       const int pos = t_start;  // FWD: 0, BWD: len
       lvl_prev = 0.0;
       float v0;
@@ -323,6 +350,25 @@ struct Chunk {
             rc[A0 + i] = lv + (double)v - cxp;
           }
         }
+      } else if constexpr (WIN) {
+        // as below; positions before the window (forward) or beyond the sequence
+        // (backward) may be involved: entries marked "does not exist" read no
+        // cumulative score, and level slots wrap for negative positions
+        if (cval) {
+          for (int i = lj; i < Kmax; i += J) {
+            const int pos = FWD ? t_start - i : t_start + i;
+            float v;
+            if (mode == 1) {
+              if (FWD) v = has_ps ? ps_b[(size_t)pos * C + c] * kLog2e : 0.0f;
+              else v = has_pe ? pe_b[(size_t)(pos - 1) * C + c] * kLog2e : 0.0f;
+            } else {
+              v = init_st[(size_t)i * C + c];
+            }
+            const double lv = (mode == 1) ? 0.0 : init_lv[i];
+            // (forward: pos may be negative, a position of the window below)
+            rc[A0 + i] = (v < -1e29f) ? kInvD : lv + (double)v - sgn * (double)cum_b[(ptrdiff_t)pos * C + c] * kLog2eD;
+          }
+        }
       } else {
         if (cval) {
           for (int i = lj; i < Kmax; i += J) {
@@ -341,7 +387,8 @@ struct Chunk {
       }
       for (int i = tid; i < Kmax; i += NT) {
         const int pos = FWD ? t_start - i : t_start + i;
-        lring[pos % RS] = (mode == 1) ? 0.0 : init_lv[i];
+        if constexpr (WIN) lring[((pos % RS) + RS) % RS] = (mode == 1) ? 0.0 : init_lv[i];
+        else lring[pos % RS] = (mode == 1) ? 0.0 : init_lv[i];
       }
     }
     __syncthreads();
@@ -378,12 +425,19 @@ struct Chunk {
     }
 
     const int rec_spec = (mode == 1) ? (FWD ? t_lo : t_hi) : -1;
-    const int rec_end = FWD ? ((t_hi < len) ? t_hi : -1) : ((j >= 1) ? t_lo : -1);
+    // (window: the backward's chunk 0 records its state at position 0 for the window below)
+    const int rec_end = FWD ? ((t_hi < len) ? t_hi : -1)
+                            : ((j >= 1 || (WIN && p.tst_st != nullptr)) ? t_lo : -1);
 
     int A = A0;  // ring index of the current position
     for (int t = t_first; t != t_end; t += dir) {
       if constexpr (MARG) {
-        if (t == t_hi - 1) {
+        if (WIN && from_org && t == t_hi - 1) {
+          // window: a chunk that starts from the handed-over state is exact in the
+          // global frame, so its marginals need no frame (factor 1)
+          zd = p.mz2[b];
+          if (tid == 0) p.mframe[item] = 0.0;
+        } else if (t == t_hi - 1) {
           // frame estimate from the ring of position t_hi (index A) and the Kmax-1 behind
           // it; operands from an opaque copy of the sequence index, so that nothing of
           // this once-per-chunk block is hoisted out of the step loop
@@ -530,6 +584,14 @@ struct Chunk {
               if (pr < own_hi) e_own_b[(size_t)pr * C + c] = ea[R - 1];
               else halo_i[(size_t)(pr - t_hi) * C + c] = ea[R - 1];
             }
+            if constexpr (WIN) {
+              // window: end sums beyond len (positions of the window above): the top
+              // chunk's to thalo, the chunk below it keeps them in its halo rows
+              if (p.thalo != nullptr && cval && lj == J - 1 && pr > len) {
+                if (j == jl && from_org && pr <= len + Kmax - 1) p.thalo[((size_t)b * Kmax + (pr - len - 1)) * C + c] = ea[R - 1];
+                else if (j < jl && pr <= t_hi - 1 + Kmax) halo_i[(size_t)(pr - t_hi) * C + c] = ea[R - 1];
+              }
+            }
             // end sums slide to positions t+1+lj+16r: the last lane takes the previous
             // register (register 0: the new position t+1), then the row rotates one
             // lane up, fused with the accumulation.  Descending r reads ea[r-1] first.
@@ -643,12 +705,21 @@ struct Chunk {
               const float ah = rv[i] - mx;
               if (store && owned) p.val[((size_t)b * (T + 1) + t) * C + ci] = ah;
               if (t == len) p.fin[(size_t)b * C + ci] = ah;
+              if constexpr (WIN) {
+                // checkpoint rows of the bounded-memory backward (levels in the chunk frame)
+                if (p.ck_ah != nullptr && owned && t % p.ck_every == 0 && t / p.ck_every < p.ck_n)
+                  p.ck_ah[((size_t)b * p.ck_n + t / p.ck_every) * C + ci] = ah;
+              }
             }
           }
         }
         if (tid == 0) {
           if (store && owned) p.lvl[(size_t)b * (T + 1) + t] = lvl_t;
           if (t == len) p.fin_lvl[b] = lvl_t;
+          if constexpr (WIN) {
+            if (p.ck_ah != nullptr && owned && t % p.ck_every == 0 && t / p.ck_every < p.ck_n)
+              p.ck_al[(size_t)b * p.ck_n + t / p.ck_every] = lvl_t;
+          }
         }
       } else {
         if (cval && lj == 0 && store && owned) p.val[((size_t)b * (T + 1) + t) * C + c] = mixv;
@@ -666,6 +737,12 @@ struct Chunk {
       if (t == rec_spec || t == rec_end) {
         float* st = (t == rec_spec ? p.st_spec : p.st_end) + (size_t)item * Kmax * C;
         double* lv = (t == rec_spec ? p.lv_spec : p.lv_end) + (size_t)item * Kmax;
+        if constexpr (WIN && !FWD) {
+          if (t == rec_end && j == 0) {
+            st = p.tst_st + (size_t)b * Kmax * C;
+            lv = p.tst_lv + (size_t)b * Kmax;
+          }
+        }
         if constexpr (EMIT) {
           if (cval) {
             double carry = cx_t;
@@ -691,6 +768,13 @@ struct Chunk {
             }
           }
         }
+        if constexpr (WIN && !FWD) {
+          // the state handed to the window below: there position 0 of this window is
+          // the end of that window's sequence part, and its ring entry takes
+          // proj_end of the row before it (segments ending there), which this
+          // window's position 0 (no segment of the window ends there) leaves out
+          if (t == rec_end && j == 0 && has_pe && cval && lj == 0) st[c] += pe_b[c - (ptrdiff_t)C] * kLog2e;
+        }
         for (int i = tid; i < Kmax; i += NT) {
           const int pos = FWD ? t - i : t + i;
           lv[i] = (i == 0) ? lvl_t : lring[pos % RS];
@@ -707,6 +791,12 @@ struct Chunk {
           if (pr <= t_hi - 1 + Kmax && pr <= len) {
             if (pr < own_hi) e_own_b[(size_t)pr * C + c] = ea[r];
             else halo_i[(size_t)(pr - t_hi) * C + c] = ea[r];
+          }
+          if constexpr (WIN) {
+            if (p.thalo != nullptr && pr > len) {
+              if (j == jl && from_org && pr <= len + Kmax - 1) p.thalo[((size_t)b * Kmax + (pr - len - 1)) * C + c] = ea[r];
+              else if (j < jl && pr <= t_hi - 1 + Kmax) halo_i[(size_t)(pr - t_hi) * C + c] = ea[r];
+            }
           }
         }
         if (lj == 0) e_own_b[(size_t)t_lo * C + c] = 0.0f;
@@ -734,12 +824,21 @@ inline bool narrow_mix(const ScanParams& p) { return p.C <= 2 * J; }
 // score instances carry none of the emission code's registers).
 template <int J, int R, bool FWD, bool LOGSR, bool MARG>
 int launch_chunk_any(const Plan& pl, const ScanParams& p, hipStream_t st) {
+  if (p.win) {
+    // windows of the bounded-memory backward: 16-lane log-semiring scans
+    if constexpr (J == 16 && LOGSR && (FWD || MARG)) {
+      if (p.emit != nullptr) return (int)hipErrorInvalidValue;
+      return narrow_mix<J>(p) ? launch_chunk_dir<Chunk<J, R, FWD, LOGSR, MARG, 2, kInWin>>(pl, p, pl.fast_lds, pl.FNT, st)
+                              : launch_chunk_dir<Chunk<J, R, FWD, LOGSR, MARG, 4, kInWin>>(pl, p, pl.fast_lds, pl.FNT, st);
+    }
+    return (int)hipErrorInvalidValue;
+  }
   const bool em = p.emit != nullptr;
   if (narrow_mix<J>(p))
-    return em ? launch_chunk_dir<Chunk<J, R, FWD, LOGSR, MARG, 2, true>>(pl, p, pl.fast_lds, pl.FNT, st)
-              : launch_chunk_dir<Chunk<J, R, FWD, LOGSR, MARG, 2, false>>(pl, p, pl.fast_lds, pl.FNT, st);
-  return em ? launch_chunk_dir<Chunk<J, R, FWD, LOGSR, MARG, 4, true>>(pl, p, pl.fast_lds, pl.FNT, st)
-            : launch_chunk_dir<Chunk<J, R, FWD, LOGSR, MARG, 4, false>>(pl, p, pl.fast_lds, pl.FNT, st);
+    return em ? launch_chunk_dir<Chunk<J, R, FWD, LOGSR, MARG, 2, kInEmit>>(pl, p, pl.fast_lds, pl.FNT, st)
+              : launch_chunk_dir<Chunk<J, R, FWD, LOGSR, MARG, 2, kInCum>>(pl, p, pl.fast_lds, pl.FNT, st);
+  return em ? launch_chunk_dir<Chunk<J, R, FWD, LOGSR, MARG, 4, kInEmit>>(pl, p, pl.fast_lds, pl.FNT, st)
+            : launch_chunk_dir<Chunk<J, R, FWD, LOGSR, MARG, 4, kInCum>>(pl, p, pl.fast_lds, pl.FNT, st);
 }
 
 template <int J, int R>

@@ -186,7 +186,11 @@ __global__ void __launch_bounds__(1024) coverage_kernel(FusedParams f) {
   const int jl = len > 0 ? (len - 1) / Lc : 0;
   if (len == 0 || j > jl) return;
   double acc = 0.0;
-  if (j == 0) {
+  if (j == 0 && f.org_ok != nullptr && f.org_ok[b] != 0) {
+    return;  // window of a longer sequence: position 0 is not covered by the starts there alone
+  } else if (j >= 1 && f.end_ok != nullptr && f.end_ok[b] != 0 && j * Lc - 1 + Kmax > len) {
+    return;  // window: segments covering t_ref may end in the window above
+  } else if (j == 0) {
     for (int c = threadIdx.x; c < C; c += blockDim.x) acc += (double)f.s_out[(size_t)b * (T + 1) * C + c];
   } else {
     // lvs[i]: the chunk's level at t_lo + i; ew[i, c]: its beta state there plus the
@@ -298,6 +302,13 @@ __global__ void fused_rows_kernel(FusedParams f) {
         E = (float)e;
       }
       if (t < len) S = (float)(fj * (double)f.s_out[o]);
+    }
+    if (f.accum) {
+      // window of the bounded-memory backward: rows at its edges take parts from two windows
+      f.grad_cum[o] += g * (E - S);
+      if (f.grad_ps != nullptr && t < T) f.grad_ps[((size_t)b * T + t) * C + c] += g * S;
+      if (f.grad_pe != nullptr && t >= 1) f.grad_pe[((size_t)b * T + t - 1) * C + c] += g * E;
+      continue;
     }
     if (!f.shift) f.grad_cum[o] = g * (E - S);
     else if (t >= 1) f.grad_cum[((size_t)b * T + t - 1) * C + c] = g * (E - S);
@@ -439,8 +450,8 @@ __global__ void __launch_bounds__(256) fused_shared_kernel(FusedParams f) {
   }
   for (int m = 32; m >= 1; m >>= 1) acc += __shfl_xor(acc, m, 64);
   if (lane == 0) {
-    if (idx < n_tr) f.grad_tr[idx] = (float)acc;
-    else f.grad_db[idx - n_tr] = (float)acc;
+    float* out = idx < n_tr ? f.grad_tr + idx : f.grad_db + (idx - n_tr);
+    *out = f.accum ? *out + (float)acc : (float)acc;
   }
 }
 

@@ -77,6 +77,15 @@ _SIGNATURES = {
     "tsm_gold_score_emissions": ([_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _p, _sz, _p], _i32),
     "tsm_gold_score_emissions_backward": (
         [_p, _p, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _sz, _p], _i32),
+    "tsm_checkpoint_plan": ([_i64, _i64, _i64, _i64, _i32, _i32, _sz, ctypes.POINTER(_i64), ctypes.POINTER(_i64),
+                             ctypes.POINTER(_sz), ctypes.POINTER(_sz)], _i32),
+    "tsm_checkpointed_workspace": ([_i64, _i64, _i64, _i64, _i32, _i32, _i64, ctypes.POINTER(_sz),
+                                    ctypes.POINTER(_sz)], _i32),
+    "tsm_forward_checkpointed": (
+        [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _sz, _p], _i32),
+    "tsm_backward_checkpointed": (
+        [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p,
+         _p, _sz, _p], _i32),
     "tsm_ring_checkpoints": ([_p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p], _i32),
     "tsm_timing_enable": ([_i32], _i32),
     "tsm_timing_read": ([ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i64), _i32], _i32),

@@ -20,6 +20,7 @@ import torch
 from .. import _native
 from .autograd import (
     SemiCRFEmissionsHIP,
+    SemiCRFStreamingCheckpointedHIP,
     SemiCRFStreamingHIP,
     _compute_checkpoint_interval,
     launch_streaming_hip_backward,
@@ -73,6 +74,7 @@ __all__ = [
     "semi_crf_streaming_forward",
     "semi_crf_emissions_forward",
     "SemiCRFStreamingHIP",
+    "SemiCRFStreamingCheckpointedHIP",
     "SemiCRFEmissionsHIP",
     "SemiCRFStreamingTriton",
     "compute_edge_block_streaming",

@@ -175,6 +175,65 @@ class SemiCRFStreamingHIP(torch.autograd.Function):
         )
 
 
+class SemiCRFStreamingCheckpointedHIP(torch.autograd.Function):
+    r"""Bounded-memory variant of :class:`SemiCRFStreamingHIP` (log semiring,
+    static transitions): the forward keeps per-window checkpoints only (the scan
+    state and the alpha-hat row at each window start, O(T/window * K*C)), and the
+    backward recomputes alpha one window at a time, top window first, holding
+    one window's tables.  The memory scheme of the reference's ring checkpoints
+    with per-segment alpha recomputation (``pytorch_reference.py:380-423``),
+    with windows of whole scan chunks instead of ``sqrt(T*K)`` positions.
+    ``apply(cum_scores, transition, duration_bias, lengths, K, proj_start,
+    proj_end, window)``.
+    """
+
+    @staticmethod
+    def forward(ctx, cum_scores, transition, duration_bias, lengths, K, proj_start, proj_end, window):
+        B, Tp1, _ = cum_scores.shape
+        nw = -(-(Tp1 - 1) // int(window))
+        det = lambda x: x.detach() if x is not None else None
+        part, z2, st, lv, ah, al = ops.scan_forward_ck(
+            cum_scores.detach(), transition.detach(), duration_bias.detach(), lengths, int(K),
+            det(proj_start), det(proj_end), int(window), nw,
+        )
+        ctx.save_for_backward(cum_scores, transition, duration_bias, lengths, proj_start, proj_end, st, lv, ah, al,
+                              z2)
+        ctx.K = int(K)
+        ctx.window = int(window)
+        return part
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        cum, tr, db, lengths, ps, pe, st, lv, ah, al, z2 = ctx.saved_tensors
+        g = grad_output.detach().to(torch.float32).contiguous()
+        det = lambda x: x.detach() if x is not None else None
+        g_cum, g_tr, g_db, g_ps, g_pe = ops.scan_backward_ck(
+            cum.detach(), tr.detach(), db.detach(), lengths, ctx.K, det(ps), det(pe), ctx.window, st, lv, ah, al,
+            z2, g,
+        )
+        return (
+            g_cum, g_tr, g_db, None, None,
+            g_ps if ps is not None else None,
+            g_pe if pe is not None else None,
+            None,
+        )
+
+
+def _checkpoint_window(cum, tr, K, ps, pe, memory_budget) -> Optional[int]:
+    """Window of the bounded-memory backward for ``memory_budget`` bytes, or None
+    when the problem has no such plan (duration-dependent transitions, C > 64,
+    K > 513): those keep the full tables."""
+    if tr.dim() != 2:
+        return None
+    B, Tp1, C = cum.shape
+    try:
+        w, nw, _, _ = ops.checkpoint_plan(B, Tp1 - 1, C, int(K), ps is not None, pe is not None,
+                                          int(memory_budget))
+    except NotImplementedError:
+        return None
+    return w if nw >= 2 else None
+
+
 def semi_crf_streaming_forward(
     cum_scores: torch.Tensor,
     transition: torch.Tensor,
@@ -186,6 +245,7 @@ def semi_crf_streaming_forward(
     proj_end: Optional[torch.Tensor] = None,
     use_triton: bool = True,
     use_compile: bool = False,
+    memory_budget: Optional[int] = None,
 ) -> torch.Tensor:
     r"""Semi-CRF log partition (``semiring="log"``) or Viterbi score (``"max"``), shape ``(B,)``.
 
@@ -193,6 +253,12 @@ def semi_crf_streaming_forward(
     (``streaming/autograd.py:270-431``); see the module docstring for the
     differences.  Edges are built on the fly from ``cum_scores`` with the
     destination-first convention ``edge[c_dst, c_src] = seg[c_dst] + transition[c_src, c_dst]``.
+
+    ``memory_budget`` (bytes; no reference counterpart): with gradients in the
+    log semiring, bound the backward's working memory by recomputing alpha window
+    by window (:class:`SemiCRFStreamingCheckpointedHIP`); ``0`` picks about
+    eight windows.  ``None`` (default) keeps the full O(T*C) tables, the fastest
+    backward.  Problems without a bounded plan keep the full tables.
     """
     if semiring not in SEMIRINGS:
         raise ValueError(f"semiring must be 'log' or 'max', got {semiring!r}")
@@ -203,7 +269,12 @@ def semi_crf_streaming_forward(
     needs_grad = torch.is_grad_enabled() and any(
         t is not None and t.requires_grad for t in (cum, tr, db, ps, pe)
     )
-    if needs_grad:
+    window = None
+    if needs_grad and semiring == "log" and memory_budget is not None:
+        window = _checkpoint_window(cum, tr, K, ps, pe, memory_budget)
+    if window is not None:
+        out = SemiCRFStreamingCheckpointedHIP.apply(cum, tr, db, lengths, int(K), ps, pe, window)
+    elif needs_grad:
         out = SemiCRFStreamingHIP.apply(cum, tr, db, lengths, int(K), semiring, ps, pe)
     elif semiring == "log":
         out = ops.scan_forward(cum, tr, db, lengths, int(K), SEMIRINGS["log"], ps, pe, False)[0]

@@ -465,6 +465,107 @@ def _(labels, lengths, grad_output, T, C, K, Kdb):
     return f(B, T, C), f(C, C), f(Kdb, C)
 
 
+# --------------------------------------------------------------------------- bounded-memory backward
+def checkpoint_plan(B: int, T: int, C: int, K: int, has_ps: bool, has_pe: bool,
+                    budget_bytes: int = 0) -> tuple[int, int, int, int]:
+    """(window, n_windows, forward workspace bytes, backward workspace bytes) of the
+    checkpointed forward / backward (``tsm_checkpoint_plan``); raises
+    NotImplementedError for problems without a 16-lane fused plan."""
+    lib = N.lib()
+    w, nw = ctypes.c_int64(0), ctypes.c_int64(0)
+    fw, bw = ctypes.c_size_t(0), ctypes.c_size_t(0)
+    N.check(lib.tsm_checkpoint_plan(B, T, C, K, int(has_ps), int(has_pe), int(budget_bytes), ctypes.byref(w),
+                                    ctypes.byref(nw), ctypes.byref(fw), ctypes.byref(bw)), "tsm_checkpoint_plan")
+    return int(w.value), int(nw.value), int(fw.value), int(bw.value)
+
+
+def _ck_workspace(B: int, T: int, C: int, K: int, has_ps: bool, has_pe: bool, window: int) -> tuple[int, int]:
+    lib = N.lib()
+    fw, bw = ctypes.c_size_t(0), ctypes.c_size_t(0)
+    N.check(lib.tsm_checkpointed_workspace(B, T, C, K, int(has_ps), int(has_pe), window, ctypes.byref(fw),
+                                           ctypes.byref(bw)), "tsm_checkpointed_workspace")
+    return int(fw.value), int(bw.value)
+
+
+@torch.library.custom_op("tsm_amd::scan_forward_ck", mutates_args=())
+def scan_forward_ck(
+    cum: Tensor, transition: Tensor, duration_bias: Tensor, lengths: Tensor, K: int,
+    proj_start: Optional[Tensor], proj_end: Optional[Tensor], window: int, n_windows: int,
+) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """Log partition (B,), log2 partition (B,) fp64 and the window checkpoints
+    (state (B,nw,Kmax,C), levels (B,nw,Kmax), alpha-hat rows (B,nw,C), their levels (B,nw))."""
+    lib = N.lib()
+    B, Tp1, C = cum.shape
+    T = Tp1 - 1
+    dev = cum.device
+    Kmax = max(K - 1, 1)
+    part = torch.empty(B, device=dev, dtype=torch.float32)
+    z2 = torch.empty(B, device=dev, dtype=torch.float64)
+    ck_st = torch.empty(B, n_windows, Kmax, C, device=dev, dtype=torch.float32)
+    ck_lv = torch.empty(B, n_windows, Kmax, device=dev, dtype=torch.float64)
+    ck_ah = torch.empty(B, n_windows, C, device=dev, dtype=torch.float32)
+    ck_al = torch.empty(B, n_windows, device=dev, dtype=torch.float64)
+    fw, _ = _ck_workspace(B, T, C, K, proj_start is not None, proj_end is not None, window)
+    ws = _workspace(fw, dev)
+    with torch.cuda.device(dev):
+        rc = lib.tsm_forward_checkpointed(
+            N.ptr(cum), N.ptr(transition), N.ptr(duration_bias), N.ptr(lengths), N.ptr(proj_start), N.ptr(proj_end),
+            B, T, C, K, window, N.ptr(part), N.ptr(z2), N.ptr(ck_st), N.ptr(ck_lv), N.ptr(ck_ah), N.ptr(ck_al),
+            N.ptr(ws), ws.numel(), _stream(dev),
+        )
+    N.check(rc, "tsm_forward_checkpointed")
+    return part, z2, ck_st, ck_lv, ck_ah, ck_al
+
+
+@scan_forward_ck.register_fake
+def _(cum, transition, duration_bias, lengths, K, proj_start, proj_end, window, n_windows):
+    B, Tp1, C = cum.shape
+    Kmax = max(K - 1, 1)
+    f = cum.new_empty
+    return (f(B), f(B, dtype=torch.float64), f(B, n_windows, Kmax, C), f(B, n_windows, Kmax, dtype=torch.float64),
+            f(B, n_windows, C), f(B, n_windows, dtype=torch.float64))
+
+
+@torch.library.custom_op("tsm_amd::scan_backward_ck", mutates_args=())
+def scan_backward_ck(
+    cum: Tensor, transition: Tensor, duration_bias: Tensor, lengths: Tensor, K: int,
+    proj_start: Optional[Tensor], proj_end: Optional[Tensor], window: int, ck_state: Tensor, ck_level: Tensor,
+    ck_alpha: Tensor, ck_alpha_level: Tensor, log2_partition: Tensor, grad_output: Tensor,
+) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """As :func:`scan_backward` (log semiring), recomputing alpha window by window
+    from the checkpoints of :func:`scan_forward_ck`."""
+    lib = N.lib()
+    B, Tp1, C = cum.shape
+    T = Tp1 - 1
+    dev = cum.device
+    g_cum = torch.empty(B, Tp1, C, device=dev, dtype=torch.float32)
+    g_tr = torch.empty(C, C, device=dev, dtype=torch.float32)
+    g_db = torch.empty(K, C, device=dev, dtype=torch.float32)
+    g_ps = torch.empty(B, T, C, device=dev, dtype=torch.float32) if proj_start is not None else None
+    g_pe = torch.empty(B, T, C, device=dev, dtype=torch.float32) if proj_end is not None else None
+    _, bw = _ck_workspace(B, T, C, K, proj_start is not None, proj_end is not None, window)
+    ws = _workspace(bw, dev)
+    with torch.cuda.device(dev):
+        rc = lib.tsm_backward_checkpointed(
+            N.ptr(cum), N.ptr(transition), N.ptr(duration_bias), N.ptr(lengths), N.ptr(proj_start), N.ptr(proj_end),
+            B, T, C, K, window, N.ptr(ck_state), N.ptr(ck_level), N.ptr(ck_alpha), N.ptr(ck_alpha_level),
+            N.ptr(log2_partition), N.ptr(grad_output), N.ptr(g_cum), N.ptr(g_tr), N.ptr(g_db), N.ptr(g_ps),
+            N.ptr(g_pe), N.ptr(ws), ws.numel(), _stream(dev),
+        )
+    N.check(rc, "tsm_backward_checkpointed")
+    empty = torch.empty(0, device=dev, dtype=torch.float32)
+    return g_cum, g_tr, g_db, g_ps if g_ps is not None else empty, g_pe if g_pe is not None else empty.clone()
+
+
+@scan_backward_ck.register_fake
+def _(cum, transition, duration_bias, lengths, K, proj_start, proj_end, window, ck_state, ck_level, ck_alpha,
+      ck_alpha_level, log2_partition, grad_output):
+    B, Tp1, C = cum.shape
+    g_ps = cum.new_empty(B, Tp1 - 1, C) if proj_start is not None else cum.new_empty(0)
+    g_pe = cum.new_empty(B, Tp1 - 1, C) if proj_end is not None else cum.new_empty(0)
+    return cum.new_empty(B, Tp1, C), cum.new_empty(C, C), cum.new_empty(K, C), g_ps, g_pe
+
+
 # --------------------------------------------------------------------------- checkpoints
 @torch.library.custom_op("tsm_amd::ring_checkpoints", mutates_args=())
 def ring_checkpoints(alpha_hat: Tensor, alpha_level: Tensor, lengths: Tensor, K: int, interval: int,
