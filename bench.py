@@ -407,6 +407,9 @@ def main():
                     help="skip the per-pass timings (forward only, Viterbi), e.g. under a profiler")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 256 MiB device copy (PMC counter calibration)")
+    ap.add_argument("--memory-budget", type=int, default=None,
+                    help="time the bounded-memory backward (checkpointed windows) for this budget in "
+                         "bytes (0: about eight windows) instead of the full-table backward")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -442,7 +445,7 @@ def main():
         if record:
             e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
             e0.record()
-        part = tsa.semi_crf_streaming_forward(cum, tr, db, L, K)
+        part = tsa.semi_crf_streaming_forward(cum, tr, db, L, K, memory_budget=args.memory_budget)
         if record:
             e1.record()
         part.sum().backward()
@@ -545,6 +548,7 @@ def main():
             "avg_launch_ms": dom_avg_ms,
         },
         "max_memory_allocated_bytes": peak_mem,
+        "memory_budget": args.memory_budget,
         "nominal_roofline_frac_fwdbwd": value / roofline_cells_per_s("fwdbwd_log"),
         "passes": passes,
         "fwd_ms": fwd_ms,
@@ -553,6 +557,11 @@ def main():
         "plan": plan,
         "logZ": float(part.detach()[0]),
     }
+    if args.memory_budget is not None:
+        from torch_semimarkov_amd.streaming import ops as tops
+        w, nw, fw, bw = tops.checkpoint_plan(B, T, C, K, False, False, args.memory_budget)
+        out["bounded"] = {"window": w, "n_windows": nw, "forward_workspace_bytes": fw,
+                          "backward_workspace_bytes": bw}
     if not args.no_cpu and args.cpu_sample > 0:
         out["cpu_baseline"] = cpu_baseline(args.config, cum_h, tr_h, db_h, K, min(args.cpu_sample, T))
         out["speedup_vs_cpu"] = value / out["cpu_baseline"]["value"]

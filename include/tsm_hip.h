@@ -312,14 +312,16 @@ int tsm_gold_score_emissions_backward(const int64_t* labels, const int64_t* leng
  * Static (C, C) transitions, cumulative-score input, plans with the 16-lane
  * register-resident scans and fused marginals (C <= 64, K <= 513); other
  * problems get TSM_ERR_UNSUPPORTED.
- *   tsm_checkpoint_plan   the window (a multiple of the chunk length) whose
- *                         backward workspace fits budget_bytes (0: about eight
- *                         windows), the window count nw = ceil(T / window),
- *                         and the two workspace sizes
+ *   tsm_checkpoint_plan   the longest window (a multiple of the chunk length)
+ *                         whose backward workspace fits budget_bytes (0: about
+ *                         eight windows; one chunk when nothing fits), the
+ *                         window count nw = ceil(T / window), and the two
+ *                         workspace sizes.  Every sequence's window w runs in
+ *                         the same launches; the workspace grows with B.
  *   tsm_checkpointed_workspace  the two workspace sizes for a given window
  *   tsm_forward_checkpointed  partition / log2_partition as tsm_forward, and
- *                         ck_state (B, nw, Kmax, C) f32, ck_level (B, nw, Kmax)
- *                         f64, ck_alpha (B, nw, C) f32, ck_alpha_level (B, nw)
+ *                         ck_state (nw, B, Kmax, C) f32, ck_level (nw, B, Kmax)
+ *                         f64, ck_alpha (nw, B, C) f32, ck_alpha_level (nw, B)
  *                         f64 (Kmax = max(K-1, 1); entries of window 0 unused)
  *   tsm_backward_checkpointed  the gradients of tsm_backward (same outputs,
  *                         fully written) from the inputs and the checkpoints

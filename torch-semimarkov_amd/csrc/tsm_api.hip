@@ -1655,10 +1655,10 @@ struct WinWs {
 
 WinWs carve_window(Carver& cv, const Plan& pw) {
   WinWs w;
-  w.ah = cv.take<float>((size_t)(pw.T + 1) * pw.C);
-  w.al = cv.take<double>((size_t)pw.T + 1);
-  w.z2 = cv.take<double>(1);
-  w.zout = cv.take<float>(1);
+  w.ah = cv.take<float>((size_t)pw.B * (pw.T + 1) * pw.C);
+  w.al = cv.take<double>((size_t)pw.B * (pw.T + 1));
+  w.z2 = cv.take<double>((size_t)pw.B);
+  w.zout = cv.take<float>((size_t)pw.B);
   w.fs = carve_scan(cv, pw, false);
   w.bw = carve_backward(cv, pw);
   return w;
@@ -1682,13 +1682,13 @@ struct CkFixed {
 CkFixed carve_ck_fixed(Carver& cv, const CkGeom& g) {
   CkFixed f;
   const size_t n = (size_t)g.full.B * g.nw;
-  const size_t KC = (size_t)g.full.Kmax * g.full.C;
+  const size_t KC = (size_t)g.full.B * g.full.Kmax * g.full.C;
   f.lenw = cv.take<int64_t>(n);
   f.okf = cv.take<int>(n);
   f.okb = cv.take<int>(n);
   for (int i = 0; i < 2; ++i) {
     f.st[i] = cv.take<float>(KC);
-    f.lv[i] = cv.take<double>(g.full.Kmax);
+    f.lv[i] = cv.take<double>((size_t)g.full.B * g.full.Kmax);
   }
   f.thalo = cv.take<float>(KC);
   return f;
@@ -1705,11 +1705,11 @@ size_t ck_backward_bytes(const CkGeom& g) {
 }
 
 int ck_window_plans(CkGeom& g, int has_ps, int has_pe) {
-  const int64_t T = g.full.T;
-  int rc = ck_plan(1, std::min<int64_t>(g.Wlen, T), g.full.C, g.full.K, has_ps, has_pe, &g.win);
+  const int64_t T = g.full.T, B = g.full.B;
+  int rc = ck_plan(B, std::min<int64_t>(g.Wlen, T), g.full.C, g.full.K, has_ps, has_pe, &g.win);
   if (rc) return rc;
   const int64_t last = T - (int64_t)(g.nw - 1) * g.Wlen;
-  return ck_plan(1, last, g.full.C, g.full.K, has_ps, has_pe, &g.last);
+  return ck_plan(B, last, g.full.C, g.full.K, has_ps, has_pe, &g.last);
 }
 
 int ck_geometry(int64_t B, int64_t T, int64_t C, int64_t K, int has_ps, int has_pe, int64_t window, CkGeom* g) {
@@ -1798,6 +1798,8 @@ int tsm_forward_checkpointed(const float* cum, const float* tr, const float* db,
   ScanWs w = carve_scan(cv, g.full, false);
   tsm::ScanParams p = scan_params(g.full, w, cum, tr, db, len, ps, pe);
   p.win = 1;
+  p.xseq = (T + 1) * C;
+  p.pseq = T * C;
   p.val = nullptr;
   p.lvl = nullptr;
   if (log2_partition) p.z2 = log2_partition;
@@ -1848,106 +1850,112 @@ int tsm_backward_checkpointed(const float* cum, const float* tr, const float* db
   char* region = static_cast<char*>(workspace) + ((cv.off + 255) & ~size_t(255));
   e = tsm::launch_window_setup(len, (int)B, (int)T, g.Wlen, g.nw, fx.lenw, fx.okf, fx.okb, st);
   if (e != hipSuccess) return hip_fail(e, "tsm_backward_checkpointed (windows)");
-  for (int64_t b = 0; b < B; ++b) {
-    int cur = 0;
-    for (int w = g.nw - 1; w >= 0; --w) {
-      const Plan& pw = (w == g.nw - 1) ? g.last : g.win;
-      const int64_t a = (int64_t)w * g.Wlen, Tw = pw.T;
-      const size_t o = (size_t)b * g.nw + w;
-      Carver wc(region);
-      const WinWs ww = carve_window(wc, pw);
-      const float* cum_w = cum + ((size_t)b * (T + 1) + a) * C;
-      const float* ps_w = ps ? ps + ((size_t)b * T + a) * C : nullptr;
-      const float* pe_w = pe ? pe + ((size_t)b * T + a) * C : nullptr;
-      // alpha over the window, from the forward's checkpoint at its start
-      e = tsm::launch_window_row0(ck_alpha, ck_alpha_level, fx.okf, o, (int)C, ww.ah, ww.al, st);
-      if (e != hipSuccess) return hip_fail(e, "tsm_backward_checkpointed (window start)");
-      tsm::ScanParams p = scan_params(pw, ww.fs, cum_w, tr, db, fx.lenw + o, ps_w, pe_w);
-      p.win = 1;
-      p.org_st = ck_state + o * KC;
-      p.org_lv = ck_level + o * Kmax;
-      p.org_ok = fx.okf + o;
-      p.val = ww.ah;
-      p.lvl = ww.al;
-      p.z2 = ww.z2;
-      p.zout = ww.zout;
-      e = tsm::launch_scan_forward(pw, p, TSM_SEMIRING_LOG, st);
-      if (e != hipSuccess) return hip_fail(e, "tsm_backward_checkpointed (window forward)");
-      // the fused backward over the window, from the state the window above recorded
-      const BwdWs& bw = ww.bw;
-      tsm::FusedParams f{};
-      f.lengths = fx.lenw + o;
-      f.trans = tr;
-      f.aval = ww.ah;
-      f.uval = bw.uval;
-      f.B = 1;
-      f.T = (int)Tw;
-      f.C = (int)C;
-      f.K = pw.K;
-      f.Kmax = Kmax;
-      f.P = pw.P;
-      f.Lc = pw.Lc;
-      f.GNB = pw.GNB;
-      f.GTB = pw.GTB;
-      f.offs = bw.scan.offs;
-      f.mframe = bw.mframe;
-      f.cum = cum_w;
-      f.db = db;
-      f.ps = ps_w;
-      f.alvl = ww.al;
-      f.z2 = log2_partition + b;
-      f.st_end = bw.scan.st_end;
-      f.lv_end = bw.scan.lv_end;
-      f.e_own = bw.e_own;
-      f.s_out = bw.s_out;
-      f.halo = bw.halo;
-      f.db_part = bw.db_part;
-      f.tr_part = bw.tr_part;
-      f.grad_output = grad_output + b;
-      f.grad_cum = grad_cum + ((size_t)b * (T + 1) + a) * C;
-      f.grad_ps = grad_ps ? grad_ps + ((size_t)b * T + a) * C : nullptr;
-      f.grad_pe = grad_pe ? grad_pe + ((size_t)b * T + a) * C : nullptr;
-      f.grad_tr = grad_tr;
-      f.grad_db = grad_db;
-      f.accum = 1;
-      f.org_ok = fx.okf + o;
-      f.end_ok = fx.okb + o;
-      e = tsm::launch_u_rows(pw, f, st);
-      if (e != hipSuccess) return hip_fail(e, "tsm_backward_checkpointed (u rows)");
-      tsm::ScanParams q = scan_params(pw, bw.scan, cum_w, tr, db, fx.lenw + o, ps_w, pe_w);
-      q.win = 1;
-      q.org_st = fx.st[cur];
-      q.org_lv = fx.lv[cur];
-      q.org_ok = fx.okb + o;
-      q.thalo = fx.thalo;
-      // (no window below window 0: nothing to record, and no row before its position 0)
-      q.tst_st = w >= 1 ? fx.st[1 - cur] : nullptr;
-      q.tst_lv = w >= 1 ? fx.lv[1 - cur] : nullptr;
-      q.val = nullptr;
-      q.lvl = nullptr;
-      q.zout = nullptr;
-      q.uval = bw.uval;
-      q.aval = ww.ah;
-      q.alvl = ww.al;
-      q.mz2 = log2_partition + b;
-      q.e_own = bw.e_own;
-      q.s_out = bw.s_out;
-      q.halo = bw.halo;
-      q.db_part = bw.db_part;
-      q.mframe = bw.mframe;
-      e = tsm::launch_scan_backward_fused(pw, q, st);
-      if (e != hipSuccess) return hip_fail(e, "tsm_backward_checkpointed (window beta scan)");
-      e = tsm::launch_fused_finalize(pw, f, st);
-      if (e != hipSuccess) return hip_fail(e, "tsm_backward_checkpointed (window finalize)");
-      e = tsm::launch_window_state_fix(fx.lv[1 - cur], bw.scan.offs, Kmax, st);
-      if (e == hipSuccess)
-        e = tsm::launch_window_halo_add(fx.thalo, bw.halo, bw.mframe, fx.lenw, fx.okb, o, pw.Lc, Kmax, (int)C,
-                                        (int)(T - (a + Tw)), grad_output + b,
-                                        grad_cum + ((size_t)b * (T + 1) + a + Tw) * C,
-                                        grad_pe ? grad_pe + ((size_t)b * T + a + Tw) * C : nullptr, st);
-      if (e != hipSuccess) return hip_fail(e, "tsm_backward_checkpointed (window edges)");
-      cur = 1 - cur;
-    }
+  const int64_t xseq = (T + 1) * C, pseq = T * C;
+  int cur = 0;
+  for (int w = g.nw - 1; w >= 0; --w) {
+    // window w of every sequence: rows a .. a + Tw
+    const Plan& pw = (w == g.nw - 1) ? g.last : g.win;
+    const int64_t a = (int64_t)w * g.Wlen, Tw = pw.T;
+    const size_t o = (size_t)w * B;  // the window's (B,) slice of lengths and flags
+    Carver wc(region);
+    const WinWs ww = carve_window(wc, pw);
+    const float* cum_w = cum + a * C;
+    const float* ps_w = ps ? ps + a * C : nullptr;
+    const float* pe_w = pe ? pe + a * C : nullptr;
+    // alpha over the window, from the forward's checkpoints at its start
+    e = tsm::launch_window_row0(ck_alpha + o * C, ck_alpha_level + o, fx.okf + o, (int)B, (int)Tw, (int)C, ww.ah,
+                                ww.al, st);
+    if (e != hipSuccess) return hip_fail(e, "tsm_backward_checkpointed (window start)");
+    tsm::ScanParams p = scan_params(pw, ww.fs, cum_w, tr, db, fx.lenw + o, ps_w, pe_w);
+    p.win = 1;
+    p.xseq = xseq;
+    p.pseq = pseq;
+    p.org_st = ck_state + o * KC;
+    p.org_lv = ck_level + o * Kmax;
+    p.org_ok = fx.okf + o;
+    p.val = ww.ah;
+    p.lvl = ww.al;
+    p.z2 = ww.z2;
+    p.zout = ww.zout;
+    e = tsm::launch_scan_forward(pw, p, TSM_SEMIRING_LOG, st);
+    if (e != hipSuccess) return hip_fail(e, "tsm_backward_checkpointed (window forward)");
+    // the fused backward over the window, from the states the window above recorded
+    const BwdWs& bw = ww.bw;
+    tsm::FusedParams f{};
+    f.lengths = fx.lenw + o;
+    f.trans = tr;
+    f.aval = ww.ah;
+    f.uval = bw.uval;
+    f.B = (int)B;
+    f.T = (int)Tw;
+    f.C = (int)C;
+    f.K = pw.K;
+    f.Kmax = Kmax;
+    f.P = pw.P;
+    f.Lc = pw.Lc;
+    f.GNB = pw.GNB;
+    f.GTB = pw.GTB;
+    f.offs = bw.scan.offs;
+    f.mframe = bw.mframe;
+    f.cum = cum_w;
+    f.db = db;
+    f.ps = ps_w;
+    f.alvl = ww.al;
+    f.z2 = log2_partition;
+    f.st_end = bw.scan.st_end;
+    f.lv_end = bw.scan.lv_end;
+    f.e_own = bw.e_own;
+    f.s_out = bw.s_out;
+    f.halo = bw.halo;
+    f.db_part = bw.db_part;
+    f.tr_part = bw.tr_part;
+    f.grad_output = grad_output;
+    f.grad_cum = grad_cum + a * C;
+    f.grad_ps = grad_ps ? grad_ps + a * C : nullptr;
+    f.grad_pe = grad_pe ? grad_pe + a * C : nullptr;
+    f.grad_tr = grad_tr;
+    f.grad_db = grad_db;
+    f.accum = 1;
+    f.org_ok = fx.okf + o;
+    f.end_ok = fx.okb + o;
+    f.xseq = xseq;
+    f.pseq = pseq;
+    e = tsm::launch_u_rows(pw, f, st);
+    if (e != hipSuccess) return hip_fail(e, "tsm_backward_checkpointed (u rows)");
+    tsm::ScanParams q = scan_params(pw, bw.scan, cum_w, tr, db, fx.lenw + o, ps_w, pe_w);
+    q.win = 1;
+    q.xseq = xseq;
+    q.pseq = pseq;
+    q.org_st = fx.st[cur];
+    q.org_lv = fx.lv[cur];
+    q.org_ok = fx.okb + o;
+    q.thalo = fx.thalo;
+    // (no window below window 0: nothing to record, and no row before its position 0)
+    q.tst_st = w >= 1 ? fx.st[1 - cur] : nullptr;
+    q.tst_lv = w >= 1 ? fx.lv[1 - cur] : nullptr;
+    q.val = nullptr;
+    q.lvl = nullptr;
+    q.zout = nullptr;
+    q.uval = bw.uval;
+    q.aval = ww.ah;
+    q.alvl = ww.al;
+    q.mz2 = log2_partition;
+    q.e_own = bw.e_own;
+    q.s_out = bw.s_out;
+    q.halo = bw.halo;
+    q.db_part = bw.db_part;
+    q.mframe = bw.mframe;
+    e = tsm::launch_scan_backward_fused(pw, q, st);
+    if (e != hipSuccess) return hip_fail(e, "tsm_backward_checkpointed (window beta scan)");
+    e = tsm::launch_fused_finalize(pw, f, st);
+    if (e != hipSuccess) return hip_fail(e, "tsm_backward_checkpointed (window finalize)");
+    if (w >= 1) e = tsm::launch_window_state_fix(fx.lv[1 - cur], bw.scan.offs, (int)B, pw.P, Kmax, st);
+    if (e == hipSuccess)
+      e = tsm::launch_window_halo_add(fx.thalo, bw.halo, bw.mframe, fx.lenw + o, fx.okb + o, (int)B, pw.P, pw.Lc, Kmax,
+                                      (int)C, (int)(T - (a + Tw)), grad_output, grad_cum + (a + Tw) * C,
+                                      grad_pe ? grad_pe + (a + Tw) * C : nullptr, xseq, pseq, st);
+    if (e != hipSuccess) return hip_fail(e, "tsm_backward_checkpointed (window edges)");
+    cur = 1 - cur;
   }
   return TSM_OK;
 }

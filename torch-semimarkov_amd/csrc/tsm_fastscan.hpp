@@ -151,11 +151,14 @@ struct Chunk {
         init_lv = p.org_lv + (size_t)b * Kmax;
       }
     }
-    const float* cum_b = p.cum + (size_t)b * (T + 1) * C;  // not read with emission input
+    // (a window's inputs are rows of the full tensors: their sequence strides)
+    const size_t xseq = WIN ? (size_t)p.xseq : (size_t)(T + 1) * C;
+    const size_t pseq = WIN ? (size_t)p.pseq : (size_t)T * C;
+    const float* cum_b = p.cum + (size_t)b * xseq;  // not read with emission input
     const float* em_b = emit ? p.emit + (size_t)b * T * C : nullptr;
     const bool has_ps = p.ps != nullptr, has_pe = p.pe != nullptr;
-    const float* ps_b = has_ps ? p.ps + (size_t)b * T * C : nullptr;
-    const float* pe_b = has_pe ? p.pe + (size_t)b * T * C : nullptr;
+    const float* ps_b = has_ps ? p.ps + (size_t)b * pseq : nullptr;
+    const float* pe_b = has_pe ? p.pe + (size_t)b * pseq : nullptr;
     const bool store = !MARG && p.val != nullptr;  // the fused backward keeps no beta table
     const double sgn = FWD ? 1.0 : -1.0;
     // fp64 cumulative score of position pos (own label) in log2 units, times sgn
@@ -465,8 +468,12 @@ struct Chunk {
               for (int i = lj; i < Kmax; i += J) {
                 const int pos = t_hi + i;
                 if (pos <= len) {
-                  const double pbv = (has_pe && pos >= 1) ? (double)(p.pe[((size_t)bo * T + pos - 1) * C + c] * kLog2e) : 0.0;
-                  const double cxv = -(double)p.cum[(row0 + pos) * C + c] * kLog2eD;
+                  const double pbv =
+                      (has_pe && pos >= 1)
+                          ? (double)((WIN ? pe_b[(size_t)(pos - 1) * C + c] : p.pe[((size_t)bo * T + pos - 1) * C + c]) *
+                                     kLog2e)
+                          : 0.0;
+                  const double cxv = -(double)(WIN ? cum_b[(size_t)pos * C + c] : p.cum[(row0 + pos) * C + c]) * kLog2eD;
                   const double lb = (rc[A + i] - pbv) + cxv;  // log2 beta(pos, c), chunk frame
                   const double la = (double)p.aval[(row0 + pos) * C + c] + p.alvl[row0 + pos];
                   m = fmax(m, la + lb);
@@ -708,7 +715,7 @@ struct Chunk {
               if constexpr (WIN) {
                 // checkpoint rows of the bounded-memory backward (levels in the chunk frame)
                 if (p.ck_ah != nullptr && owned && t % p.ck_every == 0 && t / p.ck_every < p.ck_n)
-                  p.ck_ah[((size_t)b * p.ck_n + t / p.ck_every) * C + ci] = ah;
+                  p.ck_ah[((size_t)(t / p.ck_every) * p.B + b) * C + ci] = ah;
               }
             }
           }
@@ -718,7 +725,7 @@ struct Chunk {
           if (t == len) p.fin_lvl[b] = lvl_t;
           if constexpr (WIN) {
             if (p.ck_ah != nullptr && owned && t % p.ck_every == 0 && t / p.ck_every < p.ck_n)
-              p.ck_al[(size_t)b * p.ck_n + t / p.ck_every] = lvl_t;
+              p.ck_al[(size_t)(t / p.ck_every) * p.B + b] = lvl_t;
           }
         }
       } else {

@@ -204,7 +204,7 @@ __global__ void __launch_bounds__(1024) coverage_kernel(FusedParams f) {
     const size_t item = (size_t)b * f.P + j;
     const float* st = f.st_end + item * Kmax * C;
     const bool emit = f.emit != nullptr;
-    const float* cum_b = emit ? nullptr : f.cum + (size_t)b * (T + 1) * C;
+    const float* cum_b = emit ? nullptr : f.cum + (size_t)b * (f.xseq ? (size_t)f.xseq : (size_t)(T + 1) * C);
     const float* em_b = emit ? f.emit + (size_t)b * T * C : nullptr;
     const float* cref = emit ? nullptr : cum_b + (size_t)t_ref * C;
     const int ni = min(Kmax, len - t_lo + 1);  // positions t_lo .. min(len, t_lo+Kmax-1)
@@ -245,7 +245,7 @@ __global__ void __launch_bounds__(1024) coverage_kernel(FusedParams f) {
       } else {
         a -= (cum_b[(size_t)s * C + c] - cref[c]) * kLog2e;
       }
-      if (f.ps != nullptr) a += f.ps[((size_t)b * T + s) * C + c] * kLog2e;
+      if (f.ps != nullptr) a += f.ps[(size_t)b * (f.pseq ? (size_t)f.pseq : (size_t)T * C) + (size_t)s * C + c] * kLog2e;
       const int k0 = t_ref - s + 1, k1 = min(Kmax, len - s);
       float sk0 = 0.0f, sk1 = 0.0f;
 #pragma unroll 4
@@ -304,10 +304,12 @@ __global__ void fused_rows_kernel(FusedParams f) {
       if (t < len) S = (float)(fj * (double)f.s_out[o]);
     }
     if (f.accum) {
-      // window of the bounded-memory backward: rows at its edges take parts from two windows
-      f.grad_cum[o] += g * (E - S);
-      if (f.grad_ps != nullptr && t < T) f.grad_ps[((size_t)b * T + t) * C + c] += g * S;
-      if (f.grad_pe != nullptr && t >= 1) f.grad_pe[((size_t)b * T + t - 1) * C + c] += g * E;
+      // window of the bounded-memory backward: rows of the full tensors (their
+      // strides); rows at the window's edges take parts from two windows
+      const size_t xo = (size_t)b * f.xseq + (size_t)t * C + c, po = (size_t)b * f.pseq + (size_t)t * C + c;
+      f.grad_cum[xo] += g * (E - S);
+      if (f.grad_ps != nullptr && t < T) f.grad_ps[po] += g * S;
+      if (f.grad_pe != nullptr && t >= 1) f.grad_pe[po - C] += g * E;
       continue;
     }
     if (!f.shift) f.grad_cum[o] = g * (E - S);

@@ -74,13 +74,15 @@ struct ScanParams {
   // emission input: (B, T, C) projected scores in place of cum (register-resident scans), or null
   const float* emit;
   // bounded-memory backward (win = 1: the problem is one window of longer
-  // sequences; 16-lane log-semiring instances).  Chunks that would start exactly
-  // from the sequence start / end start from org_st / org_lv (B, Kmax, C) /
-  // (B, Kmax), ring format, global levels, where org_ok[b]; the forward records
-  // alpha-hat rows t % ck_every == 0 in ck_ah (B, ck_n, C) / ck_al (B, ck_n);
-  // the fused backward's top chunk writes the end sums of positions len+1 ..
-  // len+Kmax-1 to thalo (B, Kmax, C), its chunk 0 its state at position 0 to
-  // tst_st / tst_lv (chunk frame).
+  // sequences; 16-lane log-semiring instances).  cum / ps / pe point at the
+  // window's first row of sequence 0 and sequence b's rows start xseq / pseq
+  // elements further (the full tensors' strides).  Chunks that would start
+  // exactly from the sequence start / end start from org_st / org_lv (B, Kmax,
+  // C) / (B, Kmax), ring format, global levels, where org_ok[b]; the forward
+  // records alpha-hat rows t % ck_every == 0 in ck_ah (ck_n, B, C) / ck_al
+  // (ck_n, B); the fused backward's top chunk writes the end sums of positions
+  // len+1 .. len+Kmax-1 to thalo (B, Kmax, C), its chunk 0 its state at
+  // position 0 to tst_st / tst_lv (chunk frame).
   int win;
   const float* org_st;
   const double* org_lv;
@@ -91,6 +93,7 @@ struct ScanParams {
   float* thalo;
   float* tst_st;
   double* tst_lv;
+  int64_t xseq, pseq;
 };
 
 struct MargParams {
@@ -172,13 +175,17 @@ struct FusedParams {
   float* grad_db;
   int shift;               // 1: grad_cum is (B, T, C) and row t >= 1 goes to row t-1 (row 0 is dropped)
   // bounded-memory backward: add the window's rows and shared gradients into the
-  // outputs (accum); chunk 0 of a sequence with a handed-over start state
-  // (org_ok[b]) keeps its frame factor (position 0 is not the sequence start),
-  // and so does a chunk whose coverage segments may end beyond the window when
-  // the sequence goes on (end_ok[b])
+  // outputs (accum); cum / ps and the row outputs point at the window's first
+  // row of sequence 0, sequence b's rows xseq (cum, grad_cum) / pseq (ps and
+  // the projection gradients) elements further (0: the window's own T).
+  // Chunk 0 of a sequence with a handed-over start state (org_ok[b]) keeps its
+  // frame factor (position 0 is not the sequence start), and so does a chunk
+  // whose coverage segments may end beyond the window when the sequence goes
+  // on (end_ok[b])
   int accum;
   const int* org_ok;
   const int* end_ok;
+  int64_t xseq, pseq;
 };
 
 struct ViterbiParams {
@@ -312,12 +319,12 @@ int launch_window_setup(const int64_t* lengths, int B, int T, int Wlen, int nw, 
                         hipStream_t s);
 int launch_ck_extract(const float* st_end, const double* lv_end, const double* offs, int B, int P, int Wc, int Kmax,
                       int C, int nw, float* ck_st, double* ck_lv, double* ck_al, hipStream_t s);
-int launch_window_row0(const float* ck_ah, const double* ck_al, const int* okf, size_t o, int C, float* ah,
+int launch_window_row0(const float* ck_ah, const double* ck_al, const int* okf, int B, int Tw, int C, float* ah,
                        double* al, hipStream_t s);
-int launch_window_state_fix(double* lv, const double* offs, int Kmax, hipStream_t s);
+int launch_window_state_fix(double* lv, const double* offs, int B, int P, int Kmax, hipStream_t s);
 int launch_window_halo_add(const float* thalo, const float* halo, const double* mframe, const int64_t* lenw,
-                           const int* okb, size_t o, int Lc, int Kmax, int C, int rows, const float* gout, float* gcum_e,
-                           float* gpe_e, hipStream_t s);
+                           const int* okb, int B, int P, int Lc, int Kmax, int C, int rows, const float* gout,
+                           float* gcum_e, float* gpe_e, int64_t xseq, int64_t pseq, hipStream_t s);
 int launch_fill_zero(float* p, size_t n, hipStream_t s);
 
 // Opt-in per-kernel timing.  Kernel ids index the totals of timing_read().

@@ -493,7 +493,7 @@ def scan_forward_ck(
     proj_start: Optional[Tensor], proj_end: Optional[Tensor], window: int, n_windows: int,
 ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
     """Log partition (B,), log2 partition (B,) fp64 and the window checkpoints
-    (state (B,nw,Kmax,C), levels (B,nw,Kmax), alpha-hat rows (B,nw,C), their levels (B,nw))."""
+    (state (nw,B,Kmax,C), levels (nw,B,Kmax), alpha-hat rows (nw,B,C), their levels (nw,B))."""
     lib = N.lib()
     B, Tp1, C = cum.shape
     T = Tp1 - 1
@@ -501,10 +501,10 @@ def scan_forward_ck(
     Kmax = max(K - 1, 1)
     part = torch.empty(B, device=dev, dtype=torch.float32)
     z2 = torch.empty(B, device=dev, dtype=torch.float64)
-    ck_st = torch.empty(B, n_windows, Kmax, C, device=dev, dtype=torch.float32)
-    ck_lv = torch.empty(B, n_windows, Kmax, device=dev, dtype=torch.float64)
-    ck_ah = torch.empty(B, n_windows, C, device=dev, dtype=torch.float32)
-    ck_al = torch.empty(B, n_windows, device=dev, dtype=torch.float64)
+    ck_st = torch.empty(n_windows, B, Kmax, C, device=dev, dtype=torch.float32)
+    ck_lv = torch.empty(n_windows, B, Kmax, device=dev, dtype=torch.float64)
+    ck_ah = torch.empty(n_windows, B, C, device=dev, dtype=torch.float32)
+    ck_al = torch.empty(n_windows, B, device=dev, dtype=torch.float64)
     fw, _ = _ck_workspace(B, T, C, K, proj_start is not None, proj_end is not None, window)
     ws = _workspace(fw, dev)
     with torch.cuda.device(dev):
@@ -522,8 +522,8 @@ def _(cum, transition, duration_bias, lengths, K, proj_start, proj_end, window, 
     B, Tp1, C = cum.shape
     Kmax = max(K - 1, 1)
     f = cum.new_empty
-    return (f(B), f(B, dtype=torch.float64), f(B, n_windows, Kmax, C), f(B, n_windows, Kmax, dtype=torch.float64),
-            f(B, n_windows, C), f(B, n_windows, dtype=torch.float64))
+    return (f(B), f(B, dtype=torch.float64), f(n_windows, B, Kmax, C), f(n_windows, B, Kmax, dtype=torch.float64),
+            f(n_windows, B, C), f(n_windows, B, dtype=torch.float64))
 
 
 @torch.library.custom_op("tsm_amd::scan_backward_ck", mutates_args=())
