@@ -368,8 +368,9 @@ def measure_passes(args, cum, tr, db, L, K, cells, fwdbwd_ms, plan):
     partition only), forward + backward (the timed step) and Viterbi with
     backtrace (max semiring), each as nominal cells/s and as a fraction of that
     pass's roofline (ops per cell fixed in OPS).  Viterbi is timed only where
-    the register-resident plan exists (plan["fast"]); otherwise the exact
-    kernel would run K*C^2 terms per step on one workgroup per sequence."""
+    the register-resident or the cooperative plan exists (the factorised
+    max-plus scan); otherwise the exact kernel would run K*C^2 terms per step
+    on one workgroup per sequence."""
     from torch_semimarkov_amd.streaming import ops
 
     def timed(fn):
@@ -384,7 +385,8 @@ def measure_passes(args, cum, tr, db, L, K, cells, fwdbwd_ms, plan):
 
     with torch.no_grad():
         fwd = timed(lambda: ops.scan_forward(cum, tr, db, L, K, 0, None, None, False))
-        vit = timed(lambda: ops.viterbi(cum, tr, db, L, K, None, None, True)) if plan.get("fast") else None
+        vit = (timed(lambda: ops.viterbi(cum, tr, db, L, K, None, None, True))
+               if (plan.get("fast") or plan.get("coop")) else None)
 
     def entry(ms, kind):
         rate = cells / (ms / 1e3)

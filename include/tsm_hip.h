@@ -177,10 +177,14 @@ int tsm_backward(const float* cum_scores, const float* transition, const float* 
  *                           with verification like the log-semiring scan:
  *                           scores within 1e-5 relative, segmentations identical
  *                           when no two candidates tie;
- *   TSM_VITERBI_AUTO        factorised when the register-resident scan fits
- *                           and the problem has >= 2^28 cells (B*T*K*C^2) or
- *                           its plan cuts each sequence into several chunks
- *                           (tsm_plan_info P >= 2); exact otherwise.
+ *   TSM_VITERBI_AUTO        factorised when the register-resident scan or the
+ *                           cooperative scan (C <= 128, K <= 513; tsm_plan_info
+ *                           coop = 1) fits and the problem has >= 2^28 cells
+ *                           (B*T*K*C^2) or its plan cuts each sequence into
+ *                           several chunks (tsm_plan_info P >= 2); exact
+ *                           otherwise.  The exact kernel holds one sequence's
+ *                           ring in LDS: C = 128 with K = 500 only runs
+ *                           factorised.
  * Duration-dependent transitions (trans_rows > 0) always run the exact kernel
  * (the factorisation does not hold; TSM_VITERBI_FACTORISED is refused).
  * Ties: the smallest duration, then the first source label, then the first

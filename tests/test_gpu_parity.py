@@ -356,6 +356,85 @@ def test_coop_scan_recomputes_non_mixing_chunks():
     assert_grads(grads, g64)
 
 
+COOP_MAX_CASES = [
+    (2, 300, 40, 128, [300, 177], False),
+    (3, 200, 9, 80, [200, 150, 7], True),
+    (1, 300, 200, 96, None, False),
+]
+
+
+@pytest.mark.parametrize("B,T,K,C,lengths,proj", COOP_MAX_CASES)
+def test_coop_max_semiring_vs_fp64_oracle(B, T, K, C, lengths, proj):
+    """The max-plus cooperative scan (forward and beta) under the max semiring's
+    gradients (soft max-marginals) against the fp64 oracle."""
+    assert N.plan_info(B, T, C, K, proj, proj)["coop"] == 1
+    cum, tr, db, L, ps, pe = rand_problem(B, T, K, C, 4500 + T + K + C, lengths, proj)
+    g = torch.linspace(0.5, 2.0, B)
+    p64, g64 = oracle_fp64(cum, tr, db, L, K, "max", ps, pe, g)
+    part, grads = run_hip(cum, tr, db, L, K, "max", ps, pe, g)
+    live = L > 0
+    np.testing.assert_allclose(part[live].double().numpy(), p64[live].numpy(), rtol=RTOL_Z, atol=1e-6)
+    assert_grads(grads, g64)
+
+
+@pytest.mark.parametrize("proj", [False, True])
+def test_coop_factorised_viterbi_vs_fp64_optimum(proj):
+    """C = 96 (cooperative plan, several chunks per sequence): AUTO takes the
+    factorised max-plus cooperative scan; its score is within 1e-5 of the fp64
+    optimum and its segments are the optimum's on gap-separated inputs (a
+    self-transition penalty removes runs of one label cut into segments)."""
+    from oracle import cref
+
+    B, T, K, C = 2, 6000, 12, 96
+    info = N.plan_info(B, T, C, K, proj, proj)
+    assert info["coop"] == 1 and info["P"] >= 2, info
+    cum, tr, db, L, ps, pe = rand_problem(B, T, K, C, 4700, [6000, 4333], proj, tscale=0.5, dscale=0.5)
+    tr = tr - 30.0 * torch.eye(C)
+    args = [cum.to(DEV), tr.to(DEV), db.to(DEV), L.to(DEV), K] + to_dev(ps, pe)
+    score, cnt, segs = ops.viterbi(*args, True, N.TSM_VITERBI_AUTO)
+    f_score, _, _ = ops.viterbi(*args, True, N.TSM_VITERBI_FACTORISED)
+    assert torch.equal(score.cpu(), f_score.cpu())
+    if ps is None:
+        v64 = cref.viterbi(cum.double(), tr.double(), db.double(), L, K, dtype=np.float64)
+        np.testing.assert_allclose(score.cpu().double().numpy(), v64["score"], rtol=1e-5)
+        cnt, segs = cnt.cpu(), segs.cpu()
+        for b in range(B):
+            got = [tuple(int(v) for v in segs[b, i]) for i in range(int(cnt[b]) - 1, -1, -1)]
+            assert [x[:3] for x in got] == [tuple(x[:3]) for x in v64["segments"][b]], b
+    else:
+        # projections: the fp64 max-semiring oracle's value
+        want = R.streaming_oracle(cum.double(), tr.double(), db.double(), L, K, "max", ps.double(), pe.double())
+        np.testing.assert_allclose(score.cpu().double().numpy(), want.numpy(), rtol=1e-5)
+    e_score, _, _ = ops.viterbi(*args, True, N.TSM_VITERBI_EXACT)
+    np.testing.assert_allclose(score.cpu().numpy(), e_score.cpu().numpy(), rtol=2e-5)
+
+
+def test_coop_factorised_viterbi_long_durations_c128():
+    """The C = 128, K = 500 cooperative instance (32 durations per lane, the
+    C = 128 configuration's) with backpointers: score within 1e-5 of the fp64
+    optimum and the optimum's segments; the exact kernel cannot hold this ring
+    in LDS, so before the max-plus cooperative scan this Viterbi was refused."""
+    from oracle import cref
+
+    B, T, K, C = 1, 1000, 500, 128
+    info = N.plan_info(B, T, C, K)
+    assert info["coop"] == 1 and info["CR"] == 32, info
+    g = torch.Generator().manual_seed(4800)
+    cum = torch.zeros(B, T + 1, C)
+    cum[:, 1:] = (0.2 * torch.randn(B, T, C, generator=g)).cumsum(1)
+    tr = 0.5 * torch.randn(C, C, generator=g) - 30.0 * torch.eye(C)
+    k = torch.arange(K, dtype=torch.float32)[:, None]
+    db = -0.5 * ((k - 150.0) / 50.0) ** 2 + 0.1 * torch.randn(K, C, generator=g)  # durations around 150
+    L = torch.tensor([T])
+    score, cnt, segs = ops.viterbi(cum.to(DEV), tr.to(DEV), db.to(DEV), L.to(DEV), K, None, None, True,
+                                   N.TSM_VITERBI_AUTO)
+    v64 = cref.viterbi(cum.double(), tr.double(), db.double(), L, K, dtype=np.float64)
+    np.testing.assert_allclose(score.cpu().double().numpy(), v64["score"], rtol=1e-5)
+    got = [tuple(int(v) for v in segs[0, i].cpu()) for i in range(int(cnt[0]) - 1, -1, -1)]
+    assert [x[:3] for x in got] == [tuple(x[:3]) for x in v64["segments"][0]]
+    assert max(x[1] - x[0] + 1 for x in got) > 64  # durations beyond the first lanes' ranges occur
+
+
 @pytest.mark.parametrize("B,T,K,C,lengths,proj,sr", CASES)
 def test_random_problems_vs_fp64_oracle(B, T, K, C, lengths, proj, sr, scan_path):
     cum, tr, db, L, ps, pe = rand_problem(B, T, K, C, 1000 + T + K + C, lengths, proj)

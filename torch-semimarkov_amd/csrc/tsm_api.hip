@@ -626,10 +626,10 @@ size_t tr_part_len(const Plan& p) {
   return (size_t)p.B * marg_nb(p) * (p.dense ? (size_t)p.Kmax : 1) * p.C * p.C;
 }
 
-// The forward runs a generic scan kernel unless a register-resident or
-// cooperative plan covers its semiring.
+// The forward runs a generic scan kernel unless a register-resident plan covers
+// its semiring (log only) or the plan is cooperative (both semirings).
 bool forward_generic(const Plan& pl, int semiring) {
-  return semiring != TSM_SEMIRING_LOG || (!pl.fast && !pl.coop);
+  return !pl.coop && (semiring != TSM_SEMIRING_LOG || !pl.fast);
 }
 
 size_t forward_ws_bytes(const Plan& pl, int semiring) {
@@ -700,7 +700,7 @@ size_t viterbi_ws_bytes(const Plan& pl, int with_tb) {
   Carver cv(nullptr);
   if (with_tb) cv.take<int32_t>((size_t)pl.B * (pl.T + 1) * pl.C);
   cv.take<int32_t>(pl.B);
-  if (pl.fast) {
+  if (pl.fast || pl.coop) {
     carve_scan(cv, pl, false);
     if (with_tb) cv.take<int32_t>((size_t)pl.B * (pl.T + 1) * pl.C);  // factorised backpointers, exact format
   }
@@ -709,13 +709,13 @@ size_t viterbi_ws_bytes(const Plan& pl, int with_tb) {
 }
 
 // Factorised Viterbi is used for algorithm 2, and for algorithm 0 when the
-// register-resident scan fits and either the problem has at least 2^28 cells
-// (B*T*K*C^2) or the plan cuts each sequence into several chunks: the exact
-// kernel runs one workgroup per sequence through all T steps, so few long
-// sequences leave most CUs idle (cfg1, B=4 x 1000 steps: 3.2 ms) while the
-// chunked scan spreads them over the chip.
+// register-resident or the cooperative scan fits and either the problem has at
+// least 2^28 cells (B*T*K*C^2) or the plan cuts each sequence into several
+// chunks: the exact kernel runs one workgroup per sequence through all T steps,
+// so few long sequences leave most CUs idle (cfg1, B=4 x 1000 steps: 3.2 ms)
+// while the chunked scan spreads them over the chip.
 bool viterbi_factorised(const Plan& pl, int algorithm) {
-  if (algorithm == TSM_VITERBI_EXACT || !pl.fast || pl.dense) return false;
+  if (algorithm == TSM_VITERBI_EXACT || (!pl.fast && !pl.coop) || pl.dense) return false;
   if (algorithm == TSM_VITERBI_FACTORISED) return true;
   const double cells = (double)pl.B * pl.T * pl.K * (double)pl.C * pl.C;
   return cells >= (double)(1 << 28) || pl.P >= 2;
@@ -1173,8 +1173,9 @@ int viterbi_impl(const float* cum, const float* emit, const float* tr, const flo
   if (rc) return rc;
   if (algorithm == TSM_VITERBI_FACTORISED && pl.dense)
     return fail(TSM_ERR_UNSUPPORTED, "the factorised Viterbi needs static (C, C) transitions");
-  if (algorithm == TSM_VITERBI_FACTORISED && !pl.fast)
-    return fail(TSM_ERR_UNSUPPORTED, "the factorised Viterbi needs the register-resident scan (C <= 64, rings in LDS)");
+  if (algorithm == TSM_VITERBI_FACTORISED && !pl.fast && !pl.coop)
+    return fail(TSM_ERR_UNSUPPORTED,
+                "the factorised Viterbi needs the register-resident or the cooperative scan (C <= 128, K <= 513)");
   if (viterbi_factorised(pl, algorithm)) {
     const size_t need = viterbi_ws_bytes(pl, with_tb);
     if (!workspace || ws_bytes < need)
@@ -1194,7 +1195,8 @@ int viterbi_impl(const float* cum, const float* emit, const float* tr, const flo
     p.zout = score;
     p.bp = bp;
     hipStream_t st = (hipStream_t)stream;
-    int e = tsm::launch_scan_viterbi(pl, p, st);
+    // cooperative plans (C > 64): the max-plus cooperative scan, with backpointers
+    int e = pl.fast ? tsm::launch_scan_viterbi(pl, p, st) : tsm::launch_scan_forward(pl, p, TSM_SEMIRING_MAX, st);
     if (e != hipSuccess) return hip_fail(e, "tsm_viterbi (factorised scan)");
     if (with_tb) {
       e = tsm::launch_fact_to_exact(bp, len, pl.B, pl.T, pl.C, bp_exact, st);
@@ -1544,7 +1546,8 @@ int tsm_viterbi_emissions_workspace(int64_t B, int64_t T, int64_t C, int64_t K, 
   Plan p;
   const int rc = make_plan(B, T, C, K, 0, 0, trans_rows, &p);
   if (rc) return rc;
-  *bytes = viterbi_ws_bytes(p, with_tb) + (viterbi_factorised(p, algorithm) ? 0 : emit_cum_bytes(p));
+  // (the register-resident scans read the scores; every other kernel reads cum_scores built first)
+  *bytes = viterbi_ws_bytes(p, with_tb) + ((viterbi_factorised(p, algorithm) && p.fast) ? 0 : emit_cum_bytes(p));
   return TSM_OK;
 }
 
@@ -1558,7 +1561,7 @@ int tsm_viterbi_emissions(const float* scores, const float* tr, const float* db,
   if (algorithm < TSM_VITERBI_AUTO || algorithm > TSM_VITERBI_FACTORISED)
     return fail(TSM_ERR_INVALID, "algorithm must be TSM_VITERBI_AUTO (0), _EXACT (1) or _FACTORISED (2), got %d",
                 algorithm);
-  if (viterbi_factorised(pl, algorithm))
+  if (viterbi_factorised(pl, algorithm) && pl.fast)
     return viterbi_impl(nullptr, scores, tr, db, len, ps, pe, B, T, C, K, trans_rows, score, with_tb, algorithm,
                         seg_count, segments, workspace, ws_bytes, stream);
   float* cum = nullptr;

@@ -98,10 +98,14 @@ __device__ inline bool exchange_row(const ScanParams& p, unsigned long long* xb,
   return *sflag == 0;
 }
 
-template <int J, int R, int CJ, bool FWD>
+// LOGSR: log-sum-exp over durations and source labels; else max-plus, with the
+// factorised Viterbi's backpointers `(k << 16) | c'` per (t, c) when p.bp is set
+// (ties to the smallest duration, then the smallest source label, as the
+// single-workgroup scan).
+template <int J, int R, int CJ, bool FWD, bool LOGSR = true>
 struct CoopChunk {
   static constexpr bool kFwd = FWD;
-  static constexpr bool kLog = true;
+  static constexpr bool kLog = LOGSR;
   // register budget: a lane holds 2R fp64 terms (ring reads, duration biases)
   static constexpr int kMaxThreads = R > 16 ? 256 : 512;
   __device__ static double* red(char* smem, const ScanParams& p) {
@@ -189,14 +193,32 @@ struct CoopChunk {
       float v0;
       if (FWD) {
         float mm = kMinusInf;
+        [[maybe_unused]] int mi = 0x7fffffff;
+        if constexpr (LOGSR) {
 #pragma unroll
-        for (int i = 0; i < CJ; ++i)
-          if (lj + J * i < C) mm = fmax2(mm, trr[i]);
-        float sm = 0.0f;
+          for (int i = 0; i < CJ; ++i)
+            if (lj + J * i < C) mm = fmax2(mm, trr[i]);
+        } else {
 #pragma unroll
-        for (int i = 0; i < CJ; ++i)
-          if (lj + J * i < C) sm += exp2_hw(trr[i] - mm);
-        const float u0 = group_lse2<J>(mm, sm);
+          for (int i = 0; i < CJ; ++i)
+            if (lj + J * i < C && trr[i] > mm) {
+              mm = trr[i];
+              mi = lj + J * i;
+            }
+        }
+        float u0;
+        if constexpr (LOGSR) {
+          float sm = 0.0f;
+#pragma unroll
+          for (int i = 0; i < CJ; ++i)
+            if (lj + J * i < C) sm += exp2_hw(trr[i] - mm);
+          u0 = group_lse2<J>(mm, sm);
+        } else {
+          // best source label of a segment starting at position 0
+          const ValIdx best = group_argmax_first<J>(ValIdx{mm, mi});
+          u0 = best.v;
+          if (p.bp != nullptr && cval && lj == 0 && j == 0) p.bp[((size_t)b * (T + 1)) * C + c] = best.i;
+        }
         v0 = u0 + ((has_ps && T > 0) ? ps_b[c] * kLog2e : 0.0f);
         if (lead && g == 0) {
 #pragma unroll
@@ -290,25 +312,44 @@ struct CoopChunk {
       double e[R];
 #pragma unroll
       for (int r = 0; r < R; ++r) e[r] = rb[J * r];
-      double y0 = e[0] + dbr[0];
-      float s0 = 1.0f, s1 = 0.0f;
+      float a2;
+      [[maybe_unused]] int kbest = 0;
+      if constexpr (LOGSR) {
+        double y0 = e[0] + dbr[0];
+        float s0 = 1.0f, s1 = 0.0f;
 #pragma unroll
-      for (int r = 1; r < R; ++r) {
-        const float x = exp2_hw((float)(e[r] - e[0]));
-        if (r & 1) s1 = fmaf(x, edb[r], s1);
-        else s0 = fmaf(x, edb[r], s0);
+        for (int r = 1; r < R; ++r) {
+          const float x = exp2_hw((float)(e[r] - e[0]));
+          if (r & 1) s1 = fmaf(x, edb[r], s1);
+          else s0 = fmaf(x, edb[r], s0);
+        }
+        float sacc = s0 + s1;
+        if (__ballot(!(sacc <= FLT_MAX) || lane_exact)) {
+          double mx2 = y0;
+#pragma unroll
+          for (int r = 1; r < R; ++r) mx2 = fmax(mx2, e[r] + dbr[r]);
+          sacc = 0.0f;
+#pragma unroll
+          for (int r = 0; r < R; ++r) sacc += exp2_hw((float)((e[r] + dbr[r]) - mx2));
+          y0 = mx2;
+        }
+        a2 = group_lse2<J>((float)((y0 + cx_t) - lvl_prev), sacc) + pa_t;
+      } else {
+        // max over durations; ties go to the smallest duration (lanes hold ascending k)
+        double ym = e[0] + dbr[0];
+        int km = 1 + lj;
+#pragma unroll
+        for (int r = 1; r < R; ++r) {
+          const double y = e[r] + dbr[r];
+          if (y > ym) {
+            ym = y;
+            km = 1 + lj + J * r;
+          }
+        }
+        const ValIdx best = group_argmax_first<J>(ValIdx{(float)((ym + cx_t) - lvl_prev), km});
+        a2 = best.v + pa_t;
+        kbest = best.i;
       }
-      float sacc = s0 + s1;
-      if (__ballot(!(sacc <= FLT_MAX) || lane_exact)) {
-        double mx2 = y0;
-#pragma unroll
-        for (int r = 1; r < R; ++r) mx2 = fmax(mx2, e[r] + dbr[r]);
-        sacc = 0.0f;
-#pragma unroll
-        for (int r = 0; r < R; ++r) sacc += exp2_hw((float)((e[r] + dbr[r]) - mx2));
-        y0 = mx2;
-      }
-      const float a2 = group_lse2<J>((float)((y0 + cx_t) - lvl_prev), sacc) + pa_t;
 
       // ---- the group's row of all labels ----
       ++s;
@@ -326,15 +367,35 @@ struct CoopChunk {
       }
       const float mx = group_max<J>(ml);
       const double lvl_t = lvl_prev + (double)mx;
-      float mq = kMinusInf;
+      float mixv;
+      if constexpr (LOGSR) {
+        float mq = kMinusInf;
 #pragma unroll
-      for (int i = 0; i < CJ; ++i)
-        if (lj + J * i < C) mq = fmax2(mq, (rv[i] - mx) + trr[i]);
-      float sq = 0.0f;
+        for (int i = 0; i < CJ; ++i)
+          if (lj + J * i < C) mq = fmax2(mq, (rv[i] - mx) + trr[i]);
+        float sq = 0.0f;
 #pragma unroll
-      for (int i = 0; i < CJ; ++i)
-        if (lj + J * i < C) sq += exp2_hw(((rv[i] - mx) + trr[i]) - mq);
-      const float mixv = group_lse2<J>(mq, sq);
+        for (int i = 0; i < CJ; ++i)
+          if (lj + J * i < C) sq += exp2_hw(((rv[i] - mx) + trr[i]) - mq);
+        mixv = group_lse2<J>(mq, sq);
+      } else {
+        float mq = kMinusInf;
+        int mqi = 0x7fffffff;
+#pragma unroll
+        for (int i = 0; i < CJ; ++i)
+          if (lj + J * i < C) {
+            const float q = (rv[i] - mx) + trr[i];
+            if (q > mq) {
+              mq = q;
+              mqi = lj + J * i;
+            }
+          }
+        // best source label for a segment starting at t (first on ties)
+        const ValIdx best = group_argmax_first<J>(ValIdx{mq, mqi});
+        mixv = best.v;
+        if (FWD && p.bp != nullptr && cval && lj == 0 && (j == 0 || t > t_lo))
+          p.bp[((size_t)b * (T + 1) + t) * C + c] = (kbest << 16) | best.i;
+      }
 
       const bool owned = FWD ? (j == 0 || t > t_lo) : (t < t_hi || j == jl);
       if (FWD) {

@@ -273,7 +273,7 @@ int launch_fast_max_j16_hi(const Plan& pl, const ScanParams& p, hipStream_t s);
 int launch_fast_max_j32(const Plan& pl, const ScanParams& p, hipStream_t s);
 int launch_fast_max_j64(const Plan& pl, const ScanParams& p, hipStream_t s);
 // cooperative log-semiring scan (tsm_coop.hip), pl.CR durations per lane
-int launch_coop_scan(const Plan& pl, const ScanParams& p, bool forward, hipStream_t s);
+int launch_coop_scan(const Plan& pl, const ScanParams& p, bool forward, bool logsr, hipStream_t s);
 int launch_scan_viterbi(const Plan& pl, const ScanParams& p, hipStream_t s);
 // Chunked speculative backtrace (tsm_backtrace.hip): P chunks of Lc positions per
 // sequence, walks starting D positions above their chunk, TCH backpointer rows

@@ -615,14 +615,14 @@ int launch_any(const Plan& pl, const ScanParams& p, int semiring, bool fwd, hipS
     return launch_dense_scan(pl, q, semiring, fwd, st);
   }
   if (semiring == kLog && pl.fast) return launch_fast(pl, p, fwd, st);
-  if (semiring == kLog && pl.coop) {
+  if (pl.coop) {
     // the cooperative scan's ring geometry replaces the generic one
     ScanParams q = p;
     q.RS = pl.CRS;
     q.RL = pl.CRL;
     q.R = pl.CR;
     q.KP = 16 * pl.CR;
-    return launch_coop_scan(pl, q, fwd, st);
+    return launch_coop_scan(pl, q, fwd, semiring == kLog, st);
   }
   return semiring == kLog ? launch_sr<true>(pl, p, fwd, st) : launch_sr<false>(pl, p, fwd, st);
 }

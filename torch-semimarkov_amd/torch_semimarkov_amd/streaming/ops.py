@@ -44,7 +44,7 @@ def _check_cooperative(rec: Tensor, B: int, T: int, C: int, K: int, semiring: in
     wait on their partner blocks; a group that gives up marks its sequences with
     recomputed = -1 and NaN results.  For those plans only, read the marks (one
     host synchronisation) and raise instead of returning NaN."""
-    if semiring != N.TSM_SEMIRING_LOG or tr_rows != 0 or not N.plan_info(B, T, C, K)["coop"]:
+    if tr_rows != 0 or not N.plan_info(B, T, C, K)["coop"]:
         return
     bad = torch.nonzero(rec < 0).flatten().tolist()
     if bad:
