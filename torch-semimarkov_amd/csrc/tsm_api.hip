@@ -1010,7 +1010,9 @@ int backward_impl(const float* cum, const float* emit, const float* tr, const fl
     f.lv_end = w.lv_end;
     f.e_own = e_own;
     f.s_out = s_out;
-    f.halo = halo;
+    // the cumulative-score scan takes each end sum from the tables at its owner
+    // chunk and writes no halo rows; the emission scan slides them (halo rows)
+    f.halo = emit != nullptr ? halo : nullptr;
     f.db_part = db_part;
     f.tr_part = tr_part;
     f.grad_output = grad_output;

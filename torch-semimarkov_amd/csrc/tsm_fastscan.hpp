@@ -88,6 +88,17 @@ struct Chunk {
   // to p.thalo, and chunk 0 records its boundary state at position 0 in
   // p.tst_st / p.tst_lv for the window below.
   static constexpr bool WIN = IN == kInWin;
+  // Fused marginals: where the end sums E[s,c] (the probability that a segment
+  // of label c ends at s) come from.  The cumulative-score instance takes them
+  // at each owned step s from the tables themselves, E = 2^(alpha[s,c] +
+  // beta[s,c] - log2 Z) (alpha from the forward's table, beta the step's own
+  // mixed state), one exponential per (s, c).  The emission and window
+  // instances slide per-term end sums along a DPP row instead (three more
+  // operations per term): with emission input the score gradient is a running
+  // sum of E - S over all later positions, which needs E and S summed from the
+  // same terms, and a window's top chunk hands the end sums of segments that
+  // cross into the window above to that window.
+  static constexpr bool ESLIDE = EMIT || WIN;
   static_assert(!MARG || (!FWD && LOGSR && J == 16), "fused marginals: backward log scan, 16-lane DPP rows");
   static constexpr int kCJ = CJ;
   static constexpr bool kFwd = FWD;
@@ -242,14 +253,14 @@ struct Chunk {
     // zeroed partials with no-return atomics, which never contend.
     constexpr bool kRegD = R <= 20;
     double zd = 0.0;
-    float d32[MARG ? R : 1], ea[MARG ? R : 1];
+    float d32[MARG ? R : 1], ea[(MARG && ESLIDE) ? R : 1];
     double d64[MARG && kRegD ? R : 1];
     [[maybe_unused]] double* dbp = MARG ? p.db_part + (size_t)item * Kmax * C : nullptr;
     if constexpr (MARG) {
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         d32[r] = 0.0f;
-        ea[r] = 0.0f;
+        if constexpr (ESLIDE) ea[r] = 0.0f;
         if constexpr (kRegD) {
           d64[r] = 0.0;
         } else {
@@ -422,9 +433,12 @@ struct Chunk {
     float pb_n = pb_src[(size_t)pb_row(t_first) * C + c];
     [[maybe_unused]] float u_n = 0.0f;
     [[maybe_unused]] double la_n = 0.0;
+    [[maybe_unused]] float ah_n = 0.0f;  // alpha-hat[t, c] (end sums from the tables)
+    [[maybe_unused]] const float* ah_b = MARG ? p.aval + (size_t)b * (T + 1) * C : nullptr;
     if constexpr (MARG) {
       u_n = u_b[(size_t)clampT(t_first) * C + c];
       la_n = al_b[clampT(t_first)];
+      if constexpr (!ESLIDE) ah_n = ah_b[(size_t)clampT(t_first) * C + c];
     }
 
     const int rec_spec = (mode == 1) ? (FWD ? t_lo : t_hi) : -1;
@@ -484,6 +498,13 @@ struct Chunk {
           double mn;
           block_minmax(m, m, red(smem, p), zd, mn);
           if (tid == 0) p.mframe[(size_t)bo * p.P + j] = zd - p.mz2[bo];
+          if constexpr (!ESLIDE) {
+            // the last chunk also owns row len, the start state of the scan (beta
+            // level 0, no label mix): E[len] = 2^(alpha[len] - log2 Z)
+            if (j == jl && cval && lj == 0)
+              e_own_b[(size_t)len * C + c] =
+                  exp2_hw((float)(p.alvl[row0 + len] - zd) + p.aval[(row0 + len) * C + c]);
+          }
         }
       }
       if (--A < 0) {
@@ -507,11 +528,13 @@ struct Chunk {
       const float pb_t = pb_n * ((FWD ? true : t >= 1) ? pb_scale : 0.0f);
       [[maybe_unused]] const float u_t = u_n;
       [[maybe_unused]] const double la_t = la_n;
+      [[maybe_unused]] const float ah_t = ah_n;
       {
         const int tn = t + dir;
         if constexpr (MARG) {
           u_n = u_b[(size_t)clampT(tn) * C + c];
           la_n = al_b[clampT(tn)];
+          if constexpr (!ESLIDE) ah_n = ah_b[(size_t)clampT(tn) * C + c];
         }
         cum_n = xs_b[(size_t)xs_row(tn) * C + c];
         pa_n = pa_src[(size_t)pa_row(tn) * C + c];
@@ -585,6 +608,11 @@ struct Chunk {
               for (int r = 0; r < R; ++r) tm[r] = (tm[r] * F1) * 0x1p-100f;
               F = 1.0f;
             }
+            if constexpr (!ESLIDE) {
+              // duration sums only (end sums from the tables, after the label mix)
+#pragma unroll
+              for (int r = 0; r < R; ++r) d32[r] += tm[r] * F;
+            } else {
             // the end sum of position t+1+KP (lane J-1, register R-1) is complete: out
             const int pr = t + 1 + KP;
             if (cval && lj == J - 1 && pr <= t_hi - 1 + Kmax && pr <= len) {
@@ -611,6 +639,7 @@ struct Chunk {
               // a bitwise merge: a select would become a register-array read at a lane-dependent index
               const float sl = __int_as_float((__float_as_int(prv) & lane_last) | (__float_as_int(ea[r]) & ~lane_last));
               ea[r] = add_row_ror1(sl, P);
+            }
             }
           }
         }
@@ -732,6 +761,12 @@ struct Chunk {
         if (cval && lj == 0 && store && owned) p.val[((size_t)b * (T + 1) + t) * C + c] = mixv;
         if (tid == 0 && store && owned) p.lvl[(size_t)b * (T + 1) + t] = lvl_t;
       }
+      if constexpr (MARG && !ESLIDE) {
+        // end sum of the owned row t: 2^(alpha[t,c] + beta[t,c] - log2 Z), beta the
+        // mixed state of this step in the chunk frame; no segment ends at position 0
+        if (t < t_hi && cval && lj == 0)
+          e_own_b[(size_t)t * C + c] = (t == 0) ? 0.0f : exp2_hw((float)((la_t + lvl_t) - zd) + (ah_t + mixv));
+      }
       // ---- ring entry for position t ----
       if (cval && lj == 0) {
         rc[A] = (lvl_t + (double)(mixv + pb_t)) - cx_t;
@@ -791,7 +826,8 @@ struct Chunk {
     if constexpr (MARG) {
       // rows still in the registers (lane lj, register r: position t_lo+1+lj+16r),
       // row t_lo (no own starts end there) and the duration sums
-      if (cval) {
+      if constexpr (ESLIDE) {
+       if (cval) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
           const int pr = t_lo + 1 + lj + J * r;
@@ -807,6 +843,7 @@ struct Chunk {
           }
         }
         if (lj == 0) e_own_b[(size_t)t_lo * C + c] = 0.0f;
+       }
       }
       fold_d();
       if constexpr (kRegD) {

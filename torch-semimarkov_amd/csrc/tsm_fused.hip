@@ -4,7 +4,10 @@
 //   u pass      u[t,c] = log2 sum_c' 2^(alpha-hat[t,c'] + trans[c',c] log2 e), the
 //               forward side of a segment starting at t with label c (the scan
 //               reads one value per step instead of redoing the label mix);
-//   scan        per chunk j, in its own frame: end sums e_own / halo, start sums
+//   scan        per chunk j, in its own frame: end sums e_own (cumulative scores:
+//               each owned row from the alpha table and the step's beta state;
+//               emission input and windows: per-term sums, rows past the chunk
+//               in halo), start sums
 //               s_out, duration sums db_part, frame estimate mframe[j];
 //   rows        grad_cum / grad_proj from E and S, each chunk's values times
 //               f_j = 2^(mframe[j] + offs[j]) (offs: the chunk's verified
@@ -298,7 +301,8 @@ __global__ void fused_rows_kernel(FusedParams f) {
       if (t > 0) {
         double e = fj * (double)f.e_own[o];
         const int d = t - j * Lc;  // rows j*Lc .. j*Lc+Kmax-1 also take chunk j-1's halo
-        if (j >= 1 && d < Kmax) e += fscale(f, b, j - 1) * (double)f.halo[(((size_t)b * f.P + j - 1) * Kmax + d) * C + c];
+        if (f.halo != nullptr && j >= 1 && d < Kmax)
+          e += fscale(f, b, j - 1) * (double)f.halo[(((size_t)b * f.P + j - 1) * Kmax + d) * C + c];
         E = (float)e;
       }
       if (t < len) S = (float)(fj * (double)f.s_out[o]);

@@ -154,7 +154,7 @@ struct FusedParams {
   double* mframe;          // (B*P) frame estimates; the frame scale pass turns them into factors f_j
   const float* e_own;      // (B, T+1, C)
   const float* s_out;      // (B, T+1, C)
-  const float* halo;       // (B*P, Kmax, C)
+  const float* halo;       // (B*P, Kmax, C), or null when the scan took each end sum from the tables
   const double* db_part;   // (B*P, Kmax, C)
   double* tr_part;         // (B*GNB, C, C)
   // coverage pass: inputs, the forward's levels and log2 Z, the backward chunks'
