@@ -602,6 +602,26 @@ def _ops_backward(cum, tr, db, L, K, ps=None, pe=None, g=None):
     return [x.cpu() for x in (gc, gt, gd, gps, gpe)], rec.cpu()
 
 
+@pytest.mark.parametrize("drop", [30.0, 60.0, 1e9])
+def test_fused_backward_suppressed_durations(drop, monkeypatch):
+    """Some durations of some labels suppressed by a large negative bias (30 and
+    60 nats below the rest, and the reference's NEG_INF = -1e9 masking): the
+    duration sums are kept without each term's bias factor and multiplied by it
+    when folded, so a lane whose factors fall below 2^-64 takes the exact
+    two-pass form; the gradients match the fp64 oracle either way."""
+    monkeypatch.delenv("TSM_SCAN_PATH", raising=False)
+    monkeypatch.delenv("TSM_MARGINAL_PATH", raising=False)
+    B, T, K, C = 2, 3000, 40, 40
+    _fused_plan(B, T, C, K, False)
+    cum, tr, db, L, _, _ = rand_problem(B, T, K, C, 5150, [3000, 1977])
+    db[20:33, ::3] -= drop
+    g = torch.tensor([1.0, 0.6])
+    p64, g64 = oracle_fp64(cum, tr, db, L, K, g=g)
+    part, grads = run_hip(cum, tr, db, L, K, g=g)
+    np.testing.assert_allclose(part.double().numpy(), p64.numpy(), rtol=RTOL_Z)
+    assert_grads(grads, g64)
+
+
 def test_fused_backward_recomputes_non_mixing_chunks(monkeypatch):
     """Sticky transitions and evidence at the sequence end: the beta states of
     the speculative chunks disagree with the exact ones, chunks are recomputed

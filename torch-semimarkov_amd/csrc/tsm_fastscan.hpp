@@ -214,7 +214,8 @@ struct Chunk {
     for (int r = 0; r < R; ++r) {
       const double d = (double)dbr[r] - (double)dbr[0];
       edb[r] = exp2_hw((float)d);
-      lane_exact = lane_exact || (d > 64.0);
+      // (fused marginals without sliding end sums also divide by the factor: keep it >= 2^-64)
+      lane_exact = lane_exact || (d > 64.0) || (MARG && !ESLIDE && d < -64.0 && 1 + lj + J * r <= Kmax);
     }
 
     // ---- empty rings ----
@@ -271,11 +272,13 @@ struct Chunk {
       if (tid == 0) p.mframe[item] = 0.0;
       if constexpr (!kRegD) __threadfence();  // the zeros before the first atomic add
     }
+    // (without sliding end sums the fp32 sums hold x * F: times the register's
+    // duration-bias factor, or 1 on a lane with extreme factors, when folded)
     auto fold_d = [&]() {
       if constexpr (MARG && kRegD) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-          d64[r] += (double)d32[r];
+          d64[r] += (double)((ESLIDE || lane_exact) ? d32[r] : d32[r] * edb[r]);
           d32[r] = 0.0f;
         }
       } else if constexpr (MARG) {
@@ -286,7 +289,8 @@ struct Chunk {
         double* a = dbp + (size_t)ljo * C + c;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-          if (cval && 1 + ljo + J * r <= Kmax) unsafeAtomicAdd(a, (double)d32[r]);
+          if (cval && 1 + ljo + J * r <= Kmax)
+            unsafeAtomicAdd(a, (double)((ESLIDE || lane_exact) ? d32[r] : d32[r] * edb[r]));
           a += (size_t)J * C;
           d32[r] = 0.0f;
         }
@@ -551,15 +555,22 @@ struct Chunk {
       if constexpr (LOGSR) {
         double y0 = e[0] + (double)dbr[0];
         float s0 = 1.0f, s1 = 0.0f;
-        float tm[MARG ? R : 1];  // MARG: the lane's terms 2^(x + db - y0)
+        // MARG: the lane's terms 2^(x + db - y0); without sliding end sums, the
+        // terms without their duration-bias factor (D sums x * F, and the fold
+        // multiplies by the factor, which is constant per register)
+        float tm[MARG ? R : 1];
         if constexpr (MARG) tm[0] = 1.0f;
 #pragma unroll
         for (int r = 1; r < R; ++r) {
           const float x = exp2_hw((float)(e[r] - e[0]));
-          if constexpr (MARG) {
+          if constexpr (MARG && ESLIDE) {
             tm[r] = x * edb[r];
             if (r & 1) s1 += tm[r];
             else s0 += tm[r];
+          } else if constexpr (MARG) {
+            tm[r] = x;
+            if (r & 1) s1 = fmaf(x, edb[r], s1);
+            else s0 = fmaf(x, edb[r], s0);
           } else {
             if (r & 1) s1 = fmaf(x, edb[r], s1);
             else s0 = fmaf(x, edb[r], s0);
@@ -585,7 +596,12 @@ struct Chunk {
 #pragma unroll
           for (int r = 0; r < R; ++r) {
             const float q = exp2_hw((float)(ey[r] - m));
-            if constexpr (MARG) tm[r] = q;
+            if constexpr (MARG && ESLIDE) {
+              tm[r] = q;
+            } else if constexpr (MARG) {
+              // a lane with extreme factors keeps the whole term (its fold multiplies by 1)
+              tm[r] = (lane_exact || !(edb[r] > 0.0f)) ? q : q * __builtin_amdgcn_rcpf(edb[r]);
+            }
             s += q;
           }
           y0 = m;
