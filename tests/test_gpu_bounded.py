@@ -128,11 +128,12 @@ def test_checkpointed_backward_vs_oracle_and_full_table(B, T, K, C, proj, wc, ki
     np.testing.assert_allclose(part.double().numpy(), z, rtol=RTOL_Z)
     for got, ref, name in zip(grads, want, NAMES):
         np.testing.assert_allclose(got.double().numpy(), ref, **GRAD_TOL, err_msg=name)
-    # the full-table backward of the same inputs: the same quantities, other chunking
+    # the full-table backward of the same inputs: the same quantities, other chunking and
+    # other roundings (each within the bar of the oracle above, so within twice it of each other)
     pf, gf = run_full(cum, tr, db, L, K, ps, pe, gout)
     np.testing.assert_allclose(part.numpy(), pf.numpy(), rtol=2e-6)
     for got, ref, name in zip(grads, gf, NAMES):
-        np.testing.assert_allclose(got.numpy(), ref.numpy(), rtol=1e-5, atol=5e-5, err_msg=name)
+        np.testing.assert_allclose(got.numpy(), ref.numpy(), rtol=2e-5, atol=5e-5, err_msg=name)
 
 
 def test_checkpointed_window_aligned_with_sequence_end():
@@ -180,7 +181,7 @@ def test_checkpoint_plan_budget_and_memory():
     assert peak_ck < 0.6 * peak_full
     np.testing.assert_allclose(part.numpy(), pf.numpy(), rtol=2e-6)
     for got, ref, name in zip(grads, gf, NAMES):
-        np.testing.assert_allclose(got.numpy(), ref.numpy(), rtol=1e-5, atol=5e-5, err_msg=name)
+        np.testing.assert_allclose(got.numpy(), ref.numpy(), rtol=2e-5, atol=5e-5, err_msg=name)
 
 
 def test_checkpointed_rejects_bad_window_and_unsupported_plans():
@@ -209,7 +210,7 @@ def test_streaming_forward_memory_budget_autograd():
         outs.append((z.detach().cpu(), [v.cpu() for v in g]))
     np.testing.assert_allclose(outs[1][0].numpy(), outs[0][0].numpy(), rtol=2e-6)
     for got, ref, name in zip(outs[1][1], outs[0][1], NAMES):
-        np.testing.assert_allclose(got.numpy(), ref.numpy(), rtol=1e-5, atol=5e-5, err_msg=name)
+        np.testing.assert_allclose(got.numpy(), ref.numpy(), rtol=2e-5, atol=5e-5, err_msg=name)
     C2 = 80
     c2 = torch.randn(1, 200, C2).cumsum(1).to(DEV).requires_grad_(True)
     z = tsa.semi_crf_streaming_forward(c2, torch.zeros(C2, C2, device=DEV), torch.zeros(8, C2, device=DEV),
