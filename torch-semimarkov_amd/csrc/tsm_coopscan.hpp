@@ -70,15 +70,19 @@ __device__ __forceinline__ bool aborted(const ScanParams& p) {
   return __hip_atomic_load(p.xabort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
 }
 
-// Writes this member's results of step s and gathers the group's full row of
-// step s into row[0..C).  All threads call it; false when the group gave up.
-__device__ inline bool exchange_row(const ScanParams& p, unsigned long long* xb, unsigned s, bool writer, int c,
-                                    float a2, float* row, int* sflag) {
-  const int C = p.C, par = s & 1;
+// Writes this member's result of step s into the group's slot of the step's parity.
+__device__ __forceinline__ void publish_row(const ScanParams& p, unsigned long long* xb, unsigned s, bool writer,
+                                            int c, float a2) {
   if (writer) {
     const unsigned long long w = ((unsigned long long)s << 32) | (unsigned long long)__float_as_uint(a2);
-    __hip_atomic_store(&xb[par * C + c], w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&xb[(s & 1) * p.C + c], w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+}
+
+// Gathers the group's full row of step s into row[0..C).  All threads call it;
+// false when the group gave up.
+__device__ inline bool gather_row(const ScanParams& p, unsigned long long* xb, unsigned s, float* row, int* sflag) {
+  const int C = p.C, par = s & 1;
   for (int cc = threadIdx.x; cc < C; cc += blockDim.x) {
     unsigned long long w;
     int n = 0;
@@ -96,6 +100,14 @@ __device__ inline bool exchange_row(const ScanParams& p, unsigned long long* xb,
   }
   lds_barrier();
   return *sflag == 0;
+}
+
+// Writes this member's results of step s and gathers the group's full row of
+// step s into row[0..C).  All threads call it; false when the group gave up.
+__device__ inline bool exchange_row(const ScanParams& p, unsigned long long* xb, unsigned s, bool writer, int c,
+                                    float a2, float* row, int* sflag) {
+  publish_row(p, xb, s, writer, c, a2);
+  return gather_row(p, xb, s, row, sflag);
 }
 
 // LOGSR: log-sum-exp over durations and source labels; else max-plus, with the
@@ -283,7 +295,42 @@ struct CoopChunk {
     const int rec_spec = (mode == 1) ? (FWD ? t_lo : t_hi) : -1;
     const int rec_end = FWD ? ((t_hi < len) ? t_hi : -1) : ((j >= 1) ? t_lo : -1);
 
+    // The pull of step t+1 over durations of register r >= 1 reads positions that
+    // exist before step t's row comes back, so it runs while the row travels
+    // between the members (the exchange is most of a step): psum = sum over
+    // r >= 1 of 2^(e[r] - e[1]) * edb[r] (log), or the best of those terms (max).
+    // The next step adds the register-0 terms (durations 1..16; the first is the
+    // position step t writes).  `base` points at the next step's r = 0 entries.
+    [[maybe_unused]] float psum = 0.0f;
+    [[maybe_unused]] double pe1 = 0.0, pmax = 0.0;
+    [[maybe_unused]] int pk = 0;
+    auto partial_pull = [&](const double* base) {
+      if constexpr (LOGSR) {
+        pe1 = base[J];
+        float q0 = edb[1], q1 = 0.0f;
+#pragma unroll
+        for (int r = 2; r < R; ++r) {
+          const float x = exp2_hw((float)(base[J * r] - pe1));
+          if (r & 1) q1 = fmaf(x, edb[r], q1);
+          else q0 = fmaf(x, edb[r], q0);
+        }
+        psum = q0 + q1;
+      } else {
+        pmax = base[J] + dbr[1];
+        pk = 1 + lj + J;
+#pragma unroll
+        for (int r = 2; r < R; ++r) {
+          const double y = base[J * r] + dbr[r];
+          if (y > pmax) {
+            pmax = y;
+            pk = 1 + lj + J * r;
+          }
+        }
+      }
+    };
+
     int A = A0;  // ring index of the current position
+    partial_pull(rc + A0 + lj);  // step t_first: index A0 - 1, entries from A0 on
     for (int t = t_first; t != t_end; t += dir) {
       if (--A < 0) {
         if (cval) {
@@ -307,24 +354,22 @@ struct CoopChunk {
         pb_n = pb_src[(size_t)pb_row(tn) * C + c];
       }
 
-      // ---- pull over the lane's durations (own labels) ----
+      // ---- pull over the lane's durations (own labels): the register-0 terms
+      //      and the partial sums of the others, computed during the last exchange ----
       const double* rb = rc + A + 1 + lj;
-      double e[R];
-#pragma unroll
-      for (int r = 0; r < R; ++r) e[r] = rb[J * r];
+      const double e0 = rb[0];
       float a2;
       [[maybe_unused]] int kbest = 0;
       if constexpr (LOGSR) {
-        double y0 = e[0] + dbr[0];
-        float s0 = 1.0f, s1 = 0.0f;
+        double y0 = e0 + dbr[0];
+        // 1 + 2^(e[1] - e[0]) * psum: the one-pass sum relative to the first term
+        float sacc = fmaf(exp2_hw((float)(pe1 - e0)), psum, 1.0f);
+        // overflow, extreme factors, or a partial sum so large that an underflowed
+        // 2^(e[1] - e[0]) could still matter: the exact two-pass form
+        if (__ballot(!(sacc <= FLT_MAX) || lane_exact || !(psum <= 0x1p64f))) {
+          double e[R];
 #pragma unroll
-        for (int r = 1; r < R; ++r) {
-          const float x = exp2_hw((float)(e[r] - e[0]));
-          if (r & 1) s1 = fmaf(x, edb[r], s1);
-          else s0 = fmaf(x, edb[r], s0);
-        }
-        float sacc = s0 + s1;
-        if (__ballot(!(sacc <= FLT_MAX) || lane_exact)) {
+          for (int r = 0; r < R; ++r) e[r] = rb[J * r];
           double mx2 = y0;
 #pragma unroll
           for (int r = 1; r < R; ++r) mx2 = fmax(mx2, e[r] + dbr[r]);
@@ -335,26 +380,26 @@ struct CoopChunk {
         }
         a2 = group_lse2<J>((float)((y0 + cx_t) - lvl_prev), sacc) + pa_t;
       } else {
-        // max over durations; ties go to the smallest duration (lanes hold ascending k)
-        double ym = e[0] + dbr[0];
+        // max over durations; ties go to the smallest duration (lanes hold ascending
+        // k; register 0 holds the lane's smallest)
+        double ym = e0 + dbr[0];
         int km = 1 + lj;
-#pragma unroll
-        for (int r = 1; r < R; ++r) {
-          const double y = e[r] + dbr[r];
-          if (y > ym) {
-            ym = y;
-            km = 1 + lj + J * r;
-          }
+        if (pmax > ym) {
+          ym = pmax;
+          km = pk;
         }
         const ValIdx best = group_argmax_first<J>(ValIdx{(float)((ym + cx_t) - lvl_prev), km});
         a2 = best.v + pa_t;
         kbest = best.i;
       }
 
-      // ---- the group's row of all labels ----
+      // ---- the group's row of all labels; the next step's partial pull meanwhile
+      //      (its index A - 1: entries from A on; every one exists already) ----
       ++s;
       const int par = s & 1;
-      if (!exchange_row(p, xb, s, cval && lj == 0, c, a2, row + par * C, sflag)) return false;
+      publish_row(p, xb, s, cval && lj == 0, c, a2);
+      partial_pull(rc + A + lj);
+      if (!gather_row(p, xb, s, row + par * C, sflag)) return false;
 
       // ---- all labels: normaliser and label mix of the own labels ----
       float rv[CJ];
