@@ -196,6 +196,9 @@ struct Chunk {
       const int di = k < K - 1 ? k : K - 1;
       dbr[r] = (k <= Kmax) ? p.db[(size_t)di * C + c] * kLog2e : (float)kInvD;
     }
+    // Kmax = 1: the duration-1 bias of the label (the register-0 bias of lane 0)
+    [[maybe_unused]] const bool k1 = Kmax == 1;
+    [[maybe_unused]] const float db1 = p.db[(size_t)(K > 1 ? 1 : 0) * C + c] * kLog2e;
     float trr[kCJ];
 #pragma unroll
     for (int i = 0; i < kCJ; ++i) {
@@ -552,7 +555,12 @@ struct Chunk {
       for (int r = 0; r < R; ++r) e[r] = rb[J * r];
       float a2;
       int kbest = 0;
-      if constexpr (LOGSR) {
+      if (!MARG && R == 1 && k1) {
+        // a single duration (Kmax = 1, the HMM): the term of lane 0, which every lane
+        // reads itself; the group reduction would return exactly this value
+        a2 = (float)(((rc[A + 1] + (double)db1) + cx_t) - lvl_prev) + pa_t;
+        kbest = 1;
+      } else if constexpr (LOGSR) {
         double y0 = e[0] + (double)dbr[0];
         float s0 = 1.0f, s1 = 0.0f;
         // MARG: the lane's terms 2^(x + db - y0); without sliding end sums, the
