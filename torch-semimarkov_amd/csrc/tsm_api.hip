@@ -113,7 +113,7 @@ void plan_fast(Plan& p, const DeviceInfo& di, int fj_only = 0) {
     // linear ring of RL > KP entries, compacted every RL - KP steps: about 2*KP+1
     // entries, fewer when LDS is short (at least 32 steps between compactions).
     // RL % 32 == J % 32 puts the label rows of a half-wave on distinct banks.
-    auto ring_fits = [&](int rl, int per) { return (size_t)per * tsm::fast_lds_layout(p.C, rl, RS).total <= (size_t)di.max_lds; };
+    auto ring_fits = [&](int rl, int per) { return (size_t)per * tsm::fast_lds_layout(p.C, rl, RS, 0).total <= (size_t)di.max_lds; };
     auto bank_down = [&](int rl) { while (rl > 0 && rl % 32 != J % 32) --rl; return rl; };
     // the longest ring (<= 2*KP+1 entries) of which `per` fit one CU, 0 if none does
     auto ring_for = [&](int per) {
@@ -123,9 +123,34 @@ void plan_fast(Plan& p, const DeviceInfo& di, int fj_only = 0) {
       rl = bank_down(rl);
       return rl < KP + 33 ? 0 : rl;
     };
-    const int RL = ring_for(1);
+    int RL = ring_for(1);
     if (RL == 0) continue;
-    const size_t lds = tsm::fast_lds_layout(p.C, RL, RS).total;
+    // 16-lane plans: the fused-marginal beta scan's operand stage behind the rings,
+    // batches of 16, 8 or 4 steps (the longest that fits), else batches of 4 with
+    // the ring shortened (down to the same 32 steps between compactions)
+    size_t fstage = 0;
+    int fsb = 0;
+    if (J == 16) {
+      auto stage_bytes = [&](int sb) { return (size_t)(NT / J) * (2 * sb + 1) * 16; };
+      for (int sb : {16, 8, 4}) {
+        if (tsm::fast_lds_layout(p.C, RL, RS, stage_bytes(sb)).total <= (size_t)di.max_lds) {
+          fstage = stage_bytes(sb);
+          fsb = sb;
+          break;
+        }
+      }
+      if (fsb == 0) {
+        int rl = RL;
+        while (rl >= KP + 33 && tsm::fast_lds_layout(p.C, rl, RS, stage_bytes(4)).total > (size_t)di.max_lds)
+          rl = bank_down(rl - 1);
+        if (rl >= KP + 33) {
+          RL = rl;
+          fstage = stage_bytes(4);
+          fsb = 4;
+        }
+      }
+    }
+    const size_t lds = tsm::fast_lds_layout(p.C, RL, RS, fstage).total;
     // rings for two chunks per CU (used when the compiled kernel also leaves
     // registers for a second workgroup)
     const int RL2 = ring_for(2);
@@ -139,8 +164,10 @@ void plan_fast(Plan& p, const DeviceInfo& di, int fj_only = 0) {
       p.FRS = RS;
       p.FRL = RL;
       p.fast_lds = lds;
+      p.fstage = fstage;
+      p.FSB = fsb;
       p.FRL2 = RL2;
-      p.fast_lds2 = RL2 > 0 ? tsm::fast_lds_layout(p.C, RL2, RS).total : 0;
+      p.fast_lds2 = RL2 > 0 ? tsm::fast_lds_layout(p.C, RL2, RS, 0).total : 0;
     }
   }
 }
@@ -434,7 +461,7 @@ int make_plan(int64_t B, int64_t T, int64_t C, int64_t K, int has_ps, int has_pe
   p.mfused = 0;
   const char* menv = getenv("TSM_MARGINAL_PATH");
   const bool separate = menv != nullptr && strcmp(menv, "separate") == 0;
-  if (!separate && p.fast && p.FJ == 16) {
+  if (!separate && p.fast && p.FJ == 16 && p.FSB > 0) {
     p.mfused = 1;
     // transition gradient: about eight blocks per CU, at least 256 starts each
     int64_t gnb = cdiv(8 * (int64_t)di.n_cu, (int64_t)p.B);

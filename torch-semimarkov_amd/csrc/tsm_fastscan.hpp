@@ -105,7 +105,7 @@ struct Chunk {
   static constexpr bool kLog = LOGSR;
   static constexpr int kMaxThreads = R > 16 ? 512 : 1024;
   __device__ static double* red(char* smem, const ScanParams& p) {
-    return reinterpret_cast<double*>(smem + fast_lds_layout(p.C, p.RL, p.RS).red);
+    return reinterpret_cast<double*>(smem + fast_lds_layout(p.C, p.RL, p.RS, 0).red);
   }
   // Emission input: sgn * cum * log2(e), in the chunk's frame, of the position i
   // behind `base` (FWD: base - i, BWD: base + i), for i = i0 + lj of one block of
@@ -145,7 +145,7 @@ struct Chunk {
     const int C = p.C, Kmax = p.Kmax, K = p.K, RS = p.RS, RL = p.RL, T = p.T;
     const int len = seq_len(p, b);
     const int item = b * p.P + j;
-    const FastLds L = fast_lds_layout(C, RL, RS);
+    const FastLds L = fast_lds_layout(C, RL, RS, 0);
     double* ring = reinterpret_cast<double*>(smem + L.ring);
     double* lring = reinterpret_cast<double*>(smem + L.lring);
     float* row = reinterpret_cast<float*>(smem + L.row);
@@ -414,7 +414,7 @@ struct Chunk {
     }
     __syncthreads();
 
-    // ---- per-step operands, prefetched one step ahead ----
+    // ---- per-step operands ----
     const int dir = FWD ? 1 : -1;
     const int t_first = t_start + dir;
     const int t_end = FWD ? t_hi + 1 : t_lo - 1;  // exclusive
@@ -433,19 +433,40 @@ struct Chunk {
     const float pb_scale = (FWD ? has_ps : has_pe) ? kLog2e : 0.0f;
     auto pa_row = [&](int t) { return FWD ? clampT1(t - 1) : clampT1(t); };
     auto pb_row = [&](int t) { return FWD ? clampT1(t) : clampT1(t - 1); };
-    float cum_n = xs_b[(size_t)xs_row(t_first) * C + c];
     // emission input: the running sgn * cum * log2(e) of the previous position
     [[maybe_unused]] double cx_run = 0.0;
-    float pa_n = pa_src[(size_t)pa_row(t_first) * C + c];
-    float pb_n = pb_src[(size_t)pb_row(t_first) * C + c];
-    [[maybe_unused]] float u_n = 0.0f;
-    [[maybe_unused]] double la_n = 0.0;
-    [[maybe_unused]] float ah_n = 0.0f;  // alpha-hat[t, c] (end sums from the tables)
     [[maybe_unused]] const float* ah_b = MARG ? p.aval + (size_t)b * (T + 1) * C : nullptr;
+    // Scans without marginals: the operands of the next step, loaded one step ahead.
+    [[maybe_unused]] float cum_n = 0.0f, pa_n = 0.0f, pb_n = 0.0f;
+    // Fused marginals (six operands per step): the operands of step si (si = 0, 1, ...
+    // from t_first) go through LDS in batches of SB <= J steps (SB = p.SB, a power of
+    // two).  Lane lj < SB of a group loads those of step n*SB + lj of batch n one
+    // batch early and writes them to the group's slots at the first step of batch n,
+    // when every read of batch n-1's slots is done (a wave runs its LDS operations in
+    // order), so a global load has SB steps to arrive instead of one.  Slots: two
+    // float4 per step (score row, proj_end side, proj_start side, u; alpha-hat row and
+    // the fp64 alpha level), and one float4 of padding per group so that the groups
+    // of a wave read different banks.
+    [[maybe_unused]] const int SB = MARG ? p.SB : 1;
+    [[maybe_unused]] const int sbs = __builtin_ctz((unsigned)SB);
+    [[maybe_unused]] float4* stg = reinterpret_cast<float4*>(smem + L.stage) + (size_t)g * (2 * SB + 1);
+    [[maybe_unused]] float qx = 0.0f, qa = 0.0f, qb = 0.0f, qu = 0.0f, qh = 0.0f;
+    [[maybe_unused]] double ql = 0.0;
+    [[maybe_unused]] auto stage_load = [&](int n) {
+      const int tq = t_first + dir * (n * SB + lj);
+      qx = xs_b[(size_t)xs_row(tq) * C + c];
+      qa = pa_src[(size_t)pa_row(tq) * C + c];
+      qb = pb_src[(size_t)pb_row(tq) * C + c];
+      qu = u_b[(size_t)clampT(tq) * C + c];
+      ql = al_b[clampT(tq)];
+      if constexpr (!ESLIDE) qh = ah_b[(size_t)clampT(tq) * C + c];
+    };
     if constexpr (MARG) {
-      u_n = u_b[(size_t)clampT(t_first) * C + c];
-      la_n = al_b[clampT(t_first)];
-      if constexpr (!ESLIDE) ah_n = ah_b[(size_t)clampT(t_first) * C + c];
+      stage_load(0);
+    } else {
+      cum_n = xs_b[(size_t)xs_row(t_first) * C + c];
+      pa_n = pa_src[(size_t)pa_row(t_first) * C + c];
+      pb_n = pb_src[(size_t)pb_row(t_first) * C + c];
     }
 
     const int rec_spec = (mode == 1) ? (FWD ? t_lo : t_hi) : -1;
@@ -528,25 +549,44 @@ struct Chunk {
         }
         A = A0 - 1;
       }
-      double cx_t;
-      if constexpr (EMIT) cx_t = cx_run = cx_run + (double)cum_n * kLog2eD;
-      else cx_t = sgn * (double)cum_n * kLog2eD;
-      const float pa_t = pa_n * ((FWD ? t >= 1 : true) ? pa_scale : 0.0f);
-      const float pb_t = pb_n * ((FWD ? true : t >= 1) ? pb_scale : 0.0f);
-      [[maybe_unused]] const float u_t = u_n;
-      [[maybe_unused]] const double la_t = la_n;
-      [[maybe_unused]] const float ah_t = ah_n;
-      {
-        const int tn = t + dir;
-        if constexpr (MARG) {
-          u_n = u_b[(size_t)clampT(tn) * C + c];
-          la_n = al_b[clampT(tn)];
-          if constexpr (!ESLIDE) ah_n = ah_b[(size_t)clampT(tn) * C + c];
+      // ---- this step's operands ----
+      float x_t, pa_v, pb_v;
+      [[maybe_unused]] float u_t = 0.0f, ah_t = 0.0f;
+      [[maybe_unused]] double la_t = 0.0;
+      if constexpr (MARG) {
+        // slot si mod SB of the staged batch
+        const int si = (t - t_first) * dir;
+        const int slot = si & (SB - 1);
+        if (slot == 0) {
+          if (lj < SB) {
+            stg[2 * lj] = make_float4(qx, qa, qb, qu);
+            stg[2 * lj + 1] = make_float4(qh, __int_as_float(__double2loint(ql)), __int_as_float(__double2hiint(ql)), 0.0f);
+          }
+          wave_lds_order();
+          stage_load((si >> sbs) + 1);
         }
+        const float4 o0 = stg[2 * slot];
+        const float4 o1 = stg[2 * slot + 1];
+        x_t = o0.x;
+        pa_v = o0.y;
+        pb_v = o0.z;
+        u_t = o0.w;
+        ah_t = o1.x;
+        la_t = __hiloint2double(__float_as_int(o1.z), __float_as_int(o1.y));
+      } else {
+        x_t = cum_n;
+        pa_v = pa_n;
+        pb_v = pb_n;
+        const int tn = t + dir;
         cum_n = xs_b[(size_t)xs_row(tn) * C + c];
         pa_n = pa_src[(size_t)pa_row(tn) * C + c];
         pb_n = pb_src[(size_t)pb_row(tn) * C + c];
       }
+      double cx_t;
+      if constexpr (EMIT) cx_t = cx_run = cx_run + (double)x_t * kLog2eD;
+      else cx_t = sgn * (double)x_t * kLog2eD;
+      const float pa_t = pa_v * ((FWD ? t >= 1 : true) ? pa_scale : 0.0f);
+      const float pb_t = pb_v * ((FWD ? true : t >= 1) ? pb_scale : 0.0f);
 
       // ---- pull over the lane's durations ----
       const double* rb = rc + A + 1 + lj;

@@ -21,6 +21,7 @@ struct ScanParams {
   const float* pe;         // (B, T, C) proj_end or null
   int B, T, C, K, Kmax, RS;
   int R, KP, RL;           // durations per lane, padded durations, ring row length
+  int SB;                  // fused-marginal beta scan: steps per operand batch (power of two)
   int P, Lc, W;            // chunks per sequence, chunk length, warm-up
   int retry;               // 1: recompute only speculative chunks that failed verification
   float tol;               // verification tolerance, log2 units

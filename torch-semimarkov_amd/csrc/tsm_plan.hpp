@@ -30,6 +30,12 @@ struct Plan {
   // FRS level slots, FRL ring length per label (fp64 entries), fast_lds bytes
   int fast, FJ, FR, FNT, FRS, FRL;
   size_t fast_lds;
+  // the operand stage the fused-marginal beta scan keeps behind the rings (16-lane
+  // plans): FSB steps per batch (16, 8 or 4), fstage bytes (per label group two
+  // float4 per step and one of padding); 0 when it does not fit, and then the
+  // marginals stay separate
+  size_t fstage;
+  int FSB;
   // Two chunks per CU for a fast scan direction whose compiled instance leaves
   // room for a second workgroup on every SIMD: P2 chunks of Lc2 positions per
   // sequence, rings of FRL2 entries (fast_lds2 bytes).  dualF / dualB / dualV: the
@@ -156,16 +162,18 @@ struct FastLds {
   size_t lring;  // double[RS]   per-position levels
   size_t row;    // float[2*C]   per-step row of all labels (double buffered)
   size_t red;    // double[64]   block reductions (verification)
+  size_t stage;  // fused marginals: per-step operands of a batch of steps, stage bytes
   size_t total;
 };
 
-__host__ __device__ inline FastLds fast_lds_layout(int C, int RL, int RS) {
+__host__ __device__ inline FastLds fast_lds_layout(int C, int RL, int RS, size_t stage) {
   FastLds L;
   size_t o = 0;
   L.ring = o; o = align16(o + 8 * (size_t)C * RL);
   L.lring = o; o = align16(o + sizeof(double) * RS);
   L.row = o; o = align16(o + sizeof(float) * 2 * C);
   L.red = o; o = align16(o + sizeof(double) * 64);
+  L.stage = o; o = align16(o + stage);
   L.total = o;
   return L;
 }

@@ -664,10 +664,11 @@ int launch_apply_offsets(const Plan& pl, const ScanParams& p, bool forward, hipS
 }
 
 int launch_scan_backward_fused(const Plan& pl, const ScanParams& p, hipStream_t st) {
-  if (!pl.fast || pl.FJ != 16) return (int)hipErrorInvalidValue;
+  if (!pl.fast || pl.FJ != 16 || pl.FSB < 4 || pl.fstage == 0) return (int)hipErrorInvalidValue;
   ScanParams q = p;
   q.RS = pl.FRS;
   q.RL = pl.FRL;
+  q.SB = pl.FSB;
   q.R = pl.FR;
   q.KP = 16 * pl.FR;
   return pl.FR <= 16 ? launch_fused_j16_lo(pl, q, st) : launch_fused_j16_hi(pl, q, st);
