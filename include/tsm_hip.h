@@ -204,6 +204,25 @@ int tsm_viterbi(const float* cum_scores, const float* transition, const float* d
                 int32_t* segments, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Segment score terms of a traceback: row i < seg_count[b] of tsm_viterbi's
+ * segments becomes out[b, i, :] = (start, end, label, content, duration bias,
+ * transition), fp64:
+ *   content    = cum_scores[b, end+1, label] - cum_scores[b, start, label]
+ *                (the fp32 difference)
+ *   duration   = duration_bias[min(end - start + 1, K - 1), label]
+ *   transition = transition[previous label, label]  (static (C, C) transitions;
+ *                the first segment's previous label is the best start label)
+ * A segment's score is (content + duration) + transition in fp64.  Rows from
+ * seg_count[b] on are not written.  No workspace.
+ * Replaces:
+ *   nn.py:532-555  SemiMarkovCRFHead._compute_segment_score (three .item()
+ *                  reads per segment)
+ * ------------------------------------------------------------------------- */
+int tsm_segment_terms(const float* cum_scores, const float* transition, const float* duration_bias,
+                      const int32_t* seg_count, const int32_t* segments, int64_t B, int64_t T, int64_t C,
+                      int64_t K, double* out, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Emission prologue: projected scores (B, T, C) -> cumulative scores
  * (B, T+1, C) fp32 with a zero first row, optionally zero-centred per (b, c)
  * over all T positions, and its backward.

@@ -446,6 +446,33 @@ def test_random_problems_vs_fp64_oracle(B, T, K, C, lengths, proj, sr, scan_path
     assert_grads(grads, g64)
 
 
+@pytest.mark.parametrize("B,T,K,C,lengths,sr", [
+    (2, 600, 20, 12, [600, 377], "log"),
+    (3, 900, 40, 24, [900, 1, 512], "log"),
+    (1, 1300, 100, 32, None, "log"),
+    (2, 700, 30, 20, [700, 333], "max"),
+])
+def test_eight_lane_groups_vs_fp64_oracle(B, T, K, C, lengths, sr, monkeypatch):
+    """Plans with few chunks take 16 lanes per label; TSM_FAST_J=8 keeps the 8-lane
+    instances (several durations per lane, a four-source label mix at C > 16, the
+    separate marginal kernel) checked against the fp64 oracle, with the Viterbi
+    score of the 8-lane factorised scan against the exact kernel."""
+    monkeypatch.delenv("TSM_SCAN_PATH", raising=False)
+    monkeypatch.setenv("TSM_FAST_J", "8")
+    info = N.plan_info(B, T, C, K)
+    assert info["fast"] == 1 and info["FJ"] == 8 and info["mfused"] == 0, info
+    cum, tr, db, L, _, _ = rand_problem(B, T, K, C, 808 + T + K, lengths)
+    g = torch.linspace(0.5, 2.0, B)
+    p64, g64 = oracle_fp64(cum, tr, db, L, K, sr, None, None, g)
+    part, grads = run_hip(cum, tr, db, L, K, sr, None, None, g)
+    np.testing.assert_allclose(part.double().numpy(), p64.numpy(), rtol=RTOL_Z, atol=1e-6)
+    assert_grads(grads, g64)
+    args = (cum.to(DEV), tr.to(DEV), db.to(DEV), L.to(DEV), K, None, None)
+    f_score, _, _ = ops.viterbi(*args, False, N.TSM_VITERBI_FACTORISED)
+    e_score, _, _ = ops.viterbi(*args, False, N.TSM_VITERBI_EXACT)
+    np.testing.assert_allclose(f_score.cpu().numpy(), e_score.cpu().numpy(), rtol=2e-5)
+
+
 @pytest.mark.parametrize("lengths", [[2600, 1900], [2600, 1560]])
 def test_chunked_scan_vs_fp64_oracle(lengths, scan_path):
     """T long enough for several speculative chunks (warm-up + verification); the
@@ -1178,6 +1205,30 @@ def test_traceback_skips_long_sequences():
     assert res.segments[1][0].start == 0 and res.segments[1][-1].end == 11
 
 
+def test_segment_terms_match_host_gathers():
+    """tsm_segment_terms against the same terms gathered on the host from the traceback
+    rows: content as the fp32 difference of two cum entries, duration bias at
+    min(end-start+1, K-1), transition from the previous label (ragged lengths, a
+    length-1 sequence); the segment scores sum to the Viterbi score."""
+    B, T, K, C = 4, 300, 12, 6
+    cum, tr, db, L, _, _ = rand_problem(B, T, K, C, 515, [300, 1, 173, 299])
+    cum_d, tr_d, db_d, L_d = cum.to(DEV), tr.to(DEV), db.to(DEV), L.to(DEV)
+    score, cnt, segs = ops.viterbi(cum_d, tr_d, db_d, L_d, K, None, None, True)
+    out = ops.segment_terms(cum_d, tr_d, db_d, cnt, segs, K).cpu().numpy()
+    cnt, segs = cnt.cpu().numpy(), segs.cpu().numpy()
+    cum_n, tr_n, db_n = cum.numpy(), tr.numpy(), db.numpy()
+    for b in range(B):
+        n = int(cnt[b])
+        assert n >= 1
+        s, e, lab, pv = (segs[b, :n, i].astype(np.int64) for i in range(4))
+        content = (cum_n[b, e + 1, lab] - cum_n[b, s, lab]).astype(np.float64)  # fp32 difference
+        want = np.stack([s, e, lab, content, db_n[np.minimum(e - s + 1, K - 1), lab].astype(np.float64),
+                         tr_n[pv, lab].astype(np.float64)], axis=-1)
+        np.testing.assert_array_equal(out[b, :n], want)
+        total = ((out[b, :n, 3] + out[b, :n, 4]) + out[b, :n, 5]).sum()
+        assert abs(total - score[b].item()) <= 1e-5 * max(1.0, abs(total)) + 1e-4
+
+
 # --------------------------------------------------------------------------- launcher contracts
 def test_launcher_checkpoints_and_backward_contract():
     z = load_golden("stream_varlen")
@@ -1194,9 +1245,17 @@ def test_launcher_checkpoints_and_backward_contract():
                  [torch.from_numpy(z[k]) for k in ("grad_cum", "grad_transition", "grad_duration_bias")])
 
 
-def test_kernel_timing_counts_launches():
+@pytest.mark.parametrize("marginals", ["default", "separate"])
+def test_kernel_timing_counts_launches(marginals, monkeypatch):
+    if marginals == "separate":
+        monkeypatch.setenv("TSM_MARGINAL_PATH", "separate")
+    else:
+        monkeypatch.delenv("TSM_MARGINAL_PATH", raising=False)
     z = load_golden("stream_medium")
     cum, tr, db, L, K, sr, ps, pe = fixture_inputs(z, requires_grad=True)
+    B, Tp1, C = cum.shape
+    fused = N.plan_info(B, Tp1 - 1, C, K)["mfused"] == 1
+    assert fused == (marginals == "default"), marginals
     N.timing_enable(True)
     try:
         part = tsa.semi_crf_streaming_forward(cum, tr, db, L, K, semiring=sr)
@@ -1205,7 +1264,8 @@ def test_kernel_timing_counts_launches():
         t = N.timing_read()
     finally:
         N.timing_enable(False)
-    for name in ("scan_fwd_kernel", "scan_bwd_kernel", "marginal_kernel", "finalize_rows_kernel"):
+    rows = ("u_rows_kernel", "fused_rows_kernel") if fused else ("marginal_kernel", "finalize_rows_kernel")
+    for name in ("scan_fwd_kernel", "scan_bwd_kernel") + rows:
         ms, n = t[name]
         assert n == 1 and ms > 0.0, (name, t[name])
     # disabled: nothing more is recorded

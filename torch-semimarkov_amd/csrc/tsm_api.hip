@@ -100,6 +100,13 @@ void plan_fast(Plan& p, const DeviceInfo& di, int fj_only = 0) {
   double best = 1e300;
   const char* jenv = getenv("TSM_FAST_J");  // diagnostics: only this lane-group size
   const int jonly = fj_only != 0 ? fj_only : (jenv != nullptr ? atoi(jenv) : 0);
+  // Fewer warm-up-long pieces of the sequences than CUs: the chunks are few and
+  // each step's latency is the time, not the wave count.  16-lane groups then win
+  // where they fit (shorter per-lane chains than 8 lanes, and the backward with
+  // fused marginals; measured at B=4, T=1000, C=24, K=100: loss + backward 1.13 ->
+  // 0.94 ms, decode 1.38 -> 1.34 ms; 32 lanes slower than either).
+  const int64_t pieces = (int64_t)p.B * std::max<int64_t>(1, (int64_t)p.T / (p.Kmax + 64));
+  const bool latency_bound = pieces < (int64_t)di.n_cu;
   for (int J : {8, 16, 32, 64}) {
     if (jonly != 0 && J != jonly) continue;
     if (p.C > 4 * J) continue;  // the label mix handles at most 4 labels per lane
@@ -154,7 +161,8 @@ void plan_fast(Plan& p, const DeviceInfo& di, int fj_only = 0) {
     // rings for two chunks per CU (used when the compiled kernel also leaves
     // registers for a second workgroup)
     const int RL2 = ring_for(2);
-    const double cost = (double)((NT / 64 + 3) / 4) * (R + 12);  // waves per SIMD x work per wave
+    double cost = (double)((NT / 64 + 3) / 4) * (R + 12);  // waves per SIMD x work per wave
+    if (latency_bound && J == 16 && fsb > 0) cost = 0.0;
     if (cost < best) {
       best = cost;
       p.fast = 1;
@@ -1291,6 +1299,22 @@ int tsm_viterbi(const float* cum, const float* tr, const float* db, const int64_
   if (!cum) return fail(TSM_ERR_INVALID, "cum_scores, transition, duration_bias and lengths are required");
   return viterbi_impl(cum, nullptr, tr, db, len, ps, pe, B, T, C, K, trans_rows, score, with_tb, algorithm,
                       seg_count, segments, workspace, ws_bytes, stream);
+}
+
+int tsm_segment_terms(const float* cum, const float* tr, const float* db, const int32_t* seg_count,
+                      const int32_t* segments, int64_t B, int64_t T, int64_t C, int64_t K, double* out, void* stream) {
+  if (!cum || !tr || !db || !seg_count || !segments || !out)
+    return fail(TSM_ERR_INVALID, "cum_scores, transition, duration_bias, seg_count, segments and out are required");
+  if (B < 0 || T < 0 || C < 1 || K < 1)
+    return fail(TSM_ERR_INVALID, "need B, T >= 0 and C, K >= 1 (got %lld, %lld, %lld, %lld)", (long long)B,
+                (long long)T, (long long)C, (long long)K);
+  if (T >= (int64_t)1 << 30 || B > 65535 || C > 4096 || K > (int64_t)1 << 30)
+    return fail(TSM_ERR_UNSUPPORTED, "segment terms: sizes too large (B=%lld, T=%lld, C=%lld)", (long long)B,
+                (long long)T, (long long)C);
+  const int e = tsm::launch_segment_terms(cum, tr, db, seg_count, segments, (int)B, (int)T, (int)C, (int)K, out,
+                                          (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "tsm_segment_terms");
+  return TSM_OK;
 }
 
 int tsm_prologue_workspace(int64_t B, int64_t T, int64_t C, size_t* bytes) {

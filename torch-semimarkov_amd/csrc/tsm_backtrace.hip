@@ -434,6 +434,41 @@ int launch_backtrace(const BtPlan& bpl, const int32_t* bp, const float* fin, con
   return bpl.TCH > 0 ? launch_bt<true>(p, st) : launch_bt<false>(p, st);
 }
 
+// Score terms of the segment rows of a traceback, one thread per row: the row
+// (start, end, label, previous label) becomes (start, end, label, content,
+// duration bias, transition) in fp64, content the fp32 difference of two
+// cumulative scores (nn.py:532-555).  Indices are clamped into their tensors.
+__global__ void segment_terms_kernel(const float* cum, const float* tr, const float* db, const int32_t* seg_count,
+                                     const int32_t* segs, int T, int C, int K, double* out) {
+  const int b = blockIdx.y;
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= T || i >= seg_count[b]) return;
+  const int4 r = reinterpret_cast<const int4*>(segs)[(size_t)b * T + i];
+  auto clampi = [](int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); };
+  const int s = clampi(r.x, 0, T - 1), e = clampi(r.y, 0, T - 1);
+  const int l = clampi(r.z, 0, C - 1), pv = clampi(r.w, 0, C - 1);
+  const float* cb = cum + (size_t)b * (T + 1) * C;
+  const float content = cb[(size_t)(e + 1) * C + l] - cb[(size_t)s * C + l];
+  const int dur = e - s + 1;
+  const int di = clampi(dur, 0, K - 1);
+  double* o = out + ((size_t)b * T + i) * 6;
+  o[0] = (double)r.x;
+  o[1] = (double)r.y;
+  o[2] = (double)r.z;
+  o[3] = (double)content;
+  o[4] = (double)db[(size_t)di * C + l];
+  o[5] = (double)tr[(size_t)pv * C + l];
+}
+
+int launch_segment_terms(const float* cum, const float* tr, const float* db, const int32_t* seg_count,
+                         const int32_t* segs, int B, int T, int C, int K, double* out, hipStream_t st) {
+  if (B == 0 || T == 0) return hipSuccess;
+  TimedLaunch tl(kKBacktrace, st);
+  hipLaunchKernelGGL(segment_terms_kernel, dim3((T + 255) / 256, B), dim3(256), 0, st, cum, tr, db, seg_count, segs, T,
+                     C, K, out);
+  return hipGetLastError();
+}
+
 int launch_fact_to_exact(const int32_t* bp, const int64_t* lengths, int B, int T, int C, int32_t* out,
                          hipStream_t st) {
   const size_t n = (size_t)B * (T + 1) * C;

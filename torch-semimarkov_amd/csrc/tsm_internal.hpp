@@ -290,6 +290,9 @@ size_t backtrace_ws_bytes(const BtPlan& bp, int B);
 int launch_backtrace(const BtPlan& bpl, const int32_t* bp, const float* fin, const int32_t* final_c,
                      const int64_t* lengths, int B, int T, int C, int Kmax, void* ws, int32_t* seg_count,
                      int32_t* segs, hipStream_t s);
+// score terms of traceback rows: (B, T, 6) fp64 (start, end, label, content, duration bias, transition)
+int launch_segment_terms(const float* cum, const float* tr, const float* db, const int32_t* seg_count,
+                         const int32_t* segs, int B, int T, int C, int K, double* out, hipStream_t s);
 // factorised backpointers (k* ending at t | c'* starting at t) to the exact format
 int launch_fact_to_exact(const int32_t* bp, const int64_t* lengths, int B, int T, int C, int32_t* out,
                          hipStream_t s);

@@ -57,6 +57,7 @@ _SIGNATURES = {
     "tsm_viterbi_workspace": ([_i64, _i64, _i64, _i64, _i64, _i32, ctypes.POINTER(_sz)], _i32),
     "tsm_viterbi": (
         [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _i32, _i32, _p, _p, _p, _sz, _p], _i32),
+    "tsm_segment_terms": ([_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _p], _i32),
     "tsm_prologue_workspace": ([_i64, _i64, _i64, ctypes.POINTER(_sz)], _i32),
     "tsm_cum_scores": ([_p, _i32, _i64, _i64, _i64, _i32, _p, _p, _sz, _p], _i32),
     "tsm_cum_scores_backward": ([_p, _i64, _i64, _i64, _i32, _p, _p, _sz, _p], _i32),

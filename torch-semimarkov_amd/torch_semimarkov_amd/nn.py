@@ -151,21 +151,10 @@ class SemiMarkovCRFHead(nn.Module):
             db = self.duration_bias.detach()
             cum_p, tr_p, db_p, len_p, _, _ = prepare_inputs(cum, tr, db, lengths, self.max_duration)
             score, cnt, segs = ops.viterbi(cum_p, tr_p, db_p, len_p, self.max_duration, None, None, True)
-            B, T = cum.shape[0], cum.shape[1] - 1
-            # every row (start, end, label, previous label) with its fp32 score terms, gathered on
-            # the GPU over all T rows (rows at or beyond a sequence's count are unwritten: zeroed
-            # first) and brought to the host in one transfer, the counts and lengths in another
-            live = torch.arange(T, device=cum.device).view(1, T) < cnt.to(cum.device).view(B, 1)
-            rows = torch.where(live.unsqueeze(-1), segs.long(), torch.zeros_like(segs, dtype=torch.long))
-            bidx = torch.arange(B, device=cum.device).view(B, 1).expand(B, T)
-            start, end, lab, prev = rows[..., 0], rows[..., 1], rows[..., 2], rows[..., 3]
-            # fp32 content exactly as (cum[end+1, l] - cum[start, l])
-            content = cum[bidx, (end + 1).clamp(max=T), lab] - cum[bidx, start, lab]
-            K = self.max_duration
-            dscore = db[torch.clamp(end - start + 1, max=K - 1), lab]
-            tscore = tr[prev, lab]
-            packed = torch.stack([start.double(), end.double(), lab.double(), content.double(), dscore.double(),
-                                  tscore.double()], dim=-1).cpu().numpy()
+            B = cum.shape[0]
+            # every segment row with its fp32 score terms (start, end, label, content, duration
+            # bias, transition; one kernel) in one transfer, the counts and lengths in another
+            packed = ops.segment_terms(cum_p, tr_p, db_p, cnt, segs, self.max_duration).cpu().numpy()
             meta = torch.stack([cnt.to(len_p.device).long(), len_p.long()]).cpu().tolist()
             counts, lens = meta
             all_segments: list[list[Segment]] = [[] for _ in range(B)]

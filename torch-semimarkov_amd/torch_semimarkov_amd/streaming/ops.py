@@ -188,6 +188,24 @@ def _(cum, transition, duration_bias, lengths, K, proj_start, proj_end, tracebac
     return cum.new_empty(B), cum.new_empty(0, dtype=torch.int32), cum.new_empty(0, dtype=torch.int32)
 
 
+def segment_terms(cum: Tensor, transition: Tensor, duration_bias: Tensor, seg_count: Tensor, segments: Tensor,
+                  K: int) -> Tensor:
+    """Score terms of :func:`viterbi`'s traceback rows (``tsm_segment_terms``): (B, T, 6) fp64
+    (start, end, label, content, duration bias, transition) for rows i < seg_count[b]; the
+    rows after those are unset.  Static (C, C) transitions."""
+    lib = N.lib()
+    B, Tp1, C = cum.shape
+    T = Tp1 - 1
+    if transition.dim() != 2:
+        raise ValueError("segment_terms: static (C, C) transitions only")
+    out = torch.empty(B, T, 6, device=cum.device, dtype=torch.float64)
+    with torch.cuda.device(cum.device):
+        rc = lib.tsm_segment_terms(N.ptr(cum), N.ptr(transition), N.ptr(duration_bias), N.ptr(seg_count),
+                                   N.ptr(segments), B, T, C, int(K), N.ptr(out), _stream(cum.device))
+    N.check(rc, "tsm_segment_terms")
+    return out
+
+
 # --------------------------------------------------------------------------- emission prologue
 _DTYPES = {torch.float32: N.TSM_DTYPE_F32, torch.bfloat16: N.TSM_DTYPE_BF16, torch.float16: N.TSM_DTYPE_F16}
 
