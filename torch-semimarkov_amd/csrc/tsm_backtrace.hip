@@ -384,14 +384,19 @@ BtPlan backtrace_plan(int B, int T, int C, int Kmax) {
   // TSM_BACKTRACE_PATH=global: walks read the rows from global memory (tests)
   const char* env = getenv("TSM_BACKTRACE_PATH");
   if (env != nullptr && strcmp(env, "global") == 0) bp.TCH = 0;
-  // about one chunk per CU, chunks of at least max(4 (Kmax+1), 1024) positions
-  const int64_t min_lc = std::max<int64_t>(4 * ((int64_t)Kmax + 1), 1024);
-  int64_t P = (device_cus() + (int64_t)B - 1) / B;
+  // about one chunk per CU, chunks of at least max(4 (Kmax+1), 1024) positions; when that
+  // leaves most CUs idle, the walks' length is the time (a chunk walks D positions into its
+  // range and then its own Lc), so chunks go down to D/2 (at B=4, T=1000, K=100: walks of
+  // about 400 positions instead of one of 1000)
+  bp.D = 2 * (Kmax + 1) + 64;
+  const int64_t cus = device_cus();
+  int64_t min_lc = std::max<int64_t>(4 * ((int64_t)Kmax + 1), 1024);
+  if ((int64_t)B * std::max<int64_t>(1, (int64_t)T / min_lc) < cus) min_lc = std::max<int64_t>(bp.D / 2, 64);
+  int64_t P = (cus + (int64_t)B - 1) / B;
   P = std::min<int64_t>(P, std::max<int64_t>(1, (int64_t)T / min_lc));
   P = std::max<int64_t>(1, std::min<int64_t>(P, kBtMaxChunks));
   bp.P = (int)P;
   bp.Lc = (int)(((int64_t)T + P - 1) / P);
-  bp.D = 2 * (Kmax + 1) + 64;
   return bp;
 }
 
