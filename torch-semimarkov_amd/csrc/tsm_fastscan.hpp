@@ -475,6 +475,12 @@ struct Chunk {
                             : ((j >= 1 || (WIN && p.tst_st != nullptr)) ? t_lo : -1);
 
     int A = A0;  // ring index of the current position
+    // per-step offsets kept as running values (uniform): row t of the (B, T+1, C) tables,
+    // entry t of the (B, T+1) levels, row t of this sequence's tables, and t mod RS
+    size_t row_off = ((size_t)b * (T + 1) + t_first) * C;
+    size_t lvl_off = (size_t)b * (T + 1) + t_first;
+    [[maybe_unused]] size_t tc_off = (size_t)t_first * C;
+    int lr = ((t_first % RS) + RS) % RS;
     for (int t = t_first; t != t_end; t += dir) {
       if constexpr (MARG) {
         if (WIN && from_org && t == t_hi - 1) {
@@ -718,9 +724,9 @@ struct Chunk {
             // leave one of ~1e-7, which the running sum accumulates)
             if constexpr (EMIT) {
               const float St = group_sum<J>(sp);
-              if (cval && lj == 0) s_out_b[(size_t)t * C + c] = St;
+              if (cval && lj == 0) s_out_b[tc_off + c] = St;
             } else {
-              if (cval && lj == 0) s_out_b[(size_t)t * C + c] = exp2_hw((float)(lam + (double)a2) + u_t);
+              if (cval && lj == 0) s_out_b[tc_off + c] = exp2_hw((float)(lam + (double)a2) + u_t);
             }
             if (((t_hi - 1 - t) & 127) == 127) fold_d();
           }
@@ -792,7 +798,7 @@ struct Chunk {
         const ValIdx best = group_argmax_first<J>(ValIdx{mq, mqi});
         mixv = best.v;
         if (FWD && p.bp != nullptr && cval && lj == 0 && (j == 0 || t > t_lo))
-          p.bp[((size_t)b * (T + 1) + t) * C + c] = (kbest << 16) | best.i;
+          p.bp[row_off + c] = (kbest << 16) | best.i;
       }
 
       const bool owned = FWD ? (j == 0 || t > t_lo) : (t < t_hi || j == jl);
@@ -803,7 +809,7 @@ struct Chunk {
             const int ci = lj + J * i;
             if (ci < C) {
               const float ah = rv[i] - mx;
-              if (store && owned) p.val[((size_t)b * (T + 1) + t) * C + ci] = ah;
+              if (store && owned) p.val[row_off + ci] = ah;
               if (t == len) p.fin[(size_t)b * C + ci] = ah;
               if constexpr (WIN) {
                 // checkpoint rows of the bounded-memory backward (levels in the chunk frame)
@@ -814,7 +820,7 @@ struct Chunk {
           }
         }
         if (tid == 0) {
-          if (store && owned) p.lvl[(size_t)b * (T + 1) + t] = lvl_t;
+          if (store && owned) p.lvl[lvl_off] = lvl_t;
           if (t == len) p.fin_lvl[b] = lvl_t;
           if constexpr (WIN) {
             if (p.ck_ah != nullptr && owned && t % p.ck_every == 0 && t / p.ck_every < p.ck_n)
@@ -822,22 +828,27 @@ struct Chunk {
           }
         }
       } else {
-        if (cval && lj == 0 && store && owned) p.val[((size_t)b * (T + 1) + t) * C + c] = mixv;
-        if (tid == 0 && store && owned) p.lvl[(size_t)b * (T + 1) + t] = lvl_t;
+        if (cval && lj == 0 && store && owned) p.val[row_off + c] = mixv;
+        if (tid == 0 && store && owned) p.lvl[lvl_off] = lvl_t;
       }
       if constexpr (MARG && !ESLIDE) {
         // end sum of the owned row t: 2^(alpha[t,c] + beta[t,c] - log2 Z), beta the
         // mixed state of this step in the chunk frame; no segment ends at position 0
         if (t < t_hi && cval && lj == 0)
-          e_own_b[(size_t)t * C + c] = (t == 0) ? 0.0f : exp2_hw((float)((la_t + lvl_t) - zd) + (ah_t + mixv));
+          e_own_b[tc_off + c] = (t == 0) ? 0.0f : exp2_hw((float)((la_t + lvl_t) - zd) + (ah_t + mixv));
       }
       // ---- ring entry for position t ----
       if (cval && lj == 0) {
         rc[A] = (lvl_t + (double)(mixv + pb_t)) - cx_t;
       }
-      if (tid == 0) lring[t % RS] = lvl_t;
+      if (tid == 0) lring[lr] = lvl_t;
       lvl_prev = lvl_t;
       wave_lds_order();
+      row_off += (ptrdiff_t)dir * C;
+      lvl_off += dir;
+      tc_off += (ptrdiff_t)dir * C;
+      lr += dir;
+      lr = (lr == RS) ? 0 : (lr < 0 ? RS - 1 : lr);
 
       // ---- boundary states for verification: positions t -/+ i, i < Kmax ----
       if (t == rec_spec || t == rec_end) {
