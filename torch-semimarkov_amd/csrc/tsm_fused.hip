@@ -434,24 +434,33 @@ __global__ void __launch_bounds__(256) fused_shared_kernel(FusedParams f) {
   const int idx = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (idx >= n_tr + n_db) return;
+  // the lane's partials in a fixed order, eight loaded at once
   double acc = 0.0;
+  auto sum_parts = [&](int nparts, auto term) {
+    int j = lane;
+    for (; j + 7 * 64 < nparts; j += 8 * 64) {
+      double v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = term(j + u * 64);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc += v[u];
+    }
+    for (; j < nparts; j += 64) acc += term(j);
+  };
   if (idx < n_tr) {
-    const int nparts = f.B * f.GNB;
-    for (int j = lane; j < nparts; j += 64)
-      acc += (double)f.grad_output[j / f.GNB] * f.tr_part[(size_t)j * n_tr + idx];
+    sum_parts(f.B * f.GNB, [&](int j) { return (double)f.grad_output[j / f.GNB] * f.tr_part[(size_t)j * n_tr + idx]; });
   } else {
     const int e = idx - n_tr;
     const int k = e / C, c = e % C;
     // durations mapping to duration-bias row k: k itself (K >= 2, k >= 1) or 1 (K == 1)
     const int dur = (K == 1) ? 1 : k;
     if (dur >= 1 && dur <= Kmax) {
-      const int nparts = f.B * f.P;
-      for (int it = lane; it < nparts; it += 64) {
+      sum_parts(f.B * f.P, [&](int it) {
         const int b = it / f.P, j = it % f.P;
         const int len = flen(f.lengths, b, T);
-        if (j > (len > 0 ? (len - 1) / f.Lc : 0)) continue;  // empty chunk
-        acc += (double)f.grad_output[b] * fscale(f, b, j) * f.db_part[((size_t)it * Kmax + dur - 1) * C + c];
-      }
+        if (j > (len > 0 ? (len - 1) / f.Lc : 0)) return 0.0;  // empty chunk
+        return (double)f.grad_output[b] * fscale(f, b, j) * f.db_part[((size_t)it * Kmax + dur - 1) * C + c];
+      });
     }
   }
   for (int m = 32; m >= 1; m >>= 1) acc += __shfl_xor(acc, m, 64);

@@ -370,10 +370,22 @@ __global__ void __launch_bounds__(256) finalize_shared_kernel(FinalParams f) {
       src = f.db_part;
     }
   }
+  auto term = [&](int j) {
+    return (double)f.grad_output[j / f.NB] * (f.bscale != nullptr ? f.bscale[j] : 1.0) * src[(size_t)j * per + off];
+  };
   double acc = 0.0;
-  if (src != nullptr)
-    for (int j = lane; j < nparts; j += 64)
-      acc += (double)f.grad_output[j / f.NB] * (f.bscale != nullptr ? f.bscale[j] : 1.0) * src[(size_t)j * per + off];
+  if (src != nullptr) {
+    // eight partials loaded at once, added in the same order as one at a time
+    int j = lane;
+    for (; j + 7 * 64 < nparts; j += 8 * 64) {
+      double v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = term(j + u * 64);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc += v[u];
+    }
+    for (; j < nparts; j += 64) acc += term(j);
+  }
   for (int m = 32; m >= 1; m >>= 1) acc += __shfl_xor(acc, m, 64);
   if (lane == 0) {
     if (idx < n_tr) f.grad_tr[idx] = (float)acc;
@@ -464,8 +476,36 @@ __global__ void __launch_bounds__(256) unit_marginal_kernel(MargParams q) {
   if (act && t0 == len && lane == 0) e_own_b[(size_t)len * C + c] = 0.0f;
   if (act && t0 < len) {
     if (lane == 0) e_own_b[(size_t)t0 * C + c] = 0.0f;  // no start of this block ends at t0
-    for (int t = t0 + lane; t < t1; t += NL) {
+    // a position's operands, loaded one iteration ahead (each iteration would otherwise
+    // wait for its own loads)
+    struct Ops {
+      float ah[kUnitMaxC];
+      float xb, ps, cu0, cu1;
+      double al, bl;
+    };
+    auto load = [&](int t, Ops& o) {
       const float* ah = q.aval + (row0 + t) * C;
+#pragma unroll
+      for (int i = 0; i < kUnitMaxC; ++i) o.ah[i] = (i < C) ? ah[i] : 0.0f;
+      o.xb = q.bval[(row0 + t + 1) * C + c];
+      o.ps = (q.ps != nullptr) ? q.ps[((size_t)b * T + t) * C + c] : 0.0f;
+      if (q.pe != nullptr) o.xb += q.pe[((size_t)b * T + t) * C + c] * kLog2e;
+      if (emit) {
+        o.cu0 = 0.0f;
+        o.cu1 = q.emit[((size_t)b * T + t) * C + c];
+      } else {
+        o.cu0 = q.cum[(row0 + t) * C + c];
+        o.cu1 = q.cum[(row0 + t + 1) * C + c];
+      }
+      o.al = q.alvl[row0 + t];
+      o.bl = q.blvl[row0 + t + 1];
+    };
+    Ops nx;
+    if (t0 + lane < t1) load(t0 + lane, nx);
+    for (int t = t0 + lane; t < t1; t += NL) {
+      const Ops o = nx;
+      if (t + NL < t1) load(t + NL, nx);
+      const float* ah = o.ah;
       float mx = kMinusInf;
 #pragma unroll
       for (int i = 0; i < kUnitMaxC; ++i)
@@ -475,12 +515,10 @@ __global__ void __launch_bounds__(256) unit_marginal_kernel(MargParams q) {
       for (int i = 0; i < kUnitMaxC; ++i)
         if (i < C) sw += exp2_hw((ah[i] + trc[i]) - mx);
       const float u2 = mx + log2_hw(sw);
-      float ua = u2, xb = q.bval[(row0 + t + 1) * C + c];
-      if (q.ps != nullptr) ua += q.ps[((size_t)b * T + t) * C + c] * kLog2e;
-      if (q.pe != nullptr) xb += q.pe[((size_t)b * T + t) * C + c] * kLog2e;
-      const double dc = emit ? (double)q.emit[((size_t)b * T + t) * C + c] * kLog2eM
-                             : ((double)q.cum[(row0 + t + 1) * C + c] - (double)q.cum[(row0 + t) * C + c]) * kLog2eM;
-      const double ax = ((q.alvl[row0 + t] + (double)ua) + (q.blvl[row0 + t + 1] + (double)xb)) - z2;
+      float ua = u2, xb = o.xb;
+      if (q.ps != nullptr) ua += o.ps * kLog2e;
+      const double dc = emit ? (double)o.cu1 * kLog2eM : ((double)o.cu1 - (double)o.cu0) * kLog2eM;
+      const double ax = ((o.al + (double)ua) + (o.bl + (double)xb)) - z2;
       const float P = exp2_hw((float)(ax + dc) + dbk);
       s_out_b[(size_t)t * C + c] = P;
       if (t + 1 < own_hi) e_own_b[(size_t)(t + 1) * C + c] = P;
