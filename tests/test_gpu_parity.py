@@ -451,12 +451,15 @@ def test_random_problems_vs_fp64_oracle(B, T, K, C, lengths, proj, sr, scan_path
     (3, 900, 40, 24, [900, 1, 512], "log"),
     (1, 1300, 100, 32, None, "log"),
     (2, 700, 30, 20, [700, 333], "max"),
+    (2, 700, 1, 8, [700, 450], "log"),
+    (2, 500, 1, 6, None, "max"),
 ])
 def test_eight_lane_groups_vs_fp64_oracle(B, T, K, C, lengths, sr, monkeypatch):
     """Plans with few chunks take 16 lanes per label; TSM_FAST_J=8 keeps the 8-lane
     instances (several durations per lane, a four-source label mix at C > 16, the
-    separate marginal kernel) checked against the fp64 oracle, with the Viterbi
-    score of the 8-lane factorised scan against the exact kernel."""
+    one-source mix of single-duration plans with C <= 8, the separate marginal
+    kernel) checked against the fp64 oracle, with the Viterbi score of the 8-lane
+    factorised scan against the exact kernel."""
     monkeypatch.delenv("TSM_SCAN_PATH", raising=False)
     monkeypatch.setenv("TSM_FAST_J", "8")
     info = N.plan_info(B, T, C, K)

@@ -934,7 +934,8 @@ struct Chunk {
   }
 };
 
-// source labels per lane of the label mix: 2 when C <= 2J, else 4 (the plan keeps C <= 4J)
+// source labels per lane of the label mix: 2 when C <= 2J, else 4 (the plan keeps C <= 4J);
+// single-duration 8-lane plans with C <= 8 take 1 (launch_chunk_any)
 template <int J>
 inline bool narrow_mix(const ScanParams& p) { return p.C <= 2 * J; }
 
@@ -953,6 +954,11 @@ int launch_chunk_any(const Plan& pl, const ScanParams& p, hipStream_t st) {
     return (int)hipErrorInvalidValue;
   }
   const bool em = p.emit != nullptr;
+  if constexpr (J == 8 && R == 1 && !MARG) {
+    // single-duration plans with no more labels than lanes per group (the HMM with
+    // C <= 8): one source label per lane in the label mix
+    if (!em && p.C <= J) return launch_chunk_dir<Chunk<J, R, FWD, LOGSR, MARG, 1, kInCum>>(pl, p, pl.fast_lds, pl.FNT, st);
+  }
   if (narrow_mix<J>(p))
     return em ? launch_chunk_dir<Chunk<J, R, FWD, LOGSR, MARG, 2, kInEmit>>(pl, p, pl.fast_lds, pl.FNT, st)
               : launch_chunk_dir<Chunk<J, R, FWD, LOGSR, MARG, 2, kInCum>>(pl, p, pl.fast_lds, pl.FNT, st);

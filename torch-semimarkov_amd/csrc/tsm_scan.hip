@@ -678,7 +678,8 @@ int fast_scan_regs(const Plan& pl, int kind) {
   // one query per instance (kind, lanes per label, durations per lane, mix width)
   static std::mutex mu;
   static std::map<std::tuple<int, int, int, int>, int> cache;
-  const auto key = std::make_tuple(kind, pl.FJ, pl.FR, pl.C <= 2 * pl.FJ ? 2 : 4);
+  const int cj = (pl.FJ == 8 && pl.FR == 1 && pl.C <= 8) ? 1 : (pl.C <= 2 * pl.FJ ? 2 : 4);
+  const auto key = std::make_tuple(kind, pl.FJ, pl.FR, cj);
   {
     std::lock_guard<std::mutex> lk(mu);
     const auto it = cache.find(key);
