@@ -109,6 +109,11 @@ def test_c_abi_rejects_bad_calls_without_touching_the_device():
     assert rc == 1 and b"alpha_hat and alpha_level" in lib.tsm_last_error()
     rc = lib.tsm_plan_info(1, 10, 600, 3, 0, 0, 0, None, 0)
     assert rc == 2
+    # segment terms: required pointers and sizes are checked before any launch
+    rc = lib.tsm_segment_terms(fake, fake, fake, None, fake, 1, 10, 4, 3, fake, None)
+    assert rc == 1 and b"seg_count" in lib.tsm_last_error()
+    rc = lib.tsm_segment_terms(fake, fake, fake, fake, fake, 1, 10, 0, 3, fake, None)
+    assert rc == 1 and b"C, K >= 1" in lib.tsm_last_error()
 
 
 def test_python_api_fails_loudly_off_gpu():
