@@ -475,6 +475,9 @@ struct Chunk {
                             : ((j >= 1 || (WIN && p.tst_st != nullptr)) ? t_lo : -1);
 
     int A = A0;  // ring index of the current position
+    // single duration: the ring entry of the previous position (the only one a step
+    // reads) also kept in a register; every lane of the label group computes it
+    [[maybe_unused]] double xr = (!MARG && R == 1 && k1) ? rc[A0] : 0.0;
     // per-step offsets kept as running values (uniform): row t of the (B, T+1, C) tables,
     // entry t of the (B, T+1) levels, row t of this sequence's tables, and t mod RS
     size_t row_off = ((size_t)b * (T + 1) + t_first) * C;
@@ -597,14 +600,17 @@ struct Chunk {
       // ---- pull over the lane's durations ----
       const double* rb = rc + A + 1 + lj;
       double e[R];
+      if (!(!MARG && R == 1 && k1)) {
 #pragma unroll
-      for (int r = 0; r < R; ++r) e[r] = rb[J * r];
+        for (int r = 0; r < R; ++r) e[r] = rb[J * r];
+      }
       float a2;
       int kbest = 0;
       if (!MARG && R == 1 && k1) {
-        // a single duration (Kmax = 1, the HMM): the term of lane 0, which every lane
-        // reads itself; the group reduction would return exactly this value
-        a2 = (float)(((rc[A + 1] + (double)db1) + cx_t) - lvl_prev) + pa_t;
+        // a single duration (Kmax = 1, the HMM): the term of lane 0 (ring entry of the
+        // previous position, xr), which every lane computes itself; the group
+        // reduction would return exactly this value
+        a2 = (float)(((xr + (double)db1) + cx_t) - lvl_prev) + pa_t;
         kbest = 1;
       } else if constexpr (LOGSR) {
         double y0 = e[0] + (double)dbr[0];
@@ -841,6 +847,7 @@ struct Chunk {
       if (cval && lj == 0) {
         rc[A] = (lvl_t + (double)(mixv + pb_t)) - cx_t;
       }
+      if (!MARG && R == 1 && k1) xr = (lvl_t + (double)(mixv + pb_t)) - cx_t;
       if (tid == 0) lring[lr] = lvl_t;
       lvl_prev = lvl_t;
       wave_lds_order();
