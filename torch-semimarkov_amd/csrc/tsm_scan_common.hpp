@@ -65,16 +65,34 @@ __device__ inline void block_minmax(double vmax, double vmin, double* red, doubl
 // over this thread's share of the Kmax*C boundary entries.  Entries unreachable
 // in both states (< -1e8 in log2 units) are skipped: they add nothing to any sum.
 __device__ inline void boundary_spread_part(const ScanParams& p, size_t e, size_t sp, double& hi, double& lo) {
-  const int Kmax = p.Kmax, C = p.C;
+  const int Kmax = p.Kmax, C = p.C, n = Kmax * C, nt = blockDim.x;
   hi = -1e300;
   lo = 1e300;
-  for (int idx = threadIdx.x; idx < Kmax * C; idx += blockDim.x) {
-    const int i = idx / C;
-    const float a = p.st_end[e * Kmax * C + idx], bb = p.st_spec[sp * Kmax * C + idx];
-    if (a < -1e8f && bb < -1e8f) continue;
-    const double d = (p.lv_end[e * Kmax + i] - p.lv_spec[sp * Kmax + i]) + ((double)a - (double)bb);
+  auto take = [&](float a, float bb, double le, double ls) {
+    if (a < -1e8f && bb < -1e8f) return;
+    const double d = (le - ls) + ((double)a - (double)bb);
     hi = fmax(hi, d);
     lo = fmin(lo, d);
+  };
+  // four entries per thread loaded before any is used (the loads of one pass overlap)
+  int idx = threadIdx.x;
+  for (; idx + 3 * nt < n; idx += 4 * nt) {
+    float a[4], bb[4];
+    double le[4], ls[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int id = idx + u * nt, i = id / C;
+      a[u] = p.st_end[e * n + id];
+      bb[u] = p.st_spec[sp * n + id];
+      le[u] = p.lv_end[e * Kmax + i];
+      ls[u] = p.lv_spec[sp * Kmax + i];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) take(a[u], bb[u], le[u], ls[u]);
+  }
+  for (; idx < n; idx += nt) {
+    const int i = idx / C;
+    take(p.st_end[e * n + idx], p.st_spec[sp * n + idx], p.lv_end[e * Kmax + i], p.lv_spec[sp * Kmax + i]);
   }
 }
 
