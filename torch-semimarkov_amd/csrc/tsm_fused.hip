@@ -291,21 +291,20 @@ __global__ void fused_rows_kernel(FusedParams f) {
   const int len = flen(f.lengths, b, T);
   const float g = f.grad_output[b];
   const size_t n = (size_t)(T + 1) * C;
-  for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < n; idx += (size_t)gridDim.x * blockDim.x) {
-    const int t = (int)(idx / C), c = (int)(idx % C);
-    const size_t o = ((size_t)b * (T + 1) + t) * C + c;
+  // entry idx = (t, c) of row t, with its own-row end sum eo, start sum so and chunk factor fj
+  // (loaded by the caller)
+  auto row = [&](int t, int c, size_t o, float eo, float so, double fj) {
     float E = 0.0f, S = 0.0f;
     if (t <= len) {
-      const int j = fchunk(t, len, Lc);
-      const double fj = fscale(f, b, j);
       if (t > 0) {
-        double e = fj * (double)f.e_own[o];
+        double e = fj * (double)eo;
+        const int j = fchunk(t, len, Lc);
         const int d = t - j * Lc;  // rows j*Lc .. j*Lc+Kmax-1 also take chunk j-1's halo
         if (f.halo != nullptr && j >= 1 && d < Kmax)
           e += fscale(f, b, j - 1) * (double)f.halo[(((size_t)b * f.P + j - 1) * Kmax + d) * C + c];
         E = (float)e;
       }
-      if (t < len) S = (float)(fj * (double)f.s_out[o]);
+      if (t < len) S = (float)(fj * (double)so);
     }
     if (f.accum) {
       // window of the bounded-memory backward: rows of the full tensors (their
@@ -314,12 +313,39 @@ __global__ void fused_rows_kernel(FusedParams f) {
       f.grad_cum[xo] += g * (E - S);
       if (f.grad_ps != nullptr && t < T) f.grad_ps[po] += g * S;
       if (f.grad_pe != nullptr && t >= 1) f.grad_pe[po - C] += g * E;
-      continue;
+      return;
     }
     if (!f.shift) f.grad_cum[o] = g * (E - S);
     else if (t >= 1) f.grad_cum[((size_t)b * T + t - 1) * C + c] = g * (E - S);
     if (f.grad_ps != nullptr && t < T) f.grad_ps[((size_t)b * T + t) * C + c] = g * S;
     if (f.grad_pe != nullptr && t >= 1) f.grad_pe[((size_t)b * T + t - 1) * C + c] = g * E;
+  };
+  // four entries per thread loaded before any is used (every load is in bounds: t <= T,
+  // and the chunk index is clamped to the sequence's chunks)
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  for (; idx + 3 * stride < n; idx += 4 * stride) {
+    int t[4], c[4];
+    size_t o[4];
+    float eo[4], so[4];
+    double fj[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const size_t id = idx + u * stride;
+      t[u] = (int)(id / C);
+      c[u] = (int)(id % C);
+      o[u] = ((size_t)b * (T + 1) + t[u]) * C + c[u];
+      eo[u] = f.e_own[o[u]];
+      so[u] = f.s_out[o[u]];
+      fj[u] = fscale(f, b, fchunk(t[u], len, Lc));
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) row(t[u], c[u], o[u], eo[u], so[u], fj[u]);
+  }
+  for (; idx < n; idx += stride) {
+    const int t = (int)(idx / C), c = (int)(idx % C);
+    const size_t o = ((size_t)b * (T + 1) + t) * C + c;
+    row(t, c, o, f.e_own[o], f.s_out[o], fscale(f, b, fchunk(t, len, Lc)));
   }
 }
 
