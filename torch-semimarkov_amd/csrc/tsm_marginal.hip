@@ -313,9 +313,9 @@ __global__ void finalize_rows_kernel(FinalParams f) {
   const int len = mlen(f.lengths, b, T);
   const float g = f.grad_output[b];
   const size_t n = (size_t)(T + 1) * C;
-  for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < n; idx += (size_t)gridDim.x * blockDim.x) {
-    const int t = (int)(idx / C), c = (int)(idx % C);
-    const size_t o = ((size_t)b * (T + 1) + t) * C + c;
+  // entry (t, c) with its own-row end sum eo and start sum so (loaded by the caller;
+  // every row t <= T of the tables exists)
+  auto row = [&](int t, int c, size_t o, float eo, float so) {
     float E = 0.0f, S = 0.0f;
     if (t <= len) {
       const int blk = t / f.TB, t0 = blk * f.TB;
@@ -323,18 +323,42 @@ __global__ void finalize_rows_kernel(FinalParams f) {
       const float ks = (f.bscale != nullptr && blk < f.NB) ? (float)f.bscale[(size_t)b * f.NB + blk] : 1.0f;
       if (t > 0) {
         // own part: written by block blk (absent when t == NB*TB, i.e. t == T)
-        if (blk < f.NB) E = ks * f.e_own[o];
+        if (blk < f.NB) E = ks * eo;
         if (blk >= 1 && t - t0 < f.Kmax) {
           const float kp = f.bscale != nullptr ? (float)f.bscale[(size_t)b * f.NB + blk - 1] : 1.0f;
           E += kp * f.halo[(((size_t)b * f.NB + blk - 1) * f.Kmax + (t - t0)) * C + c];
         }
       }
-      if (t < len) S = ks * f.s_out[o];
+      if (t < len) S = ks * so;
     }
     if (!f.shift) f.grad_cum[o] = g * (E - S);
     else if (t >= 1) f.grad_cum[((size_t)b * T + t - 1) * C + c] = g * (E - S);
     if (f.grad_ps != nullptr && t < T) f.grad_ps[((size_t)b * T + t) * C + c] = g * S;
     if (f.grad_pe != nullptr && t >= 1) f.grad_pe[((size_t)b * T + t - 1) * C + c] = g * E;
+  };
+  // four entries per thread loaded before any is used
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  for (; idx + 3 * stride < n; idx += 4 * stride) {
+    int t[4], c[4];
+    size_t o[4];
+    float eo[4], so[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const size_t id = idx + u * stride;
+      t[u] = (int)(id / C);
+      c[u] = (int)(id % C);
+      o[u] = ((size_t)b * (T + 1) + t[u]) * C + c[u];
+      eo[u] = f.e_own[o[u]];
+      so[u] = f.s_out[o[u]];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) row(t[u], c[u], o[u], eo[u], so[u]);
+  }
+  for (; idx < n; idx += stride) {
+    const int t = (int)(idx / C), c = (int)(idx % C);
+    const size_t o = ((size_t)b * (T + 1) + t) * C + c;
+    row(t, c, o, f.e_own[o], f.s_out[o]);
   }
 }
 
@@ -585,7 +609,8 @@ int launch_block_coverage(const Plan& pl, const MargParams& q, double* bscale, h
 }
 
 int launch_finalize(const Plan& pl, const FinalParams& f, hipStream_t s) {
-  int gx = (int)(((size_t)(pl.T + 1) * pl.C + 255) / 256);
+  // at least four entries per thread (the kernel loads four at a time)
+  int gx = (int)(((size_t)(pl.T + 1) * pl.C + 1023) / 1024);
   if (gx > 4096) gx = 4096;
   {
     TimedLaunch tl(kKFinalizeRows, s);
