@@ -422,7 +422,7 @@ struct Chunk {
     auto clampT1 = [&](int t) { return t < 0 ? 0 : (t > T - 1 ? T - 1 : t); };
     // projection operands: forward adds proj_end[t-1] to the pull and proj_start[t]
     // to the ring entry; backward adds proj_start[t] to the pull and proj_end[t-1]
-    // to the ring entry.  Absent projections read cum and are scaled by 0.
+    // to the ring entry.  Absent projections are not read (operand 0, scale 0).
     // per step: cum[t] (cum input) or the score row stepped over, t-1 forward and t
     // backward (emission input), whose running sum is the chunk-frame cum
     const float* xs_b = emit ? em_b : cum_b;
@@ -431,6 +431,7 @@ struct Chunk {
     const float* pb_src = FWD ? (has_ps ? ps_b : xs_b) : (has_pe ? pe_b : xs_b);
     const float pa_scale = (FWD ? has_pe : has_ps) ? kLog2e : 0.0f;
     const float pb_scale = (FWD ? has_ps : has_pe) ? kLog2e : 0.0f;
+    const bool has_pa = FWD ? has_pe : has_ps, has_pb = FWD ? has_ps : has_pe;
     auto pa_row = [&](int t) { return FWD ? clampT1(t - 1) : clampT1(t); };
     auto pb_row = [&](int t) { return FWD ? clampT1(t) : clampT1(t - 1); };
     // emission input: the running sgn * cum * log2(e) of the previous position
@@ -455,8 +456,8 @@ struct Chunk {
     [[maybe_unused]] auto stage_load = [&](int n) {
       const int tq = t_first + dir * (n * SB + lj);
       qx = xs_b[(size_t)xs_row(tq) * C + c];
-      qa = pa_src[(size_t)pa_row(tq) * C + c];
-      qb = pb_src[(size_t)pb_row(tq) * C + c];
+      qa = has_pa ? pa_src[(size_t)pa_row(tq) * C + c] : 0.0f;
+      qb = has_pb ? pb_src[(size_t)pb_row(tq) * C + c] : 0.0f;
       qu = u_b[(size_t)clampT(tq) * C + c];
       ql = al_b[clampT(tq)];
       if constexpr (!ESLIDE) qh = ah_b[(size_t)clampT(tq) * C + c];
@@ -465,8 +466,8 @@ struct Chunk {
       stage_load(0);
     } else {
       cum_n = xs_b[(size_t)xs_row(t_first) * C + c];
-      pa_n = pa_src[(size_t)pa_row(t_first) * C + c];
-      pb_n = pb_src[(size_t)pb_row(t_first) * C + c];
+      pa_n = has_pa ? pa_src[(size_t)pa_row(t_first) * C + c] : 0.0f;
+      pb_n = has_pb ? pb_src[(size_t)pb_row(t_first) * C + c] : 0.0f;
     }
 
     const int rec_spec = (mode == 1) ? (FWD ? t_lo : t_hi) : -1;
@@ -588,8 +589,8 @@ struct Chunk {
         pb_v = pb_n;
         const int tn = t + dir;
         cum_n = xs_b[(size_t)xs_row(tn) * C + c];
-        pa_n = pa_src[(size_t)pa_row(tn) * C + c];
-        pb_n = pb_src[(size_t)pb_row(tn) * C + c];
+        if (has_pa) pa_n = pa_src[(size_t)pa_row(tn) * C + c];
+        if (has_pb) pb_n = pb_src[(size_t)pb_row(tn) * C + c];
       }
       double cx_t;
       if constexpr (EMIT) cx_t = cx_run = cx_run + (double)x_t * kLog2eD;
