@@ -288,9 +288,11 @@ struct CoopChunk {
     const float pb_scale = (FWD ? has_ps : has_pe) ? kLog2e : 0.0f;
     auto pa_row = [&](int t) { return FWD ? clampT1(t - 1) : clampT1(t); };
     auto pb_row = [&](int t) { return FWD ? clampT1(t) : clampT1(t - 1); };
+    // absent projections are not read (operand 0, scale 0)
+    const bool has_pa = FWD ? has_pe : has_ps, has_pb = FWD ? has_ps : has_pe;
     float cum_n = cum_b[(size_t)clampT(t_first) * C + c];
-    float pa_n = pa_src[(size_t)pa_row(t_first) * C + c];
-    float pb_n = pb_src[(size_t)pb_row(t_first) * C + c];
+    float pa_n = has_pa ? pa_src[(size_t)pa_row(t_first) * C + c] : 0.0f;
+    float pb_n = has_pb ? pb_src[(size_t)pb_row(t_first) * C + c] : 0.0f;
 
     const int rec_spec = (mode == 1) ? (FWD ? t_lo : t_hi) : -1;
     const int rec_end = FWD ? ((t_hi < len) ? t_hi : -1) : ((j >= 1) ? t_lo : -1);
@@ -350,8 +352,8 @@ struct CoopChunk {
       {
         const int tn = t + dir;
         cum_n = cum_b[(size_t)clampT(tn) * C + c];
-        pa_n = pa_src[(size_t)pa_row(tn) * C + c];
-        pb_n = pb_src[(size_t)pb_row(tn) * C + c];
+        if (has_pa) pa_n = pa_src[(size_t)pa_row(tn) * C + c];
+        if (has_pb) pb_n = pb_src[(size_t)pb_row(tn) * C + c];
       }
 
       // ---- pull over the lane's durations (own labels): the register-0 terms
