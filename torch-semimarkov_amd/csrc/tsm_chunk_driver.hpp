@@ -15,10 +15,10 @@
 // states for verification and writes the chunk's outputs in its own frame.
 //
 // One direction is: the parallel pass over all chunks, the verification of
-// every speculative boundary, a parallel retry with a 4x warm-up of the
-// chunks that failed, verification again, a sequential per-sequence repair
-// (exact recompute of what still fails, accumulation of frame offsets), and
-// the application of the offsets to the stored levels.
+// every speculative boundary together with a parallel retry (4x warm-up) of the
+// chunks that fail it, verification again when something reran, a sequential
+// per-sequence repair (exact recompute of what still fails, accumulation of
+// frame offsets), and the application of the offsets to the stored levels.
 #pragma once
 
 #include "tsm_scan_common.hpp"
@@ -38,7 +38,25 @@ __device__ __forceinline__ void chunk_scan_body(const ScanParams& p) {
     if (threadIdx.x == 0) p.status[item] = -1;  // empty chunk
     return;
   }
-  if (p.retry && retry_skip(p, item)) return;
+  if (p.retry) {
+    // verification of a speculative chunk against its neighbour's end state (the
+    // (max, min) spread, kept for the repair); rerun with the longer warm-up when it
+    // fails.  A neighbour that reruns here rewrites that end state meanwhile: a spread
+    // measured from a half-rewritten state is measured again by the second
+    // verification, which runs because the neighbour reran, before the repair uses it.
+    if (p.status[item] != 1) return;
+    const size_t e = FWD ? (size_t)(item - 1) : (size_t)(item + 1);
+    double hi, lo, dmax, dmin;
+    boundary_spread_part(p, e, (size_t)item, hi, lo);
+    block_minmax(hi, lo, CH::red(smem, p), dmax, dmin);
+    if (threadIdx.x == 0) {
+      p.vstat[2 * item] = dmax;
+      p.vstat[2 * item + 1] = dmin;
+    }
+    if (dmax - dmin <= (double)p.tol) return;
+  } else if (blockIdx.x == 0 && threadIdx.x == 0) {
+    *p.vflag = 0;  // the retry pass sets it when it reruns a chunk
+  }
   const int mode = (FWD ? fwd_spec(p, j) : bwd_spec(p, j, len)) ? 1 : 0;
   if (threadIdx.x == 0) {
     p.status[item] = mode;
@@ -192,10 +210,9 @@ int launch_chunk_dir(const Plan& pl, const ScanParams& p, size_t lds, int nthrea
     TimedLaunch tl(fwd ? kKScanFwd : kKScanBwd, st);
     hipLaunchKernelGGL(k, dim3(pl.B * pl.P), dim3(nthreads), lds, st, p);
   }
-  e = (hipError_t)launch_verify(pl, p, fwd, st);
-  if (e != hipSuccess) return e;
   if (pl.P > 1) {
-    // failed speculative chunks again, in parallel, with a longer warm-up
+    // verification of every speculative chunk, and those that fail again, in
+    // parallel, with a longer warm-up
     {
       TimedLaunch tl(kKRetry, st);
       hipLaunchKernelGGL(kr, dim3(pl.B * pl.P), dim3(nthreads), lds, st, retry_params(p));

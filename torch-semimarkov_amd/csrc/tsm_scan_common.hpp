@@ -30,14 +30,6 @@ __device__ inline bool bwd_spec(const ScanParams& p, int j, int len) {
   return j < jl && (j + 1) * p.Lc + p.W + p.Kmax - 1 <= len;
 }
 
-// Retry pass: whether chunk `item` ran speculatively and its boundary spread
-// (measured by the verification kernel) exceeds the tolerance.  Every thread
-// reads the chunk's status before the block may rewrite it.
-__device__ inline bool retry_skip(const ScanParams& p, int item) {
-  const bool need = p.status[item] == 1 && (p.vstat[2 * item] - p.vstat[2 * item + 1] > (double)p.tol);
-  __syncthreads();
-  return !need;
-}
 
 // Block-wide max / min of a double (all threads receive the result).
 __device__ inline void block_minmax(double vmax, double vmin, double* red, double& omax, double& omin) {
