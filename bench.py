@@ -495,7 +495,7 @@ def main():
     dom_total, dom_launches = ktimes[dom]
     dom_avg_ms = dom_total / dom_launches
     nv, nt = kops[dom]
-    # roofline on the executed (factorised) work, and the survey's nominal pricing beside it
+    # roofline on the executed (factorised) work, and the nominal per-cell pricing beside it
     exec_key = "scan_bwd_kernel_fused" if (dom == "scan_bwd_kernel" and fused) else dom
     exec_ops = executed_valu_ops(exec_key, B, T, C, K)
     achieved = exec_ops / (dom_avg_ms / 1e3) / 1e12
@@ -537,7 +537,7 @@ def main():
                 "valu_equiv_ops_per_launch": exec_ops,
                 "formula": "B*T*(max(K-1,1)*C*(dv+dt*V/T) + C^2*(mv+mt*V/T)) / avg_launch_s / V_peak",
             },
-            # the survey's nominal pricing: every B*T*K*C^2 cell of the direct recursion at the
+            # nominal pricing: every B*T*K*C^2 cell of the direct recursion at the
             # pass's (VALU, transcendental) ops; above 1 because the factorisation skips most cells
             "nominal_frac": nominal_achieved / peak,
             "nominal_ops_per_cell": {"valu": nv, "transcendental": nt},
